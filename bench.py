@@ -1,0 +1,236 @@
+"""Benchmark of TinyBrainHIP's quantized matmul on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+
+Default workload (BASELINE.json config 1 at M=1, the config the headline
+metric "dequant-GEMV GB/s and % of HBM peak" is quoted on):
+  INT4 weight-only GEMV, symmetric signed 4-bit, one fp32 scale per 32
+  consecutive K elements (converter layout), x fp32 [1 x K], for the four
+  shapes [N x K] = 2048x2048, 5632x2048, 2048x5632, 32000x2048.
+  One step = one GEMV of each shape.  Weights rotate through a pool of
+  distinct copies totalling >= 2 GiB so every launch streams from HBM rather
+  than the 256 MiB Infinity Cache.  Inputs are resident in HBM before timing.
+
+value = algorithmic bytes of all GEMVs in the timed steps / wall time (GB/s),
+algorithmic bytes per GEMV = W + S + Z + 4*M*K + 4*M*N.
+The roofline object reports the dominant kernel (32000x2048) timed with HIP
+events on its own stream over back-to-back launches.  cpu_baseline times the
+restated reference CPU path (dequantize() then sgemm on all host cores) on a
+bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
+
+WORKLOADS = {
+    # name: (precision, group, shapes [(N, K)], M)
+    "int4_g32_gemv_m1": ("int4", 32, [(2048, 2048), (5632, 2048), (2048, 5632), (32000, 2048)], 1),
+    "int4_g32_gemv_m4": ("int4", 32, [(2048, 2048), (5632, 2048), (2048, 5632), (32000, 2048)], 4),
+    "int4_g32_gemv_m8": ("int4", 32, [(2048, 2048), (5632, 2048), (2048, 5632), (32000, 2048)], 8),
+    "int8_pc_gemv_m1": ("int8", 0, [(5632, 2048)], 1),
+}
+
+
+def alg_bytes(prec: str, gs: int, N: int, K: int, M: int) -> int:
+    if prec == "int4":
+        w = (K * N + 1) // 2
+        s = 4 * ((K * N + gs - 1) // gs)
+    else:
+        w = K * N
+        s = 4 * N
+    return w + s + 4 * M * K + 4 * M * N
+
+
+def make_weight(prec: str, gs: int, N: int, K: int, seed: int):
+    """Synthetic W ~ N(0, 0.02) as PyTorch [N, K], quantized with the
+    product's restatement of the reference quantizers."""
+    import tinybrain_amd as T
+
+    rng = np.random.default_rng(seed)
+    w_nk = rng.normal(0.0, 0.02, size=(N, K)).astype(np.float32)
+    if prec == "int4":
+        return T.quantize_int4_flat(w_nk, gs, shape=(K, N), layout=T.Layout.NK_FLAT)
+    return T.quantize(np.ascontiguousarray(w_nk.T), T.QuantizationMode.perChannel)
+
+
+def cpu_baseline(qts, shapes, M: int, budget_s: float = 15.0):
+    """Reference CPU path (QuantizedTensor.swift:640-642) restated in the
+    oracle: single-threaded dequantize() into a fresh fp32 [K, N] buffer, then
+    sgemm on all host cores.  Times whole steps until ~budget_s."""
+    import oracle as O
+
+    threads = min(os.cpu_count() or 1, 16)
+    oq = []
+    for qt in qts:
+        oq.append(O.QTensor(qt.shape, qt.data, qt.scales, qt.zeroPoints, int(qt.mode),
+                            int(qt.precision), qt.groupSize))
+    xs = {K: np.random.default_rng(1).normal(size=(M, K)).astype(np.float32) for _, K in shapes}
+    steps = 0
+    t_deq = t_gemm = 0.0
+    byts = 0
+    t0 = time.perf_counter()
+    while True:
+        for (N, K), q, qt in zip(shapes, oq, qts):
+            _, td, tg = O.matmul_quantized_cpu(xs[K], q, threads=threads)
+            t_deq += td
+            t_gemm += tg
+            byts += alg_bytes("int4" if qt.precision == 2 else "int8", qt.groupSize, N, K, M)
+        steps += 1
+        if time.perf_counter() - t0 > budget_s or steps >= 50:
+            break
+    wall = time.perf_counter() - t0
+    return {
+        "value": round(byts / wall / 1e9, 4),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{steps} step(s) of the same workload (one GEMV per shape, M={M}); "
+                  f"dequantize {t_deq:.2f}s single-threaded + sgemm {t_gemm:.2f}s on {threads} threads",
+        "ms_per_step": round(1e3 * wall / steps, 3),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="int4_g32_gemv_m1", choices=sorted(WORKLOADS))
+    ap.add_argument("--pool-gib", type=float, default=2.2)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; the GEMV would shard along N "
+                                   "(see DESIGN.md) but no multi-GPU path is built", "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    import torch
+    import tinybrain_amd as T
+
+    prec, gs, shapes, M = WORKLOADS[args.workload]
+    torch.cuda.set_device(0)
+    backend = T.HIPBackend(0)
+
+    # ---- weights: one quantized base per shape, copied into a >= 2 GiB pool
+    t_setup = time.perf_counter()
+    bases = [make_weight(prec, gs, N, K, seed=0x7B1A0010 + i) for i, (N, K) in enumerate(shapes)]
+    set_bytes = sum(alg_bytes(prec, gs, N, K, 0) for N, K in shapes)
+    n_sets = max(2, int(np.ceil(args.pool_gib * 2**30 / set_bytes)))
+    pool = [[T.DeviceWeight(backend, b) for b in bases] for _ in range(n_sets)]
+    pool_bytes = sum(w.device_bytes for s in pool for w in s)
+    setup_s = time.perf_counter() - t_setup
+
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev).manual_seed(2)
+    xs = {K: torch.randn((M, K), generator=gen, device=dev, dtype=torch.float32) for _, K in shapes}
+    ys = [torch.empty((M, N), device=dev, dtype=torch.float32) for N, _ in shapes]
+    stream = torch.cuda.current_stream(dev)
+
+    def step(i):
+        ws = pool[i % n_sets]
+        for j, (N, K) in enumerate(shapes):
+            backend.matmul_device(xs[K], ws[j], out=ys[j], stream=stream)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(args.warmup + i)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    step_bytes = sum(alg_bytes(prec, gs, N, K, M) for N, K in shapes)
+    value = step_bytes * args.steps / wall / 1e9
+
+    # ---- dominant kernel: the largest shape, back-to-back, HIP events
+    jd = int(np.argmax([alg_bytes(prec, gs, N, K, M) for N, K in shapes]))
+    Nd, Kd = shapes[jd]
+    reps = max(20, min(400, args.steps))
+    for i in range(10):
+        backend.matmul_device(xs[Kd], pool[i % n_sets][jd], out=ys[jd], stream=stream)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for i in range(reps):
+        backend.matmul_device(xs[Kd], pool[i % n_sets][jd], out=ys[jd], stream=stream)
+    ev1.record(stream)
+    ev1.synchronize()
+    kern_us = ev0.elapsed_time(ev1) * 1e3 / reps
+    kbytes = alg_bytes(prec, gs, Nd, Kd, M)
+    achieved = kbytes / (kern_us * 1e-6) / 1e9
+
+    # per-shape event timing (informational)
+    per_shape = {}
+    for j, (N, K) in enumerate(shapes):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(reps):
+            backend.matmul_device(xs[K], pool[i % n_sets][j], out=ys[j], stream=stream)
+        e1.record(stream)
+        e1.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        b = alg_bytes(prec, gs, N, K, M)
+        per_shape[f"{N}x{K}"] = {"us": round(us, 3), "GB_s": round(b / us / 1e3, 1),
+                                 "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
+                                 "path": pool[0][j].path}
+
+    out = {
+        "metric": "dequant-GEMV GB/s and % of HBM peak (INT4 g32, M=%d, 4 BASELINE shapes)" % M
+        if prec == "int4" else "dequant-GEMV GB/s and % of HBM peak (INT8 per-channel, M=%d)" % M,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(1e3 * wall / args.steps, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": args.workload,
+            "weights": "INT4 symmetric, group 32 along K (converter layout)" if prec == "int4"
+            else "INT8 symmetric per output channel",
+            "shapes_NxK": [f"{N}x{K}" for N, K in shapes],
+            "M": M,
+            "x": "fp32 N(0,1), W fp32 N(0,0.02) quantized",
+            "pool_bytes": pool_bytes,
+            "pool_sets": n_sets,
+            "frac_hbm_wall": round(value / HBM_PEAK_GBS, 4),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": f"{Nd}x{Kd} ({pool[0][jd].path})",
+            "kernel_us": round(kern_us, 3),
+            "alg_bytes_per_launch": kbytes,
+        },
+        "per_shape": per_shape,
+        "setup_s": round(setup_s, 1),
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(bases, shapes, M, args.cpu_budget)
+    print(json.dumps(out), flush=True)
+    backend.close()
+
+
+if __name__ == "__main__":
+    main()

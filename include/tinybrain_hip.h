@@ -1,0 +1,174 @@
+/*
+ * tinybrain_hip.h -- C ABI of TinyBrainHIP, the MI355X (gfx950) backend for
+ * TinyBrain's INT8/INT4 weight-only quantized matmul.
+ *
+ * The ABI is what a Swift `HIPBackend: QuantizedMatMulBackend` binds through
+ * a module map (`module CTinyBrainHIP { header "tinybrain_hip.h";
+ * link "tinybrain_hip"; export * }`).  Signatures carry plain pointers and
+ * sizes only.  All references are to vivekptnk/tinybrain paths.
+ *
+ * Conventions
+ *   - A weight has the reference shape [K, N] = [in_features, out_features]
+ *     (QuantizedTensor.shape, Sources/TinyBrainRuntime/QuantizedTensor.swift:73);
+ *     x is [M, K] row-major fp32, y is [M, N] row-major fp32.
+ *   - Every call returns a tbh_status; on failure tbh_last_error() returns a
+ *     message for the calling thread.  A Swift wrapper maps every non-zero
+ *     status to `throw`, which keeps the reference's fallback to its CPU path
+ *     (QuantizedTensor.swift:630-642).
+ */
+#ifndef TINYBRAIN_HIP_H
+#define TINYBRAIN_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TBH_ABI_VERSION 1
+
+/* ---- status ------------------------------------------------------------ */
+typedef int32_t tbh_status;
+enum {
+    TBH_OK = 0,
+    TBH_E_INVALID = 1,      /* bad descriptor, shape mismatch, null pointer */
+    TBH_E_UNSUPPORTED = 2,  /* a valid reference input this backend does not take */
+    TBH_E_NODEVICE = 3,     /* no usable gfx950 device */
+    TBH_E_OOM = 4,          /* device or host allocation failed */
+    TBH_E_HIP = 5           /* any other HIP runtime error */
+};
+
+/* ---- descriptor codes -------------------------------------------------- */
+/* QuantizationPrecision; the values are the TBF precision byte
+ * (ModelWeights.swift:395 writes them, :679 reads them). */
+enum { TBH_PREC_INT8 = 1, TBH_PREC_INT4 = 2 };
+
+/* QuantizationMode, QuantizedTensor.swift:31-37. */
+enum {
+    TBH_MODE_SYMMETRIC = 0,        /* INT8, one scale                      */
+    TBH_MODE_ASYMMETRIC = 1,       /* INT8, one scale + one zero point     */
+    TBH_MODE_PER_CHANNEL = 2,      /* INT8, one scale per output column n  */
+    TBH_MODE_INT4 = 3,             /* INT4, one scale per flat group       */
+    TBH_MODE_INT4_PER_CHANNEL = 4  /* rejected with TBH_E_UNSUPPORTED: the
+                                      reference's dequantize() reads its
+                                      scales along dim 0 while its quantizer
+                                      writes them along dim 1
+                                      (QuantizedTensor.swift:218-238 vs
+                                      :563-606), so the caller's CPU
+                                      fallback is the only defined result  */
+};
+
+/* Order of the flat element array.
+ *   KN_FLAT: element (k, n) is flat index k*N + n -- the runtime layout that
+ *            Tensor.quantize() writes (QuantizedTensor.swift:379-424,
+ *            :502-560) and dequantize() reads (:182-286).
+ *   NK_FLAT: element (k, n) is flat index n*K + k -- what
+ *            Scripts/convert_model.py:398-459 writes for INT4 (it quantizes
+ *            the PyTorch [N, K] tensor flattened and only reverses the
+ *            recorded shape, :489-502), i.e. groups run along K.
+ * For INT4 the group of flat index i is i / group_size in both layouts. */
+enum { TBH_LAYOUT_KN_FLAT = 0, TBH_LAYOUT_NK_FLAT = 1 };
+
+/* struct QuantizedTensor (QuantizedTensor.swift:62-166) as plain data.
+ * Counts are checked exactly as QuantizedTensor.init checks them
+ * (QuantizedTensor.swift:124-155):
+ *   data_bytes    == K*N (INT8) or ceil(K*N/2) (INT4, even flat index in the
+ *                    high nibble, QuantizedTensor.swift:201-213)
+ *   n_scales      == N (PER_CHANNEL), 1 (SYMMETRIC/ASYMMETRIC),
+ *                    ceil(K*N/group_size) (INT4, group_size > 0),
+ *                    1 (INT4, group_size == 0: one group of K*N)
+ *   n_zero_points == n_scales when zero_points != NULL. */
+typedef struct tbh_qtensor_desc {
+    int64_t K;
+    int64_t N;
+    int32_t precision;          /* TBH_PREC_*   */
+    int32_t mode;               /* TBH_MODE_*   */
+    int32_t layout;             /* TBH_LAYOUT_* */
+    int32_t group_size;         /* INT4 only; 0 = single group */
+    const int8_t *data;
+    int64_t data_bytes;
+    const float *scales;
+    int64_t n_scales;
+    const int8_t *zero_points;  /* nullable (Swift nil) */
+    int64_t n_zero_points;
+} tbh_qtensor_desc;
+
+/* Which kernel family serves a weight (see tbh_weight_info.path). */
+enum {
+    TBH_PATH_INT8_ROW = 0,      /* INT8, one scale (and zero point) per row  */
+    TBH_PATH_INT4_KGROUP = 1,   /* INT4, scales per (row, K-segment)         */
+    TBH_PATH_INT4_NGROUP = 2,   /* INT4 runtime layout, scales per (K, N-block) */
+    TBH_PATH_GENERIC = 3        /* any other INT4 grouping: slow, exact decode */
+};
+
+typedef struct tbh_weight_info {
+    int64_t K;
+    int64_t N;
+    int32_t precision;
+    int32_t mode;
+    int32_t layout;
+    int32_t group_size;
+    int32_t path;               /* TBH_PATH_* */
+    int32_t has_zero_points;    /* non-zero zero points were kept */
+    int64_t device_bytes;       /* bytes this weight holds in HBM */
+    int64_t stream_bytes;       /* bytes one matmul reads from it:
+                                   packed weights + scales + zero points */
+} tbh_weight_info;
+
+typedef struct tbh_device tbh_device;
+typedef struct tbh_weight tbh_weight;
+
+/* ---- library ----------------------------------------------------------- */
+int32_t tbh_abi_version(void);
+/* Message of the last failure on the calling thread ("" if none). */
+const char *tbh_last_error(void);
+const char *tbh_status_string(tbh_status status);
+
+/* ---- device ------------------------------------------------------------ */
+/* Replaces MetalBackend.init (Sources/TinyBrainMetal/MetalBackend.swift:38-56)
+ * and MetalBackend.isAvailable: opens HIP device `ordinal` (must be gfx950)
+ * with one internal stream.  TBH_E_NODEVICE when absent. */
+tbh_status tbh_device_open(int32_t ordinal, tbh_device **out);
+tbh_status tbh_device_close(tbh_device *dev);
+/* HIP device ordinal and compute-unit count of an open device. */
+tbh_status tbh_device_get_info(const tbh_device *dev, int32_t *ordinal, int32_t *cu_count);
+
+/* ---- weights ----------------------------------------------------------- */
+/* Replaces the weight upload of MetalBackend.cachedQuantizedBuffers
+ * (MetalBackend.swift:1282-1308) and cachedINT4Buffers (:1322-1359): copies
+ * the descriptor's arrays and repacks them ONCE into the gfx950 layout; the
+ * caller may free its arrays on return.  Thread-safe. */
+tbh_status tbh_weight_create(tbh_device *dev, const tbh_qtensor_desc *desc,
+                             tbh_weight **out);
+tbh_status tbh_weight_destroy(tbh_weight *w);
+tbh_status tbh_weight_get_info(const tbh_weight *w, tbh_weight_info *info);
+
+/* ---- matmul ------------------------------------------------------------ */
+/* Replaces QuantizedMatMulBackend.matmulQuantized
+ * (Sources/TinyBrainRuntime/Backend.swift:173-175), implemented by
+ * MetalBackend.matmulQuantized / matmulINT4 (MetalBackend.swift:894-1048):
+ * y[M,N] = x[M,K] . dequantize(w)[K,N] with fp32 accumulation.
+ * Host pointers; synchronous (the reference commits and waits, :959-960).
+ * Calls on one device are serialised. */
+tbh_status tbh_matmul(tbh_device *dev, const float *x, int64_t M, int64_t K,
+                      const tbh_weight *w, float *y);
+
+/* Same product on device pointers, enqueued on `stream` (a hipStream_t of the
+ * weight's device; NULL = the null stream).  Returns after the launch. */
+tbh_status tbh_matmul_device(const tbh_weight *w, const float *x, int64_t M,
+                             int64_t K, float *y, void *stream);
+
+/* ---- dequantize (verification) ----------------------------------------- */
+/* Replaces QuantizedTensor.dequantize() (QuantizedTensor.swift:182-286) for
+ * the uploaded weight: writes the [K, N] row-major fp32 matrix that the
+ * matmul multiplies by, bit-identical to (float)(q - zp) * scale.  For
+ * KN_FLAT weights this is exactly the reference's dequantize() output; for
+ * NK_FLAT INT4 it is that output read in the converter's [N, K] order and
+ * transposed.  Host pointer, synchronous. */
+tbh_status tbh_dequantize(tbh_device *dev, const tbh_weight *w, float *out);
+tbh_status tbh_dequantize_device(const tbh_weight *w, float *out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TINYBRAIN_HIP_H */

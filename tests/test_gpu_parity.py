@@ -1,0 +1,249 @@
+"""GPU parity: libtinybrain_hip vs the CPU oracle, through the C ABI.
+
+Bars (from the task's correctness contract):
+  * dequantize: bit-exact fp32 (bit patterns) vs QuantizedTensor.dequantize()
+    restated in the oracle;
+  * matmul: max|y^ - y| / max(|y|, 1e-3 * max_row|y|) <= 1e-3 against a float64
+    oracle over the same dequantized weights (GATE below), and L2 relative
+    error <= 1e-3 against the restated reference CPU path
+    (dequantize() + sgemm, QuantizedTensor.swift:640-642).
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle as O
+import tinybrain_amd as T
+from tinybrain_amd import _abi
+
+pytestmark = pytest.mark.gpu
+
+GATE = 1e-3          # floored max relative error vs float64
+CPU_PATH_L2 = 1e-3   # L2 relative error vs the reference CPU path
+
+
+@pytest.fixture(scope="module")
+def backend():
+    b = T.HIPBackend(0)
+    yield b
+    b.close()
+
+
+# ---------------------------------------------------------------------------
+# helpers
+# ---------------------------------------------------------------------------
+def _product(qt: O.QTensor, shape_kn, layout=T.Layout.KN_FLAT) -> T.QuantizedTensor:
+    return T.QuantizedTensor(shape_kn, qt.data, qt.scales, qt.mode, qt.precision, qt.group_size,
+                             qt.zero_points, layout)
+
+
+def _oracle_weight(qt: O.QTensor, layout) -> np.ndarray:
+    """Logical [K, N] fp32 weight: dequantize() in the stored flat order."""
+    if layout == T.Layout.KN_FLAT:
+        return O.dequantize(qt)
+    K, N = qt.shape
+    flat = O.QTensor((N, K), qt.data, qt.scales, qt.zero_points, qt.mode, qt.precision, qt.group_size)
+    return np.ascontiguousarray(O.dequantize(flat).T)
+
+
+def _check(backend, pq: T.QuantizedTensor, oq: O.QTensor, Ms=(1,), seed=1, cpu_path=True):
+    W = _oracle_weight(oq, pq.layout)
+    deq = backend.dequantize(pq)
+    np.testing.assert_array_equal(deq.view(np.uint32), W.view(np.uint32))
+    K = pq.shape[0]
+    for M in Ms:
+        x = O.fill_normal(seed * 1000 + M, M * K).reshape(M, K)
+        y = backend.matmulQuantized(x, pq)
+        y64 = O.gemm_f64(x, W)
+        err = O.parity_errors(y, y64)
+        assert err["gated"] <= GATE, (M, err)
+        if cpu_path:
+            y_ref = O.sgemm(x, W)
+            l2 = np.linalg.norm(y.astype(np.float64) - y_ref) / max(np.linalg.norm(y_ref), 1e-30)
+            assert l2 <= CPU_PATH_L2, (M, l2)
+    return backend.weight(pq)
+
+
+def _int8_pc(seed, K, N, std=0.02):
+    w = O.fill_normal(seed, K * N, std=std).reshape(K, N)
+    return O.quantize_per_channel(w)
+
+
+def _int4_nk(seed, K, N, gs, std=0.02):
+    """BASELINE / converter layout: PyTorch [N, K] quantized flat, groups along K."""
+    w_nk = O.fill_normal(seed, N * K, std=std).reshape(N, K)
+    qt = O.quantize_int4(w_nk, gs, O.ROUND_SWIFT)
+    qt.shape = (K, N)
+    return qt
+
+
+def _int4_kn(seed, K, N, gs, std=0.02):
+    """Runtime layout: Tensor.quantize(.int4) on [K, N]."""
+    return O.quantize_int4(O.fill_normal(seed, K * N, std=std).reshape(K, N), gs)
+
+
+# ---------------------------------------------------------------------------
+# INT8
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("K,N", [(128, 64), (100, 37), (2048, 256), (17, 8), (4096, 24)])
+def test_int8_per_channel(backend, K, N):
+    qt = _int8_pc(K * 7 + N, K, N)
+    w = _check(backend, _product(qt, (K, N)), qt, Ms=(1, 2, 3, 4, 5, 8))
+    assert w.path == "int8_row"
+
+
+def test_int8_baseline_config0(backend):
+    # W [5632 x 2048] (out x in) -> reference [K=2048, N=5632]
+    qt = _int8_pc(0x7B1A0000, 2048, 5632)
+    _check(backend, _product(qt, (2048, 5632)), qt, Ms=(1, 8))
+
+
+def test_int8_symmetric_and_asymmetric(backend):
+    w = O.fill_normal(77, 256 * 96).reshape(256, 96)
+    for qt in (O.quantize_symmetric(w), O.quantize_asymmetric(w - w.min() * 0.5)):
+        assert qt is not None
+        _check(backend, _product(qt, (256, 96)), qt, Ms=(1, 3))
+
+
+def test_int8_zero_points(backend):
+    qt = _int8_pc(78, 192, 40)
+    qt.zero_points = ((np.arange(40) % 9) - 4).astype(np.int8)
+    w = _check(backend, _product(qt, (192, 40)), qt, Ms=(1, 4))
+    assert w.has_zero_points
+
+
+def test_int8_reference_matmul_tolerance(backend):
+    # QuantizationTests.swift:117-135: INT8 matmul within 1% L2 of fp32
+    x = O.fill_normal(31, 128 * 256).reshape(128, 256)
+    w = O.fill_normal(32, 256 * 512).reshape(256, 512)
+    qt = O.quantize_per_channel(w)
+    y = backend.matmulQuantized(x, _product(qt, (256, 512)))
+    fp32 = O.sgemm(x, w)
+    assert np.linalg.norm(y - fp32) / np.linalg.norm(fp32) < 0.01
+
+
+# ---------------------------------------------------------------------------
+# INT4
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("K,N,gs", [(2048, 256, 32), (256, 40, 64), (512, 24, 128),
+                                    (96, 8, 32), (48, 10, 48), (100, 9, 0)])
+def test_int4_converter_layout(backend, K, N, gs):
+    qt = _int4_nk(K + N + gs, K, N, gs if gs else K * N)
+    if gs == 0:
+        qt.group_size = 0
+    w = _check(backend, _product(qt, (K, N), T.Layout.NK_FLAT), qt, Ms=(1, 2, 3, 4, 5, 8))
+    assert w.path == "int4_kgroup"
+
+
+@pytest.mark.parametrize("K,N", [(2048, 2048), (2048, 5632), (5632, 2048), (2048, 32000)])
+def test_int4_baseline_config1(backend, K, N):
+    # INT4 g32 along K, shapes [N x K], M in {1, 4, 8}
+    qt = _int4_nk(0x7B1A0010 + K + N, K, N, 32)
+    _check(backend, _product(qt, (K, N), T.Layout.NK_FLAT), qt, Ms=(1, 4, 8))
+
+
+@pytest.mark.parametrize("K,N,gs,path", [(256, 512, 32, "int4_ngroup"), (2048, 2048, 32, "int4_ngroup"),
+                                         (128, 64, 128, "int4_ngroup"), (64, 96, 96, "int4_ngroup"),
+                                         (40, 48, 48, "int4_ngroup"), (50, 40, 48, "generic"),
+                                         (33, 7, 16, "generic")])
+def test_int4_runtime_layout(backend, K, N, gs, path):
+    qt = _int4_kn(K * 3 + N + gs, K, N, gs)
+    w = _check(backend, _product(qt, (K, N)), qt, Ms=(1, 2, 4, 5))
+    assert w.path == path
+
+
+def test_int4_zero_points(backend):
+    qt = _int4_nk(91, 256, 24, 32)
+    qt.zero_points = ((np.arange(qt.scales.size) % 7) - 3).astype(np.int8)
+    w = _check(backend, _product(qt, (256, 24), T.Layout.NK_FLAT), qt, Ms=(1, 3))
+    assert w.path == "int4_kgroup" and w.has_zero_points
+    qk = _int4_kn(92, 64, 32, 32)
+    qk.zero_points = ((np.arange(qk.scales.size) % 5) - 2).astype(np.int8)
+    w = _check(backend, _product(qk, (64, 32)), qk, Ms=(1, 2))
+    assert w.path == "generic"
+
+
+def test_int4_nibble_minus_eight(backend):
+    # nibble 0x8 decodes to -8 (QuantizedTensor.swift:207-212) although the
+    # quantizers never write it
+    K, N = 64, 16
+    data = np.full(K * N // 2, np.uint8(0x8F).view(np.int8), np.int8)  # (-8, -1) pairs
+    scales = np.linspace(0.5, 2.0, K * N // 32).astype(np.float32)
+    qt = O.QTensor((K, N), data, scales, None, O.MODE_INT4, O.PREC_INT4, 32)
+    _check(backend, _product(qt, (K, N), T.Layout.NK_FLAT), qt, Ms=(1, 2))
+    _check(backend, _product(qt, (K, N)), qt, Ms=(1, 2))
+
+
+def test_int4_reference_metal_vs_cpu_consistency(backend):
+    # INT4QuantizationTests.swift:233-254: 8x128 @ 128x64, gs=128, GPU vs CPU <1% L2
+    x = O.fill_normal(51, 8 * 128).reshape(8, 128)
+    qt = O.quantize_int4(O.fill_normal(52, 128 * 64).reshape(128, 64), 128)
+    y = backend.matmulQuantized(x, _product(qt, (128, 64)))
+    y_cpu, _, _ = O.matmul_quantized_cpu(x, qt)
+    assert np.linalg.norm(y - y_cpu) / np.linalg.norm(y_cpu) < 0.01
+    assert O.parity_errors(y, O.gemm_f64(x, O.dequantize(qt)))["gated"] <= GATE
+
+
+# ---------------------------------------------------------------------------
+# boundary behaviour
+# ---------------------------------------------------------------------------
+def test_shape_mismatch_is_a_precondition(backend):
+    qt = _int8_pc(5, 64, 16)
+    pq = _product(qt, (64, 16))
+    with pytest.raises(T.PreconditionFailure):
+        backend.matmulQuantized(np.zeros((2, 63), np.float32), pq)
+    with pytest.raises(T.PreconditionFailure):
+        backend.matmulQuantized(np.zeros(64, np.float32), pq)
+    # the C ABI reports it as TBH_E_INVALID
+    w = backend.weight(pq)
+    x = np.zeros((1, 63), np.float32)
+    y = np.zeros((1, 16), np.float32)
+    st = _abi.lib().tbh_matmul(backend._dev, x.ctypes.data, 1, 63, w.handle, y.ctypes.data)
+    assert st == _abi.E_INVALID
+
+
+def test_int4_per_channel_is_unsupported(backend):
+    qt = O.quantize_int4_per_channel(O.fill_normal(6, 16 * 32).reshape(16, 32))
+    with pytest.raises(T.HIPBackendError) as e:
+        backend.matmulQuantized(np.zeros((1, 16), np.float32), _product(qt, (16, 32)))
+    assert e.value.status == _abi.E_UNSUPPORTED
+
+
+def test_empty_input(backend):
+    qt = _int8_pc(8, 32, 8)
+    y = backend.matmulQuantized(np.zeros((0, 32), np.float32), _product(qt, (32, 8)))
+    assert y.shape == (0, 8)
+
+
+def test_weight_cached_by_identifier_and_deterministic(backend):
+    qt = _int4_nk(9, 512, 64, 32)
+    pq = _product(qt, (512, 64), T.Layout.NK_FLAT)
+    x = O.fill_normal(10, 3 * 512).reshape(3, 512)
+    y1 = backend.matmulQuantized(x, pq)
+    w1 = backend.weight(pq)
+    y2 = backend.matmulQuantized(x, pq)
+    assert backend.weight(pq) is w1
+    np.testing.assert_array_equal(y1, y2)
+
+
+def test_device_resident_entry_point(backend):
+    import torch
+
+    qt = _int4_nk(12, 2048, 512, 32)
+    pq = _product(qt, (2048, 512), T.Layout.NK_FLAT)
+    w = backend.weight(pq)
+    W = _oracle_weight(qt, T.Layout.NK_FLAT)
+    stream = torch.cuda.Stream()
+    for M in (1, 4, 8):
+        x = O.fill_normal(13 + M, M * 2048).reshape(M, 2048)
+        xd = torch.from_numpy(x).cuda()
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            yd = backend.matmul_device(xd, w, stream=stream)
+        stream.synchronize()
+        err = O.parity_errors(yd.cpu().numpy(), O.gemm_f64(x, W))
+        assert err["gated"] <= GATE
+    deq = backend.dequantize_device(w)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(deq.cpu().numpy().view(np.uint32), W.view(np.uint32))

@@ -1,0 +1,104 @@
+"""ctypes binding of include/tinybrain_hip.h (libtinybrain_hip.so).
+
+The library is built in-tree by ``python -m tinybrain_amd.build``.  There is
+no fallback: if the library is missing, loading raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libtinybrain_hip.so")
+
+# status codes
+OK, E_INVALID, E_UNSUPPORTED, E_NODEVICE, E_OOM, E_HIP = range(6)
+# descriptor codes (QuantizationPrecision / QuantizationMode / layout)
+PREC_INT8, PREC_INT4 = 1, 2
+MODE_SYMMETRIC, MODE_ASYMMETRIC, MODE_PER_CHANNEL, MODE_INT4, MODE_INT4_PER_CHANNEL = range(5)
+LAYOUT_KN_FLAT, LAYOUT_NK_FLAT = 0, 1
+PATH_INT8_ROW, PATH_INT4_KGROUP, PATH_INT4_NGROUP, PATH_GENERIC = range(4)
+PATH_NAMES = {0: "int8_row", 1: "int4_kgroup", 2: "int4_ngroup", 3: "generic"}
+
+# every symbol the header declares
+EXPORTS = [
+    "tbh_abi_version", "tbh_last_error", "tbh_status_string",
+    "tbh_device_open", "tbh_device_close", "tbh_device_get_info",
+    "tbh_weight_create", "tbh_weight_destroy", "tbh_weight_get_info",
+    "tbh_matmul", "tbh_matmul_device",
+    "tbh_dequantize", "tbh_dequantize_device",
+]
+
+
+class QTensorDesc(ctypes.Structure):
+    _fields_ = [
+        ("K", ctypes.c_int64),
+        ("N", ctypes.c_int64),
+        ("precision", ctypes.c_int32),
+        ("mode", ctypes.c_int32),
+        ("layout", ctypes.c_int32),
+        ("group_size", ctypes.c_int32),
+        ("data", ctypes.c_void_p),
+        ("data_bytes", ctypes.c_int64),
+        ("scales", ctypes.c_void_p),
+        ("n_scales", ctypes.c_int64),
+        ("zero_points", ctypes.c_void_p),
+        ("n_zero_points", ctypes.c_int64),
+    ]
+
+
+class WeightInfo(ctypes.Structure):
+    _fields_ = [
+        ("K", ctypes.c_int64),
+        ("N", ctypes.c_int64),
+        ("precision", ctypes.c_int32),
+        ("mode", ctypes.c_int32),
+        ("layout", ctypes.c_int32),
+        ("group_size", ctypes.c_int32),
+        ("path", ctypes.c_int32),
+        ("has_zero_points", ctypes.c_int32),
+        ("device_bytes", ctypes.c_int64),
+        ("stream_bytes", ctypes.c_int64),
+    ]
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libtinybrain_hip.so (raises OSError when it is not built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise OSError(f"{LIB_PATH} is not built; run `python -m tinybrain_amd.build`")
+    L = ctypes.CDLL(LIB_PATH)
+    vp, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+    pp = ctypes.POINTER(ctypes.c_void_p)
+    L.tbh_abi_version.restype = i32
+    L.tbh_last_error.restype = ctypes.c_char_p
+    L.tbh_status_string.restype = ctypes.c_char_p
+    L.tbh_status_string.argtypes = [i32]
+    L.tbh_device_open.argtypes = [i32, pp]
+    L.tbh_device_close.argtypes = [vp]
+    L.tbh_device_get_info.argtypes = [vp, ctypes.POINTER(i32), ctypes.POINTER(i32)]
+    L.tbh_weight_create.argtypes = [vp, ctypes.POINTER(QTensorDesc), pp]
+    L.tbh_weight_destroy.argtypes = [vp]
+    L.tbh_weight_get_info.argtypes = [vp, ctypes.POINTER(WeightInfo)]
+    L.tbh_matmul.argtypes = [vp, vp, i64, i64, vp, vp]
+    L.tbh_matmul_device.argtypes = [vp, vp, i64, i64, vp, vp]
+    L.tbh_dequantize.argtypes = [vp, vp, vp]
+    L.tbh_dequantize_device.argtypes = [vp, vp, vp]
+    for name in ("tbh_device_open", "tbh_device_close", "tbh_device_get_info",
+                 "tbh_weight_create", "tbh_weight_destroy", "tbh_weight_get_info",
+                 "tbh_matmul", "tbh_matmul_device", "tbh_dequantize", "tbh_dequantize_device"):
+        getattr(L, name).restype = i32
+    _lib = L
+    return L
+
+
+def last_error() -> str:
+    return lib().tbh_last_error().decode("utf-8", "replace")
+
+
+def status_name(st: int) -> str:
+    return lib().tbh_status_string(st).decode()

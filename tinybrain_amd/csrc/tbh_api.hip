@@ -1,0 +1,525 @@
+// tbh_api.hip -- C ABI of libtinybrain_hip: devices, weight upload + repack,
+// matmul dispatch.  Kernels live in tbh_gemv.hip and tbh_ref_kernels.hip.
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <thread>
+#include <vector>
+
+#include "tbh_internal.h"
+
+namespace tbh {
+
+namespace {
+thread_local std::string g_last_error;
+
+int host_threads() {
+    unsigned n = std::thread::hardware_concurrency();
+    return (int)std::max(1u, std::min(n, 16u));
+}
+
+// Runs fn(lo, hi) over [0, n) split into contiguous pieces on host threads.
+template <class F>
+void parallel_for(int64_t n, F fn) {
+    int t = host_threads();
+    if (n < 4096 || t == 1) {
+        fn(int64_t(0), n);
+        return;
+    }
+    std::vector<std::thread> pool;
+    int64_t step = (n + t - 1) / t;
+    for (int i = 0; i < t; ++i) {
+        int64_t lo = i * step, hi = std::min(n, lo + step);
+        if (lo >= hi) break;
+        pool.emplace_back([=] { fn(lo, hi); });
+    }
+    for (auto &th : pool) th.join();
+}
+
+int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+}  // namespace
+
+tbh_status set_error(tbh_status st, const std::string &msg) {
+    g_last_error = msg;
+    return st;
+}
+
+tbh_status hip_error(hipError_t e, const char *what) {
+    std::string m = std::string(what) + ": " + hipGetErrorString(e);
+    return set_error(e == hipErrorOutOfMemory ? TBH_E_OOM : TBH_E_HIP, m);
+}
+
+}  // namespace tbh
+
+using namespace tbh;
+
+#define TBH_HIP(call, what)                          \
+    do {                                             \
+        hipError_t e_ = (call);                      \
+        if (e_ != hipSuccess) return hip_error(e_, what); \
+    } while (0)
+
+// Makes the weight's device current on the calling thread.
+static tbh_status use_device(int32_t ordinal) {
+    int cur = -1;
+    TBH_HIP(hipGetDevice(&cur), "hipGetDevice");
+    if (cur != ordinal) TBH_HIP(hipSetDevice(ordinal), "hipSetDevice");
+    return TBH_OK;
+}
+
+extern "C" {
+
+int32_t tbh_abi_version(void) { return TBH_ABI_VERSION; }
+
+const char *tbh_last_error(void) { return g_last_error.c_str(); }
+
+const char *tbh_status_string(tbh_status st) {
+    switch (st) {
+    case TBH_OK: return "TBH_OK";
+    case TBH_E_INVALID: return "TBH_E_INVALID";
+    case TBH_E_UNSUPPORTED: return "TBH_E_UNSUPPORTED";
+    case TBH_E_NODEVICE: return "TBH_E_NODEVICE";
+    case TBH_E_OOM: return "TBH_E_OOM";
+    case TBH_E_HIP: return "TBH_E_HIP";
+    default: return "TBH_E_UNKNOWN";
+    }
+}
+
+// ---------------------------------------------------------------------------
+// device
+// ---------------------------------------------------------------------------
+tbh_status tbh_device_open(int32_t ordinal, tbh_device **out) {
+    if (!out) return set_error(TBH_E_INVALID, "tbh_device_open: out is NULL");
+    *out = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0)
+        return set_error(TBH_E_NODEVICE, "tbh_device_open: no HIP device");
+    if (ordinal < 0 || ordinal >= count)
+        return set_error(TBH_E_NODEVICE, "tbh_device_open: ordinal out of range");
+    hipDeviceProp_t prop;
+    TBH_HIP(hipGetDeviceProperties(&prop, ordinal), "hipGetDeviceProperties");
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return set_error(TBH_E_NODEVICE, std::string("tbh_device_open: device is ") +
+                                             prop.gcnArchName + ", this library is built for gfx950");
+    TBH_HIP(hipSetDevice(ordinal), "hipSetDevice");
+    auto dev = std::make_unique<tbh_device>();
+    dev->ordinal = ordinal;
+    dev->cu_count = prop.multiProcessorCount;
+    TBH_HIP(hipStreamCreateWithFlags(&dev->stream, hipStreamNonBlocking), "hipStreamCreate");
+    *out = dev.release();
+    return TBH_OK;
+}
+
+tbh_status tbh_device_close(tbh_device *dev) {
+    if (!dev) return TBH_OK;
+    use_device(dev->ordinal);
+    if (dev->stream) hipStreamSynchronize(dev->stream);
+    if (dev->stage) hipFree(dev->stage);
+    if (dev->stream) hipStreamDestroy(dev->stream);
+    delete dev;
+    return TBH_OK;
+}
+
+tbh_status tbh_device_get_info(const tbh_device *dev, int32_t *ordinal, int32_t *cu_count) {
+    if (!dev) return set_error(TBH_E_INVALID, "tbh_device_get_info: dev is NULL");
+    if (ordinal) *ordinal = dev->ordinal;
+    if (cu_count) *cu_count = dev->cu_count;
+    return TBH_OK;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// descriptor validation: QuantizedTensor.init preconditions
+// (QuantizedTensor.swift:124-155) plus the combinations this backend takes
+// ---------------------------------------------------------------------------
+static tbh_status validate_desc(const tbh_qtensor_desc *d) {
+    if (!d) return set_error(TBH_E_INVALID, "descriptor is NULL");
+    if (d->K <= 0 || d->N <= 0)
+        return set_error(TBH_E_INVALID, "weight shape must be [K>0, N>0]");
+    if (d->layout != TBH_LAYOUT_KN_FLAT && d->layout != TBH_LAYOUT_NK_FLAT)
+        return set_error(TBH_E_INVALID, "unknown layout");
+    if (d->group_size < 0) return set_error(TBH_E_INVALID, "group_size < 0");
+    const int64_t count = d->K * d->N;
+    if (d->precision == TBH_PREC_INT8) {
+        if (d->data_bytes != count)
+            return set_error(TBH_E_INVALID, "INT8: data count must match shape");
+    } else if (d->precision == TBH_PREC_INT4) {
+        if (d->data_bytes != (count + 1) / 2)
+            return set_error(TBH_E_INVALID, "INT4: data count should be ceil(shape.count / 2)");
+    } else {
+        return set_error(TBH_E_INVALID, "unknown precision");
+    }
+    int64_t want_scales = 0;
+    switch (d->mode) {
+    case TBH_MODE_PER_CHANNEL:
+    case TBH_MODE_INT4_PER_CHANNEL: want_scales = d->N; break;
+    case TBH_MODE_SYMMETRIC:
+    case TBH_MODE_ASYMMETRIC: want_scales = 1; break;
+    case TBH_MODE_INT4:
+        want_scales = d->group_size > 0 ? (count + d->group_size - 1) / d->group_size : 1;
+        break;
+    default: return set_error(TBH_E_INVALID, "unknown mode");
+    }
+    if (d->n_scales != want_scales)
+        return set_error(TBH_E_INVALID, "scale count does not match mode/shape (need " +
+                                            std::to_string(want_scales) + ", got " +
+                                            std::to_string(d->n_scales) + ")");
+    if (!d->data || !d->scales) return set_error(TBH_E_INVALID, "data or scales is NULL");
+    if (d->zero_points && d->n_zero_points != d->n_scales)
+        return set_error(TBH_E_INVALID, "Zero points must match scales");
+    if (d->precision == TBH_PREC_INT8 &&
+        !(d->mode == TBH_MODE_SYMMETRIC || d->mode == TBH_MODE_ASYMMETRIC ||
+          d->mode == TBH_MODE_PER_CHANNEL))
+        return set_error(TBH_E_UNSUPPORTED, "INT8 precision with an INT4 mode");
+    if (d->precision == TBH_PREC_INT4 && d->mode == TBH_MODE_INT4_PER_CHANNEL)
+        return set_error(TBH_E_UNSUPPORTED,
+                         "int4PerChannel: the reference's dequantize() and quantizer disagree "
+                         "on the channel axis; use the caller's CPU fallback");
+    if (d->precision == TBH_PREC_INT4 && d->mode != TBH_MODE_INT4)
+        return set_error(TBH_E_UNSUPPORTED, "INT4 precision with an INT8 mode");
+    return TBH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// host repack
+// ---------------------------------------------------------------------------
+namespace {
+
+// q-matrix [N][K] (int8 values, K contiguous) from the flat reference array.
+std::vector<int8_t> expand_nk(const tbh_qtensor_desc &d) {
+    const int64_t K = d.K, N = d.N;
+    std::vector<int8_t> q((size_t)(K * N));
+    const uint8_t *src = reinterpret_cast<const uint8_t *>(d.data);
+    const bool int4 = d.precision == TBH_PREC_INT4;
+    auto at = [&](int64_t i) -> int8_t {
+        if (!int4) return (int8_t)src[i];
+        unsigned b = src[i >> 1];
+        unsigned raw = (i & 1) == 0 ? (b >> 4) & 0xFu : b & 0xFu;
+        return (int8_t)(raw > 7 ? (int)raw - 16 : (int)raw);
+    };
+    if (d.layout == TBH_LAYOUT_NK_FLAT) {
+        parallel_for(N, [&](int64_t lo, int64_t hi) {
+            for (int64_t n = lo; n < hi; ++n)
+                for (int64_t k = 0; k < K; ++k) q[n * K + k] = at(n * K + k);
+        });
+    } else {
+        // transpose in 64 x 64 tiles
+        const int64_t T = 64;
+        int64_t tiles_n = (N + T - 1) / T;
+        parallel_for(tiles_n, [&](int64_t lo, int64_t hi) {
+            for (int64_t tn = lo; tn < hi; ++tn) {
+                int64_t n0 = tn * T, n1 = std::min(N, n0 + T);
+                for (int64_t k0 = 0; k0 < K; k0 += T) {
+                    int64_t k1 = std::min(K, k0 + T);
+                    for (int64_t k = k0; k < k1; ++k)
+                        for (int64_t n = n0; n < n1; ++n) q[n * K + k] = at(k * N + n);
+                }
+            }
+        });
+    }
+    return q;
+}
+
+// INT8 row [Kp] bytes: within each 4-byte word, elements k..k+3 sit at byte
+// positions {0, 2, 1, 3} so that (w & 0x00FF00FF) and ((w >> 8) & 0x00FF00FF)
+// hold the pairs (k, k+1) and (k+2, k+3).  Values are offset binary (q+128).
+void pack_int8_rows(const std::vector<int8_t> &q, int64_t K, int64_t N, int64_t Kp, int64_t Np,
+                    std::vector<uint8_t> &out) {
+    static const int bp[4] = {0, 2, 1, 3};
+    out.assign((size_t)(Np * Kp), 0x80);
+    parallel_for(N, [&](int64_t lo, int64_t hi) {
+        for (int64_t n = lo; n < hi; ++n) {
+            uint8_t *row = out.data() + n * Kp;
+            const int8_t *qr = q.data() + n * K;
+            for (int64_t k = 0; k < K; ++k)
+                row[(k & ~int64_t(3)) + bp[k & 3]] = (uint8_t)((int)qr[k] + 128);
+        }
+    });
+}
+
+// INT4 row [Kp/2] bytes: each 32-bit word holds 8 consecutive elements
+// k..k+7 as offset-binary nibbles (q+8) at bit offsets
+// {0, 16, 4, 20, 8, 24, 12, 28}, which the kernel turns into f16 pairs with
+// two AND-ORs per shift.
+void pack_int4_rows(const std::vector<int8_t> &q, int64_t K, int64_t N, int64_t Kp, int64_t Np,
+                    std::vector<uint8_t> &out) {
+    static const int nb[8] = {0, 16, 4, 20, 8, 24, 12, 28};
+    const int64_t row_words = Kp / 8;
+    out.assign((size_t)(Np * Kp / 2), 0x88);
+    parallel_for(N, [&](int64_t lo, int64_t hi) {
+        for (int64_t n = lo; n < hi; ++n) {
+            uint32_t *row = reinterpret_cast<uint32_t *>(out.data() + n * (Kp / 2));
+            const int8_t *qr = q.data() + n * K;
+            for (int64_t wi = 0; wi < row_words; ++wi) {
+                uint32_t word = 0;
+                for (int j = 0; j < 8; ++j) {
+                    int64_t k = wi * 8 + j;
+                    int v = k < K ? qr[k] : 0;
+                    word |= (uint32_t)((v + 8) & 0xF) << nb[j];
+                }
+                row[wi] = word;
+            }
+        }
+    });
+}
+
+bool any_nonzero(const int8_t *p, int64_t n) {
+    if (!p) return false;
+    for (int64_t i = 0; i < n; ++i)
+        if (p[i] != 0) return true;
+    return false;
+}
+
+template <class T>
+hipError_t upload(T **dst, const T *src, size_t count, int64_t &bytes) {
+    size_t nbytes = std::max<size_t>(count * sizeof(T), 1);
+    hipError_t e = hipMalloc((void **)dst, nbytes);
+    if (e != hipSuccess) return e;
+    bytes += (int64_t)(count * sizeof(T));
+    return hipMemcpy(*dst, src, count * sizeof(T), hipMemcpyHostToDevice);
+}
+
+void free_weight(tbh_weight *w) {
+    if (!w) return;
+    hipFree(w->data);
+    hipFree(w->scales);
+    hipFree(w->zp);
+    hipFree(w->raw);
+    hipFree(w->raw_scales);
+    hipFree(w->raw_zp);
+    delete w;
+}
+
+}  // namespace
+
+extern "C" {
+
+tbh_status tbh_weight_create(tbh_device *dev, const tbh_qtensor_desc *desc, tbh_weight **out) {
+    if (!out) return set_error(TBH_E_INVALID, "tbh_weight_create: out is NULL");
+    *out = nullptr;
+    if (!dev) return set_error(TBH_E_INVALID, "tbh_weight_create: dev is NULL");
+    tbh_status st = validate_desc(desc);
+    if (st != TBH_OK) return st;
+    st = use_device(dev->ordinal);
+    if (st != TBH_OK) return st;
+
+    const tbh_qtensor_desc &d = *desc;
+    std::unique_ptr<tbh_weight, void (*)(tbh_weight *)> w(new tbh_weight, free_weight);
+    w->dev = dev;
+    w->K = d.K;
+    w->N = d.N;
+    w->precision = d.precision;
+    w->mode = d.mode;
+    w->layout = d.layout;
+    w->group_size = d.group_size;
+    const int64_t K = d.K, N = d.N, count = K * N;
+    const bool has_zp = any_nonzero(d.zero_points, d.n_zero_points);
+    hipError_t e = hipSuccess;
+
+    if (d.precision == TBH_PREC_INT8) {
+        w->path = Path::Int8Row;
+        w->Kp = round_up(K, kInt8ChunkElems);
+        w->Np = round_up(N, 8);
+        w->row_bytes = w->Kp;
+        std::vector<int8_t> q = expand_nk(d);
+        std::vector<uint8_t> packed;
+        pack_int8_rows(q, K, N, w->Kp, w->Np, packed);
+        std::vector<float> s((size_t)w->Np, 0.0f);
+        std::vector<int8_t> z((size_t)w->Np, 0);
+        const bool per_ch = d.mode == TBH_MODE_PER_CHANNEL;
+        for (int64_t n = 0; n < N; ++n) {
+            s[n] = d.scales[per_ch ? n : 0];
+            if (d.zero_points) z[n] = d.zero_points[per_ch ? n : 0];
+        }
+        e = upload(&w->data, packed.data(), packed.size(), w->device_bytes);
+        if (e == hipSuccess) e = upload(&w->scales, s.data(), s.size(), w->device_bytes);
+        if (e == hipSuccess && has_zp) e = upload(&w->zp, z.data(), z.size(), w->device_bytes);
+        w->stream_bytes = K * N + 4 * N + (has_zp ? N : 0);
+    } else {
+        const int64_t gs = d.group_size > 0 ? d.group_size : count;
+        auto group_of = [&](int64_t k, int64_t n) -> int64_t {
+            int64_t i = d.layout == TBH_LAYOUT_KN_FLAT ? k * N + n : n * K + k;
+            return i / gs;
+        };
+        // Which tables describe the grouping exactly?
+        bool kgroup = false, ngroup = false;
+        int64_t seg = 0;       // Int4KGroup: K-segment length sharing one scale (0 = whole row)
+        int64_t rpn = 0;       // Int4NGroup: rows sharing one per-k scale column
+        if (gs >= count) {
+            kgroup = true;
+            seg = 0;
+        } else if (d.layout == TBH_LAYOUT_NK_FLAT) {
+            if (K % gs == 0 && gs % kInt4ChunkElems == 0) { kgroup = true; seg = gs; }
+            else if (gs % K == 0) { kgroup = true; seg = 0; }
+        } else {
+            if (!has_zp) {
+                if (N % gs == 0) { ngroup = true; rpn = gs; }
+                else if (gs % N == 0) { ngroup = true; rpn = 0; }
+            }
+        }
+        if (kgroup || ngroup) {
+            w->Kp = round_up(K, kInt4ChunkElems);
+            w->Np = round_up(N, 8);
+            w->row_bytes = w->Kp / 2;
+            std::vector<int8_t> q = expand_nk(d);
+            std::vector<uint8_t> packed;
+            pack_int4_rows(q, K, N, w->Kp, w->Np, packed);
+            e = upload(&w->data, packed.data(), packed.size(), w->device_bytes);
+            if (kgroup) {
+                w->path = Path::Int4KGroup;
+                const int64_t G = seg ? K / seg : 1;
+                w->groups_per_row = G;
+                w->chunks_per_group = (int32_t)(seg ? seg / kInt4ChunkElems : w->Kp / kInt4ChunkElems);
+                std::vector<float> s((size_t)(w->Np * G), 0.0f);
+                std::vector<int8_t> z((size_t)(w->Np * G), 0);
+                for (int64_t n = 0; n < N; ++n)
+                    for (int64_t g = 0; g < G; ++g) {
+                        int64_t gi = group_of(seg ? g * seg : 0, n);
+                        s[n * G + g] = d.scales[gi];
+                        if (d.zero_points) z[n * G + g] = d.zero_points[gi];
+                    }
+                if (e == hipSuccess) e = upload(&w->scales, s.data(), s.size(), w->device_bytes);
+                if (e == hipSuccess && has_zp) e = upload(&w->zp, z.data(), z.size(), w->device_bytes);
+                w->stream_bytes = (count + 1) / 2 + 4 * N * G + (has_zp ? N * G : 0);
+            } else {
+                w->path = Path::Int4NGroup;
+                w->rows_per_nblock = (int32_t)(rpn ? rpn : w->Np);
+                const int64_t NB = (w->Np + w->rows_per_nblock - 1) / w->rows_per_nblock;
+                std::vector<float> t((size_t)(NB * w->Kp), 0.0f);
+                for (int64_t nb = 0; nb < NB; ++nb) {
+                    int64_t n = std::min(N - 1, nb * w->rows_per_nblock);
+                    if (nb * w->rows_per_nblock >= N) continue;
+                    for (int64_t k = 0; k < K; ++k) t[nb * w->Kp + k] = d.scales[group_of(k, n)];
+                }
+                if (e == hipSuccess) e = upload(&w->scales, t.data(), t.size(), w->device_bytes);
+                w->stream_bytes = (count + 1) / 2 + 4 * d.n_scales;
+            }
+        } else {
+            w->path = Path::Generic;
+            w->raw_bytes = d.data_bytes;
+            w->n_scales = d.n_scales;
+            e = upload(&w->raw, d.data, (size_t)d.data_bytes, w->device_bytes);
+            if (e == hipSuccess) e = upload(&w->raw_scales, d.scales, (size_t)d.n_scales, w->device_bytes);
+            if (e == hipSuccess && has_zp)
+                e = upload(&w->raw_zp, d.zero_points, (size_t)d.n_scales, w->device_bytes);
+            w->stream_bytes = d.data_bytes + 4 * d.n_scales + (has_zp ? d.n_scales : 0);
+        }
+    }
+    if (e != hipSuccess) return hip_error(e, "tbh_weight_create: upload");
+    *out = w.release();
+    return TBH_OK;
+}
+
+tbh_status tbh_weight_destroy(tbh_weight *w) {
+    if (!w) return TBH_OK;
+    use_device(w->dev->ordinal);
+    free_weight(w);
+    return TBH_OK;
+}
+
+tbh_status tbh_weight_get_info(const tbh_weight *w, tbh_weight_info *info) {
+    if (!w || !info) return set_error(TBH_E_INVALID, "tbh_weight_get_info: NULL argument");
+    info->K = w->K;
+    info->N = w->N;
+    info->precision = w->precision;
+    info->mode = w->mode;
+    info->layout = w->layout;
+    info->group_size = w->group_size;
+    info->path = (int32_t)w->path;
+    info->has_zero_points = (w->zp || w->raw_zp) ? 1 : 0;
+    info->device_bytes = w->device_bytes;
+    info->stream_bytes = w->stream_bytes;
+    return TBH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// matmul
+// ---------------------------------------------------------------------------
+static tbh_status matmul_enqueue(const tbh_weight *w, const float *x, int64_t M, float *y,
+                                 hipStream_t s) {
+    const int64_t rows = gemv_max_rows(*w);
+    for (int64_t m0 = 0; m0 < M;) {
+        int64_t mc = rows > 0 ? std::min(rows, M - m0) : M - m0;
+        GemvArgs a{x + m0 * w->K, w->K, y + m0 * w->N, w->N, mc};
+        hipError_t e = rows > 0 ? launch_gemv(*w, a, s) : launch_generic(*w, a, s);
+        if (e != hipSuccess) return hip_error(e, "matmul kernel launch");
+        m0 += mc;
+    }
+    return TBH_OK;
+}
+
+tbh_status tbh_matmul_device(const tbh_weight *w, const float *x, int64_t M, int64_t K, float *y,
+                             void *stream) {
+    if (!w) return set_error(TBH_E_INVALID, "tbh_matmul_device: weight is NULL");
+    if (M < 0) return set_error(TBH_E_INVALID, "tbh_matmul_device: M < 0");
+    if (K != w->K) return set_error(TBH_E_INVALID, "Dimensions must match (x K != weight K)");
+    if (M == 0) return TBH_OK;
+    if (!x || !y) return set_error(TBH_E_INVALID, "tbh_matmul_device: x or y is NULL");
+    tbh_status st = use_device(w->dev->ordinal);
+    if (st != TBH_OK) return st;
+    return matmul_enqueue(w, x, M, y, (hipStream_t)stream);
+}
+
+tbh_status tbh_matmul(tbh_device *dev, const float *x, int64_t M, int64_t K, const tbh_weight *w,
+                      float *y) {
+    if (!dev || !w) return set_error(TBH_E_INVALID, "tbh_matmul: NULL device or weight");
+    if (w->dev != dev) return set_error(TBH_E_INVALID, "tbh_matmul: weight belongs to another device");
+    if (M < 0) return set_error(TBH_E_INVALID, "tbh_matmul: M < 0");
+    if (K != w->K) return set_error(TBH_E_INVALID, "Dimensions must match (x K != weight K)");
+    if (M == 0) return TBH_OK;
+    if (!x || !y) return set_error(TBH_E_INVALID, "tbh_matmul: x or y is NULL");
+    std::lock_guard<std::mutex> lock(dev->mu);
+    tbh_status st = use_device(dev->ordinal);
+    if (st != TBH_OK) return st;
+    const size_t xb = (size_t)(M * K) * sizeof(float), yb = (size_t)(M * w->N) * sizeof(float);
+    const size_t need = ((xb + 255) & ~size_t(255)) + yb;
+    if (dev->stage_bytes < need) {
+        hipFree(dev->stage);
+        dev->stage = nullptr;
+        dev->stage_bytes = 0;
+        TBH_HIP(hipMalloc(&dev->stage, need), "tbh_matmul: staging buffer");
+        dev->stage_bytes = need;
+    }
+    float *dx = (float *)dev->stage;
+    float *dy = (float *)((char *)dev->stage + ((xb + 255) & ~size_t(255)));
+    TBH_HIP(hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, dev->stream), "tbh_matmul: copy x");
+    st = matmul_enqueue(w, dx, M, dy, dev->stream);
+    if (st != TBH_OK) return st;
+    TBH_HIP(hipMemcpyAsync(y, dy, yb, hipMemcpyDeviceToHost, dev->stream), "tbh_matmul: copy y");
+    TBH_HIP(hipStreamSynchronize(dev->stream), "tbh_matmul: synchronize");
+    return TBH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// dequantize
+// ---------------------------------------------------------------------------
+tbh_status tbh_dequantize_device(const tbh_weight *w, float *out, void *stream) {
+    if (!w || !out) return set_error(TBH_E_INVALID, "tbh_dequantize_device: NULL argument");
+    tbh_status st = use_device(w->dev->ordinal);
+    if (st != TBH_OK) return st;
+    hipError_t e = launch_dequant(*w, out, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_error(e, "dequantize kernel launch");
+    return TBH_OK;
+}
+
+tbh_status tbh_dequantize(tbh_device *dev, const tbh_weight *w, float *out) {
+    if (!dev || !w || !out) return set_error(TBH_E_INVALID, "tbh_dequantize: NULL argument");
+    if (w->dev != dev) return set_error(TBH_E_INVALID, "tbh_dequantize: weight belongs to another device");
+    std::lock_guard<std::mutex> lock(dev->mu);
+    tbh_status st = use_device(dev->ordinal);
+    if (st != TBH_OK) return st;
+    const size_t bytes = (size_t)(w->K * w->N) * sizeof(float);
+    float *d = nullptr;
+    TBH_HIP(hipMalloc(&d, bytes), "tbh_dequantize: output buffer");
+    hipError_t e = launch_dequant(*w, d, dev->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(out, d, bytes, hipMemcpyDeviceToHost, dev->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(dev->stream);
+    hipFree(d);
+    if (e != hipSuccess) return hip_error(e, "tbh_dequantize");
+    return TBH_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,95 @@
+// tbh_internal.h -- shared definitions of libtinybrain_hip (not installed).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <mutex>
+#include <string>
+
+#include "tinybrain_hip.h"
+
+namespace tbh {
+
+// Repacked HBM layouts.  A "chunk" is 16 bytes of one row: 16 INT8 or 32
+// INT4 elements along K, loaded by one lane with one 128-bit load.
+constexpr int kChunkBytes = 16;
+constexpr int kInt8ChunkElems = 16;
+constexpr int kInt4ChunkElems = 32;
+
+// Largest x tile (M * Kp fp32) the VALU GEMV keeps in LDS.
+constexpr int64_t kMaxLdsBytes = 64 * 1024;
+
+enum class Path : int32_t {
+    Int8Row = TBH_PATH_INT8_ROW,
+    Int4KGroup = TBH_PATH_INT4_KGROUP,
+    Int4NGroup = TBH_PATH_INT4_NGROUP,
+    Generic = TBH_PATH_GENERIC,
+};
+
+}  // namespace tbh
+
+struct tbh_device {
+    int32_t ordinal = 0;
+    int32_t cu_count = 0;
+    hipStream_t stream = nullptr;
+    std::mutex mu;               // serialises tbh_matmul / tbh_dequantize
+    void *stage = nullptr;       // device staging for the host-pointer calls
+    size_t stage_bytes = 0;
+};
+
+struct tbh_weight {
+    tbh_device *dev = nullptr;
+    int64_t K = 0, N = 0;
+    int32_t precision = 0, mode = 0, layout = 0, group_size = 0;
+    tbh::Path path = tbh::Path::Generic;
+
+    // fast paths: data [Np][row_bytes], offset-binary values
+    int64_t Kp = 0, Np = 0, row_bytes = 0;
+    uint8_t *data = nullptr;
+    float *scales = nullptr;     // Int8Row [Np]; Int4KGroup [Np][G]; Int4NGroup [NB][Kp]
+    int8_t *zp = nullptr;        // Int8Row [Np]; Int4KGroup [Np][G]; null when all zero
+    int64_t groups_per_row = 1;  // G (Int4KGroup)
+    int32_t chunks_per_group = 1;
+    int32_t rows_per_nblock = 1; // Int4NGroup
+
+    // generic path: the reference arrays as given
+    int8_t *raw = nullptr;
+    int64_t raw_bytes = 0;
+    float *raw_scales = nullptr;
+    int64_t n_scales = 0;
+    int8_t *raw_zp = nullptr;
+
+    int64_t device_bytes = 0;
+    int64_t stream_bytes = 0;
+};
+
+namespace tbh {
+
+// Thread-local error reporting (tbh_api.hip).
+tbh_status set_error(tbh_status st, const std::string &msg);
+tbh_status hip_error(hipError_t e, const char *what);
+
+// Kernel launchers.  All validate nothing: the API layer checks shapes.
+struct GemvArgs {
+    const float *x;
+    int64_t ldx;
+    float *y;
+    int64_t ldy;
+    int64_t M;
+};
+
+// Fast VALU dequant-GEMV for M <= 4 rows of x (tbh_gemv.hip).  Returns
+// hipErrorInvalidValue when the x tile does not fit in LDS.
+hipError_t launch_gemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s);
+// Largest number of x rows one launch_gemv call handles for this weight
+// (0 when the fast path cannot take it).
+int64_t gemv_max_rows(const tbh_weight &w);
+
+// Generic INT4 kernel over the reference flat layout (tbh_ref_kernels.hip).
+hipError_t launch_generic(const tbh_weight &w, const GemvArgs &a, hipStream_t s);
+
+// Bit-exact dequantization to [K, N] row-major (tbh_ref_kernels.hip).
+hipError_t launch_dequant(const tbh_weight &w, float *out, hipStream_t s);
+
+}  // namespace tbh
