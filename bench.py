@@ -188,8 +188,8 @@ def main():
                                  "path": pool[0][j].path}
 
     out = {
-        "metric": "dequant-GEMV GB/s and % of HBM peak (INT4 g32, M=%d, 4 BASELINE shapes)" % M
-        if prec == "int4" else "dequant-GEMV GB/s and % of HBM peak (INT8 per-channel, M=%d)" % M,
+        "metric": (f"dequant-GEMV GB/s and % of HBM peak (INT4 g32, M={M}, 4 BASELINE shapes)"
+                   if prec == "int4" else f"dequant-GEMV GB/s and % of HBM peak (INT8 per-channel, M={M})"),
         "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,

@@ -3,10 +3,15 @@
 // Replaces the MSL kernels matmul_int8_dequant / matmul_int4_dequant
 // (Sources/TinyBrainMetal/Shaders/Dequant.metal:49-79,
 // DequantINT4.metal:95-137), which give each output one thread and walk K
-// with a stride-N load.  Here one wave64 owns R output rows; each lane streams
-// 16-byte chunks of those rows (K-contiguous after the one-time repack) with
-// non-temporal 128-bit loads, so every load instruction moves 1 KiB of
-// contiguous HBM.
+// with a stride-N load.  Here one wave64 owns R output rows at a time; each
+// lane streams 16-byte chunks of those rows (K-contiguous after the one-time
+// repack) with non-temporal 128-bit loads, so every load instruction moves
+// 1 KiB of contiguous HBM.
+//
+// Schedule: the grid is persistent (a few blocks per CU).  A wave walks a
+// sequence of work items -- (row group, chunk iteration) -- and issues the
+// loads of item t+1 before it computes item t, so HBM latency overlaps the
+// unpack/FMA work.  The first item's loads go out before x is staged in LDS.
 //
 // Unpack (per 32-bit word of packed weights, values stored offset-binary):
 //   INT8: (w & 0x00FF00FF) | 0x64006400 is the f16 pair 1024 + (q+128);
@@ -20,6 +25,8 @@
 // product is exactly (q - zp) * x rounded once, as in an fp32 FMA.  Scales
 // are applied once per row (INT8, per-channel), once per 32-element chunk
 // (INT4 K-groups), or folded into x per K element (INT4 runtime layout).
+#include <cstdlib>
+
 #include "tbh_internal.h"
 
 namespace tbh {
@@ -44,6 +51,7 @@ struct KParams {
     int32_t G;       // INT4 K-groups per row
     int32_t cpg;     // chunks per K-group
     int32_t rpn;     // rows per N-block (INT4 runtime layout)
+    int32_t x_vec4;  // x rows are 16-byte aligned and K % 4 == 0
 };
 
 __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
@@ -65,10 +73,76 @@ __device__ __forceinline__ float fmix(_Float16 h, float x, float acc) {
     return __builtin_fmaf((float)h, x, acc);  // v_fma_mix_f32
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
+constexpr int pow2_ceil(int v) { return v <= 1 ? 1 : 2 * pow2_ceil((v + 1) / 2); }
+
+// DPP lane permutations (gfx9 dpp_ctrl codes).
+enum : int {
+    kDppXor1 = 0xB1,         // quad_perm [1,0,3,2]
+    kDppXor2 = 0x4E,         // quad_perm [2,3,0,1]
+    kDppRor8 = 0x128,        // row_ror:8 (= lane ^ 8 inside a 16-lane row)
+    kDppRowMirror = 0x140,   // lane l <- 15 - l within the row
+    kDppHalfMirror = 0x141,  // lane l <- 7 - l within each 8-lane half row
+};
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                                 0xF, 0xF, false));
+}
+
+// Partner value of lane ^ O.
+template <int O>
+__device__ __forceinline__ float xchg(float v) {
+    if constexpr (O == 8) return dpp<kDppRor8>(v);
+    else return __shfl_xor(v, O);
+}
+
+// One transpose-reduce stage over the first CNT values: lanes with bit O set
+// keep the upper half of the values, the others the lower half; each kept
+// value absorbs the partner lane's copy.
+template <int CNT, int O, int V>
+__device__ __forceinline__ void transpose_stages(float (&v)[V], int lane) {
+    if constexpr (CNT > 1) {
+        const bool upper = (lane & O) != 0;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+        for (int i = 0; i < CNT / 2; ++i) {
+            const float send = upper ? v[i] : v[i + CNT / 2];
+            const float keep = upper ? v[i + CNT / 2] : v[i];
+            v[i] = keep + xchg<O>(send);
+        }
+        transpose_stages<CNT / 2, O / 2, V>(v, lane);
+    }
+}
+
+// Plain sum over aligned groups of G lanes (G a power of two), low bits first.
+template <int G>
+__device__ __forceinline__ float group_sum(float r) {
+    if constexpr (G >= 2) r += dpp<kDppXor1>(r);
+    if constexpr (G >= 4) r += dpp<kDppXor2>(r);
+    if constexpr (G >= 8) r += dpp<kDppHalfMirror>(r);   // quads already reduced
+    if constexpr (G >= 16) r += dpp<kDppRowMirror>(r);   // halves already reduced
+    if constexpr (G >= 32) r += __shfl_xor(r, 16);
+    if constexpr (G >= 64) r += __shfl_xor(r, 32);
+    return r;
+}
+
+// Sums V (a power of two <= 32) per-lane values over the 64 lanes of a wave
+// with a transpose-reduce: each exchange stage halves the number of values a
+// lane carries, so the cost is about V exchanges instead of 6 V.  Afterwards
+// every lane holds the total of value index
+// sum_s bit(lane, 5 - s) * (V >> (s + 1)), s = 0 .. log2(V) - 1.
+template <int V>
+__device__ __forceinline__ float reduce_multi(float (&v)[V], int lane) {
+    transpose_stages<V, 32, V>(v, lane);
+    return group_sum<64 / V>(v[0]);
+}
+
+template <int V>
+__device__ __forceinline__ int reduce_index(int lane) {
+    int idx = 0;
+#pragma unroll
+    for (int s = 0, cnt = V; cnt > 1; ++s, cnt >>= 1) idx += ((lane >> (5 - s)) & 1) * (cnt / 2);
+    return idx;
 }
 
 // LDS slot of x element k: chunks are padded by 4 floats so that the
@@ -78,94 +152,153 @@ __device__ __forceinline__ int lds_index(int k) {
     return (k / CE) * (CE + 4) + (k % CE);
 }
 
+template <int PREC, int M, bool VEC4>
+__device__ __forceinline__ void stage_x_round(const KParams &p, float4 *xs4, int lds_row, int tid,
+                                              int base) {
+    constexpr int CE = PREC == 8 ? 16 : 32;
+    constexpr int XU = 4;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        const float *xr = p.x + (int64_t)m * p.ldx;
+        float4 v[XU];
+#pragma unroll
+        for (int u = 0; u < XU; ++u) {
+            const int k = 4 * (base + u * 256 + tid);
+            if constexpr (VEC4) {
+                const float4 t = *(const float4 *)(xr + min(k, p.K - 4));
+                const bool in = k < p.K;
+                v[u] = float4{in ? t.x : 0.f, in ? t.y : 0.f, in ? t.z : 0.f, in ? t.w : 0.f};
+            } else {
+                const float a0 = xr[min(k, p.K - 1)], a1 = xr[min(k + 1, p.K - 1)];
+                const float a2 = xr[min(k + 2, p.K - 1)], a3 = xr[min(k + 3, p.K - 1)];
+                v[u] = float4{k < p.K ? a0 : 0.f, k + 1 < p.K ? a1 : 0.f,
+                              k + 2 < p.K ? a2 : 0.f, k + 3 < p.K ? a3 : 0.f};
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < XU; ++u) {
+            const int k = 4 * (base + u * 256 + tid);
+            if (k < p.Kp) {
+                float4 t = v[u];
+                if (PREC == 4) { t.z *= 0.0625f; t.w *= 0.0625f; }
+                xs4[(m * lds_row + lds_index<CE>(k)) >> 2] = t;
+            }
+        }
+    }
+}
+
+// Stages x [M][Kp] into LDS: zero beyond K, INT4 slots k % 4 in {2, 3}
+// pre-divided by 16.  Each thread issues its loads of a round (4 float4 per
+// row, on clamped always-in-bounds addresses, zeroed afterwards by selects)
+// before it waits, so staging costs one L2 round trip for Kp <= 4096.  The
+// first round is peeled out of the loop so the compiler does not wait for
+// the weight loads already in flight.
+template <int PREC, int M, bool VEC4>
+__device__ __forceinline__ void stage_x(const KParams &p, float4 *xs4, int lds_row, int tid) {
+    const int k4n = p.Kp >> 2;  // float4 slots per x row
+    stage_x_round<PREC, M, VEC4>(p, xs4, lds_row, tid, 0);
+    if (k4n > 1024) {
+        for (int base = 1024; base < k4n; base += 1024)
+            stage_x_round<PREC, M, VEC4>(p, xs4, lds_row, tid, base);
+    }
+}
+
 template <int PREC, int SM, int M, int R, bool ZP>
 __global__ __launch_bounds__(256) void gemv_valu(const KParams p) {
     constexpr int CE = PREC == 8 ? 16 : 32;  // elements per 16-byte chunk
     constexpr int CS = CE + 4;               // padded LDS floats per chunk
-    extern __shared__ float4 xs4[];  // float4-typed so that x reads are ds_read_b128
+    constexpr int V = pow2_ceil(M * R);      // values per lane to reduce
+    extern __shared__ float4 xs4[];          // float4-typed: x reads are ds_read_b128
     float *xs = reinterpret_cast<float *>(xs4);
-    const int tid = threadIdx.x;
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int GW = gridDim.x * 4;
+    const int gw = blockIdx.x * 4 + wave;
+    const int nrg = p.Np / R;
+    const int iters = (p.chunks + 63) >> 6;  // chunk iterations per row group
+    const int items = gw < nrg ? ((nrg - gw + GW - 1) / GW) * iters : 0;
     const int lds_row = p.chunks * CS;
 
-    // stage x [M][Kp] into LDS (zero beyond K; INT4 16x slots pre-divided)
-    for (int m = 0; m < M; ++m) {
-        const float *xr = p.x + (int64_t)m * p.ldx;
-        for (int k = tid; k < p.Kp; k += 256) {
-            float v = k < p.K ? xr[k] : 0.0f;
-            if (PREC == 4 && (k & 2)) v *= 0.0625f;
-            xs[m * lds_row + lds_index<CE>(k)] = v;
+    // ---- weight (and K-group scale) loads of one work item
+    u32x4 wc[R], wn[R];
+    float sc[R], sn[R], zc[R], zn[R];
+    auto load_item = [&](int t, u32x4 (&w)[R], float (&s)[R], float (&z)[R]) {
+        const int rg = gw + (t / iters) * GW;
+        int c = lane + 64 * (t % iters);
+        c = c < p.chunks ? c : p.chunks - 1;  // idle lanes re-read a valid chunk
+        const uint8_t *base = p.data + (int64_t)rg * R * p.row_bytes + (int64_t)c * 16;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            w[r] = __builtin_nontemporal_load((const u32x4 *)(base + (int64_t)r * p.row_bytes));
+        if (SM == S_KGROUP) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int64_t gi = (int64_t)(rg * R + r) * p.G + c / p.cpg;
+                s[r] = p.scales[gi];
+                z[r] = ZP ? (float)p.zp[gi] : 0.0f;
+            }
         }
-    }
+    };
+    if (items > 0) load_item(0, wc, sc, zc);
+
+    // ---- stage x [M][Kp] into LDS (zero beyond K; INT4 16x slots pre-divided).
+    if (p.x_vec4) stage_x<PREC, M, true>(p, xs4, lds_row, tid);
+    else stage_x<PREC, M, false>(p, xs4, lds_row, tid);
     __syncthreads();
 
-    const int wave = tid >> 6, lane = tid & 63;
-    const int nrg = p.Np / R;
     const uint32_t kMagic = 0x64006400u;
     const uint32_t kLo = PREC == 8 ? 0x00FF00FFu : 0x000F000Fu;
     const uint32_t kHi = 0x00F000F0u;
 
-    for (int rg = blockIdx.x * 4 + wave; rg < nrg; rg += gridDim.x * 4) {
+    float acc[M][R];
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
+
+    for (int t = 0; t < items; ++t) {
+        if (t + 1 < items) load_item(t + 1, wn, sn, zn);
+        const int rg = gw + (t / iters) * GW;
         const int n0 = rg * R;
-        float acc[M][R];
-#pragma unroll
-        for (int m = 0; m < M; ++m)
-#pragma unroll
-            for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
+        const int c = lane + 64 * (t % iters);
 
-        // per-row offset constants (INT8 row zero points)
-        h2 c8[R];
-        if (PREC == 8) {
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-                c8[r] = splat(-(1152.0f + (ZP ? (float)p.zp[n0 + r] : 0.0f)));
-        }
-        const float *tcol = nullptr;  // INT4 runtime layout: per-k scales of this N-block
-        if (SM == S_NGROUP) tcol = p.scales + (int64_t)(n0 / p.rpn) * p.Kp;
-
-        for (int c = lane; c < p.chunks; c += 64) {
-            u32x4 w[R];
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-                w[r] = __builtin_nontemporal_load(
-                    (const u32x4 *)(p.data + (int64_t)(n0 + r) * p.row_bytes + (int64_t)c * 16));
-
+        if (c < p.chunks) {
             if (PREC == 8) {
+                h2 c8[R];
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+                    c8[r] = splat(-(1152.0f + (ZP ? (float)p.zp[n0 + r] : 0.0f)));
 #pragma unroll
                 for (int d = 0; d < 4; ++d) {
                     float4 xv[M];
 #pragma unroll
-                    for (int m = 0; m < M; ++m)
-                        xv[m] = xs4[(m * lds_row + c * CS + 4 * d) >> 2];
+                    for (int m = 0; m < M; ++m) xv[m] = xs4[(m * lds_row + c * CS + 4 * d) >> 2];
 #pragma unroll
                     for (int r = 0; r < R; ++r) {
-                        const uint32_t wv = w[r][d];
-                        h2 p0 = as_h2(and_or(wv, kLo, kMagic)) + c8[r];
-                        h2 p1 = as_h2(and_or(wv >> 8, kLo, kMagic)) + c8[r];
+                        const uint32_t wv = wc[r][d];
+                        const h2 p0 = as_h2(and_or(wv, kLo, kMagic)) + c8[r];
+                        const h2 p1 = as_h2(and_or(wv >> 8, kLo, kMagic)) + c8[r];
 #pragma unroll
                         for (int m = 0; m < M; ++m) {
-                            float t = acc[m][r];
-                            t = fmix(p0.x, xv[m].x, t);
-                            t = fmix(p0.y, xv[m].y, t);
-                            t = fmix(p1.x, xv[m].z, t);
-                            t = fmix(p1.y, xv[m].w, t);
-                            acc[m][r] = t;
+                            float a = acc[m][r];
+                            a = fmix(p0.x, xv[m].x, a);
+                            a = fmix(p0.y, xv[m].y, a);
+                            a = fmix(p1.x, xv[m].z, a);
+                            a = fmix(p1.y, xv[m].w, a);
+                            acc[m][r] = a;
                         }
                     }
                 }
             } else {
                 h2 c1[R], c16[R];
-                float s[R];
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
-                    float z = 0.0f;
-                    if (SM == S_KGROUP) {
-                        const int64_t gi = (int64_t)(n0 + r) * p.G + c / p.cpg;
-                        s[r] = p.scales[gi];
-                        if (ZP) z = (float)p.zp[gi];
-                    }
+                    const float z = (SM == S_KGROUP && ZP) ? zc[r] : 0.0f;
                     c1[r] = splat(-(1032.0f + z));
                     c16[r] = splat(-(1152.0f + 16.0f * z));
                 }
+                const float *tcol = nullptr;  // runtime layout: per-k scales of this N-block
+                if (SM == S_NGROUP) tcol = p.scales + (int64_t)(n0 / p.rpn) * p.Kp + c * 32;
                 float part[M][R];
 #pragma unroll
                 for (int m = 0; m < M; ++m)
@@ -180,8 +313,8 @@ __global__ __launch_bounds__(256) void gemv_valu(const KParams p) {
                         xb[m] = xs4[(m * lds_row + c * CS + 8 * d + 4) >> 2];
                     }
                     if (SM == S_NGROUP) {
-                        const float4 ta = *(const float4 *)&tcol[c * 32 + 8 * d];
-                        const float4 tb = *(const float4 *)&tcol[c * 32 + 8 * d + 4];
+                        const float4 ta = *(const float4 *)&tcol[8 * d];
+                        const float4 tb = *(const float4 *)&tcol[8 * d + 4];
 #pragma unroll
                         for (int m = 0; m < M; ++m) {
                             xa[m].x *= ta.x; xa[m].y *= ta.y; xa[m].z *= ta.z; xa[m].w *= ta.w;
@@ -190,54 +323,60 @@ __global__ __launch_bounds__(256) void gemv_valu(const KParams p) {
                     }
 #pragma unroll
                     for (int r = 0; r < R; ++r) {
-                        const uint32_t wv = w[r][d];
+                        const uint32_t wv = wc[r][d];
                         const uint32_t w8 = wv >> 8;
-                        h2 p0 = as_h2(and_or(wv, kLo, kMagic)) + c1[r];
-                        h2 p1 = as_h2(and_or(wv, kHi, kMagic)) + c16[r];
-                        h2 p2 = as_h2(and_or(w8, kLo, kMagic)) + c1[r];
-                        h2 p3 = as_h2(and_or(w8, kHi, kMagic)) + c16[r];
+                        const h2 p0 = as_h2(and_or(wv, kLo, kMagic)) + c1[r];
+                        const h2 p1 = as_h2(and_or(wv, kHi, kMagic)) + c16[r];
+                        const h2 p2 = as_h2(and_or(w8, kLo, kMagic)) + c1[r];
+                        const h2 p3 = as_h2(and_or(w8, kHi, kMagic)) + c16[r];
 #pragma unroll
                         for (int m = 0; m < M; ++m) {
-                            float t = (SM == S_KGROUP) ? part[m][r] : acc[m][r];
-                            t = fmix(p0.x, xa[m].x, t);
-                            t = fmix(p0.y, xa[m].y, t);
-                            t = fmix(p1.x, xa[m].z, t);
-                            t = fmix(p1.y, xa[m].w, t);
-                            t = fmix(p2.x, xb[m].x, t);
-                            t = fmix(p2.y, xb[m].y, t);
-                            t = fmix(p3.x, xb[m].z, t);
-                            t = fmix(p3.y, xb[m].w, t);
-                            if (SM == S_KGROUP) part[m][r] = t;
-                            else acc[m][r] = t;
+                            float a = part[m][r];
+                            a = fmix(p0.x, xa[m].x, a);
+                            a = fmix(p0.y, xa[m].y, a);
+                            a = fmix(p1.x, xa[m].z, a);
+                            a = fmix(p1.y, xa[m].w, a);
+                            a = fmix(p2.x, xb[m].x, a);
+                            a = fmix(p2.y, xb[m].y, a);
+                            a = fmix(p3.x, xb[m].z, a);
+                            a = fmix(p3.y, xb[m].w, a);
+                            part[m][r] = a;
                         }
                     }
                 }
-                if (SM == S_KGROUP) {
 #pragma unroll
-                    for (int m = 0; m < M; ++m)
+                for (int m = 0; m < M; ++m)
 #pragma unroll
-                        for (int r = 0; r < R; ++r) acc[m][r] = __builtin_fmaf(s[r], part[m][r], acc[m][r]);
-                }
+                    for (int r = 0; r < R; ++r)
+                        acc[m][r] = SM == S_KGROUP ? __builtin_fmaf(sc[r], part[m][r], acc[m][r])
+                                                   : acc[m][r] + part[m][r];
             }
         }
 
-        // reduce across the wave and write
+        if (t % iters == iters - 1) {
+            // row group done: reduce across the wave and write
+            float v[V];
 #pragma unroll
-        for (int m = 0; m < M; ++m)
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                float v = wave_sum(acc[m][r]);
-                const int n = n0 + r;
-                if (lane == 0 && n < p.N) {
-                    if (SM == S_ROW) v *= p.scales[n];
-                    p.y[(int64_t)m * p.ldy + n] = v;
-                }
+            for (int i = 0; i < V; ++i) v[i] = i < M * R ? acc[i / R][i % R] : 0.0f;
+            const float tot = reduce_multi<V>(v, lane);
+            const int idx = reduce_index<V>(lane);
+            if ((lane & (64 / V - 1)) == 0 && idx < M * R) {
+                const int m = idx / R, n = n0 + idx % R;
+                if (n < p.N) p.y[(int64_t)m * p.ldy + n] = SM == S_ROW ? tot * p.scales[n] : tot;
             }
+#pragma unroll
+            for (int m = 0; m < M; ++m)
+#pragma unroll
+                for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            wc[r] = wn[r];
+            sc[r] = sn[r];
+            zc[r] = zn[r];
+        }
     }
 }
-
-template <int PREC>
-constexpr int chunk_elems() { return PREC == 8 ? kInt8ChunkElems : kInt4ChunkElems; }
 
 int64_t lds_bytes_for(const tbh_weight &w, int64_t M) {
     const int ce = w.precision == TBH_PREC_INT8 ? kInt8ChunkElems : kInt4ChunkElems;
@@ -274,6 +413,11 @@ hipError_t dispatch_m(int M, int R, const KParams &p, int blocks, size_t lds, hi
     }
 }
 
+int env_int(const char *name, int dflt) {
+    const char *v = std::getenv(name);
+    return v && *v ? std::atoi(v) : dflt;
+}
+
 }  // namespace
 
 int64_t gemv_max_rows(const tbh_weight &w) {
@@ -307,17 +451,24 @@ hipError_t launch_gemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s) {
     p.G = (int32_t)w.groups_per_row;
     p.cpg = w.chunks_per_group;
     p.rpn = w.rows_per_nblock;
+    p.x_vec4 = (w.K % 4 == 0 && a.ldx % 4 == 0 && ((uintptr_t)a.x & 15) == 0) ? 1 : 0;
 
-    // Rows per wave: as many as keep >= 8 waves per CU busy, within the
-    // register budget (M*R <= 16) and dividing the N-block height.
-    const int64_t target_waves = 8LL * std::max(1, w.dev->cu_count);
+    // Persistent grid: a few 4-wave blocks per CU.  Rows per wave (R): as
+    // many as still give every wave work, within the register budget
+    // (M*R <= 16) and dividing the N-block height of the runtime layout.
+    static const int bpc = env_int("TBH_GEMV_BLOCKS_PER_CU", 2);
+    static const int r_force = env_int("TBH_GEMV_ROWS", 0);
+    const int64_t cus = std::max(1, w.dev->cu_count);
+    const int64_t max_blocks = bpc * cus;
     int R = 8;
-    while (R > 1 && (w.Np / R < target_waves || M * R > 16 ||
+    while (R > 1 && (w.Np / R < 4 * max_blocks || M * R > 16 ||
                      (w.path == Path::Int4NGroup && p.rpn % R != 0) || (M > 2 && R > 4)))
         R /= 2;
-    const int64_t waves = w.Np / R;
-    const int64_t max_blocks = 8LL * std::max(1, w.dev->cu_count);
-    const int blocks = (int)std::max<int64_t>(1, std::min((waves + 3) / 4, max_blocks));
+    if (r_force > 0 && M * r_force <= 16 && !(M > 2 && r_force > 4) && w.Np % r_force == 0 &&
+        !(w.path == Path::Int4NGroup && p.rpn % r_force != 0))
+        R = r_force;
+    const int64_t groups = w.Np / R;
+    const int blocks = (int)std::max<int64_t>(1, std::min((groups + 3) / 4, max_blocks));
     const bool zp = w.zp != nullptr;
 
     switch (w.path) {
