@@ -247,3 +247,62 @@ def test_device_resident_entry_point(backend):
     deq = backend.dequantize_device(w)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(deq.cpu().numpy().view(np.uint32), W.view(np.uint32))
+
+
+# ---------------------------------------------------------------------------
+# both HBM layouts: K-contiguous rows (VALU GEMV, default) and 1 KiB MFMA
+# tiles (MFMA GEMV, TBH_LAYOUT=tiles)
+# ---------------------------------------------------------------------------
+@pytest.fixture
+def tile_layout(monkeypatch):
+    monkeypatch.setenv("TBH_LAYOUT", "tiles")
+    yield
+
+
+@pytest.mark.parametrize("K,N", [(2048, 512), (100, 37), (5632, 64), (2048, 5632)])
+def test_int8_tile_layout(backend, tile_layout, K, N):
+    qt = _int8_pc(K + 3 * N, K, N)
+    _check(backend, _product(qt, (K, N)), qt, Ms=(1, 2, 3, 4, 5, 8))
+
+
+@pytest.mark.parametrize("K,N,gs", [(2048, 512, 32), (256, 40, 64), (100, 9, 0), (5632, 48, 32),
+                                    (2048, 32000, 32), (48, 10, 48)])
+def test_int4_tile_layout(backend, tile_layout, K, N, gs):
+    qt = _int4_nk(K + N + gs + 1, K, N, gs if gs else K * N)
+    if gs == 0:
+        qt.group_size = 0
+    _check(backend, _product(qt, (K, N), T.Layout.NK_FLAT), qt, Ms=(1, 2, 3, 4, 5, 8))
+
+
+def test_tile_layout_zero_points(backend, tile_layout):
+    qt = _int4_nk(93, 256, 24, 32)
+    qt.zero_points = ((np.arange(qt.scales.size) % 7) - 3).astype(np.int8)
+    _check(backend, _product(qt, (256, 24), T.Layout.NK_FLAT), qt, Ms=(1, 3, 8))
+    q8 = _int8_pc(94, 192, 40)
+    q8.zero_points = ((np.arange(40) % 9) - 4).astype(np.int8)
+    _check(backend, _product(q8, (192, 40)), q8, Ms=(1, 4, 8))
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 6, 7, 8, 9, 16])
+def test_mfma_every_m(backend, tile_layout, M):
+    qt = _int4_nk(300 + M, 1024, 96, 32)
+    _check(backend, _product(qt, (1024, 96), T.Layout.NK_FLAT), qt, Ms=(M,))
+    q8 = _int8_pc(400 + M, 640, 80)
+    _check(backend, _product(q8, (640, 80)), q8, Ms=(M,))
+
+
+def test_x_range_extremes(backend, tile_layout):
+    # per-row power-of-two rescaling keeps huge and tiny activations exact
+    qt = _int4_nk(501, 512, 64, 32)
+    pq = _product(qt, (512, 64), T.Layout.NK_FLAT)
+    W = _oracle_weight(qt, T.Layout.NK_FLAT)
+    x = O.fill_normal(502, 4 * 512).reshape(4, 512)
+    x[0] *= 1e6
+    x[1] *= 1e-7
+    x[2, ::3] = 0.0
+    x[3, :] = 0.0
+    y = backend.matmulQuantized(x, pq)
+    y64 = O.gemm_f64(x, W)
+    for m in range(3):
+        assert O.parity_errors(y[m:m + 1], y64[m:m + 1])["gated"] <= GATE, m
+    assert np.all(y[3] == 0.0)

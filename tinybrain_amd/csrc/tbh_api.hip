@@ -3,6 +3,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <thread>
@@ -266,6 +267,71 @@ void pack_int4_rows(const std::vector<int8_t> &q, int64_t K, int64_t N, int64_t 
     });
 }
 
+// MFMA tiles (INT8): 1 KiB per (16-row tile rt, 64-element K tile sc).  Lane
+// l's 16 bytes are 4 words; words 2j and 2j+1 hold the 8 elements
+// k = 64 sc + 32 j + 8 (l / 16) + e of row 16 rt + l % 16, 4 per word at byte
+// positions {0, 2, 1, 3}, value q + 128.
+void pack_int8_tiles(const std::vector<int8_t> &q, int64_t K, int64_t N, int64_t Kp, int64_t Np,
+                     std::vector<uint8_t> &out) {
+    static const int bp[4] = {0, 2, 1, 3};
+    const int64_t SC = Kp / kMfmaInt8TileK, ntiles = Np / 16;
+    out.assign((size_t)(ntiles * SC * 1024), 0x80);
+    parallel_for(ntiles, [&](int64_t lo, int64_t hi) {
+        for (int64_t rt = lo; rt < hi; ++rt)
+            for (int64_t sc = 0; sc < SC; ++sc) {
+                uint8_t *tile = out.data() + (rt * SC + sc) * 1024;
+                for (int l = 0; l < 64; ++l) {
+                    const int64_t n = rt * 16 + (l & 15);
+                    if (n >= N) continue;
+                    const int8_t *qr = q.data() + n * K;
+                    for (int d = 0; d < 4; ++d)
+                        for (int e4 = 0; e4 < 4; ++e4) {
+                            const int64_t k = sc * 64 + 32 * (d >> 1) + 8 * (l >> 4) + 4 * (d & 1) + e4;
+                            if (k < K) tile[16 * l + 4 * d + bp[e4]] = (uint8_t)((int)qr[k] + 128);
+                        }
+                }
+            }
+    });
+}
+
+// MFMA tiles (INT4): 1 KiB per (16-row tile rt, 128-element K tile sc).  Lane
+// l's word j holds the 8 elements k = 128 sc + 32 j + 8 (l / 16) + e of row
+// 16 rt + l % 16 as nibbles q + 8 at bit offsets {0, 16, 4, 20, 8, 24, 12, 28}.
+void pack_int4_tiles(const std::vector<int8_t> &q, int64_t K, int64_t N, int64_t Kp, int64_t Np,
+                     std::vector<uint8_t> &out) {
+    static const int nb[8] = {0, 16, 4, 20, 8, 24, 12, 28};
+    const int64_t SC = Kp / kMfmaInt4TileK, ntiles = Np / 16;
+    out.assign((size_t)(ntiles * SC * 1024), 0x88);
+    parallel_for(ntiles, [&](int64_t lo, int64_t hi) {
+        for (int64_t rt = lo; rt < hi; ++rt)
+            for (int64_t sc = 0; sc < SC; ++sc) {
+                uint32_t *tile = reinterpret_cast<uint32_t *>(out.data() + (rt * SC + sc) * 1024);
+                for (int l = 0; l < 64; ++l) {
+                    const int64_t n = rt * 16 + (l & 15);
+                    if (n >= N) continue;
+                    const int8_t *qr = q.data() + n * K;
+                    for (int j = 0; j < 4; ++j) {
+                        uint32_t word = 0;
+                        for (int e = 0; e < 8; ++e) {
+                            const int64_t k = sc * 128 + 32 * j + 8 * (l >> 4) + e;
+                            const int v = k < K ? qr[k] : 0;
+                            word |= (uint32_t)((v + 8) & 0xF) << nb[e];
+                        }
+                        tile[4 * l + j] = word;
+                    }
+                }
+            }
+    });
+}
+
+// HBM layout of new weights: K-contiguous rows for the VALU GEMV (default,
+// fastest measured for decode, M = 1) or, with TBH_LAYOUT=tiles, 1 KiB MFMA
+// tiles for the MFMA GEMV.
+bool use_row_layout() {
+    const char *v = std::getenv("TBH_LAYOUT");
+    return !(v && std::strcmp(v, "tiles") == 0);
+}
+
 bool any_nonzero(const int8_t *p, int64_t n) {
     if (!p) return false;
     for (int64_t i = 0; i < n; ++i)
@@ -274,11 +340,12 @@ bool any_nonzero(const int8_t *p, int64_t n) {
 }
 
 template <class T>
-hipError_t upload(T **dst, const T *src, size_t count, int64_t &bytes) {
+hipError_t upload(T **dst, const T *src, size_t count, int64_t &bytes, int64_t &n_out) {
     size_t nbytes = std::max<size_t>(count * sizeof(T), 1);
     hipError_t e = hipMalloc((void **)dst, nbytes);
     if (e != hipSuccess) return e;
     bytes += (int64_t)(count * sizeof(T));
+    n_out = (int64_t)count;
     return hipMemcpy(*dst, src, count * sizeof(T), hipMemcpyHostToDevice);
 }
 
@@ -321,12 +388,19 @@ tbh_status tbh_weight_create(tbh_device *dev, const tbh_qtensor_desc *desc, tbh_
 
     if (d.precision == TBH_PREC_INT8) {
         w->path = Path::Int8Row;
-        w->Kp = round_up(K, kInt8ChunkElems);
-        w->Np = round_up(N, 8);
-        w->row_bytes = w->Kp;
+        w->mfma_tiles = !use_row_layout();
         std::vector<int8_t> q = expand_nk(d);
         std::vector<uint8_t> packed;
-        pack_int8_rows(q, K, N, w->Kp, w->Np, packed);
+        if (w->mfma_tiles) {
+            w->Kp = round_up(K, kMfmaInt8TileK);
+            w->Np = round_up(N, 16);
+            pack_int8_tiles(q, K, N, w->Kp, w->Np, packed);
+        } else {
+            w->Kp = round_up(K, kInt8ChunkElems);
+            w->Np = round_up(N, 8);
+            w->row_bytes = w->Kp;
+            pack_int8_rows(q, K, N, w->Kp, w->Np, packed);
+        }
         std::vector<float> s((size_t)w->Np, 0.0f);
         std::vector<int8_t> z((size_t)w->Np, 0);
         const bool per_ch = d.mode == TBH_MODE_PER_CHANNEL;
@@ -334,9 +408,9 @@ tbh_status tbh_weight_create(tbh_device *dev, const tbh_qtensor_desc *desc, tbh_
             s[n] = d.scales[per_ch ? n : 0];
             if (d.zero_points) z[n] = d.zero_points[per_ch ? n : 0];
         }
-        e = upload(&w->data, packed.data(), packed.size(), w->device_bytes);
-        if (e == hipSuccess) e = upload(&w->scales, s.data(), s.size(), w->device_bytes);
-        if (e == hipSuccess && has_zp) e = upload(&w->zp, z.data(), z.size(), w->device_bytes);
+        e = upload(&w->data, packed.data(), packed.size(), w->device_bytes, w->n_data);
+        if (e == hipSuccess) e = upload(&w->scales, s.data(), s.size(), w->device_bytes, w->n_scales_dev);
+        if (e == hipSuccess && has_zp) e = upload(&w->zp, z.data(), z.size(), w->device_bytes, w->n_zp_dev);
         w->stream_bytes = K * N + 4 * N + (has_zp ? N : 0);
     } else {
         const int64_t gs = d.group_size > 0 ? d.group_size : count;
@@ -360,14 +434,53 @@ tbh_status tbh_weight_create(tbh_device *dev, const tbh_qtensor_desc *desc, tbh_
                 else if (gs % N == 0) { ngroup = true; rpn = 0; }
             }
         }
-        if (kgroup || ngroup) {
+        if (kgroup && !use_row_layout()) {
+            // MFMA tiles; per-row scale when one group spans the row, else one
+            // scale (and zero point) per (row, 32-element chunk) in tile order
+            w->path = Path::Int4KGroup;
+            w->mfma_tiles = true;
+            w->Kp = round_up(K, kMfmaInt4TileK);
+            w->Np = round_up(N, 16);
+            const int64_t G = seg ? K / seg : 1;
+            w->groups_per_row = G;
+            w->chunks_per_group = (int32_t)(seg ? seg / kInt4ChunkElems : w->Kp / kInt4ChunkElems);
+            std::vector<int8_t> q = expand_nk(d);
+            std::vector<uint8_t> packed;
+            pack_int4_tiles(q, K, N, w->Kp, w->Np, packed);
+            e = upload(&w->data, packed.data(), packed.size(), w->device_bytes, w->n_data);
+            std::vector<float> s;
+            std::vector<int8_t> z;
+            if (G == 1) {
+                s.assign((size_t)w->Np, 0.0f);
+                z.assign((size_t)w->Np, 0);
+                for (int64_t n = 0; n < N; ++n) {
+                    const int64_t gi = group_of(0, n);
+                    s[n] = d.scales[gi];
+                    if (d.zero_points) z[n] = d.zero_points[gi];
+                }
+            } else {
+                const int64_t SC = w->Kp / kMfmaInt4TileK, ntiles = w->Np / 16;
+                s.assign((size_t)(ntiles * SC * 64), 0.0f);
+                z.assign((size_t)(ntiles * SC * 64), 0);
+                for (int64_t n = 0; n < N; ++n)
+                    for (int64_t c = 0; c < K / kInt4ChunkElems; ++c) {
+                        const int64_t gi = group_of(c * kInt4ChunkElems, n);
+                        const int64_t at = (((n / 16) * SC + c / 4) * 16 + n % 16) * 4 + c % 4;
+                        s[at] = d.scales[gi];
+                        if (d.zero_points) z[at] = d.zero_points[gi];
+                    }
+            }
+            if (e == hipSuccess) e = upload(&w->scales, s.data(), s.size(), w->device_bytes, w->n_scales_dev);
+            if (e == hipSuccess && has_zp) e = upload(&w->zp, z.data(), z.size(), w->device_bytes, w->n_zp_dev);
+            w->stream_bytes = (count + 1) / 2 + 4 * N * G + (has_zp ? N * G : 0);
+        } else if (kgroup || ngroup) {
             w->Kp = round_up(K, kInt4ChunkElems);
             w->Np = round_up(N, 8);
             w->row_bytes = w->Kp / 2;
             std::vector<int8_t> q = expand_nk(d);
             std::vector<uint8_t> packed;
             pack_int4_rows(q, K, N, w->Kp, w->Np, packed);
-            e = upload(&w->data, packed.data(), packed.size(), w->device_bytes);
+            e = upload(&w->data, packed.data(), packed.size(), w->device_bytes, w->n_data);
             if (kgroup) {
                 w->path = Path::Int4KGroup;
                 const int64_t G = seg ? K / seg : 1;
@@ -381,8 +494,8 @@ tbh_status tbh_weight_create(tbh_device *dev, const tbh_qtensor_desc *desc, tbh_
                         s[n * G + g] = d.scales[gi];
                         if (d.zero_points) z[n * G + g] = d.zero_points[gi];
                     }
-                if (e == hipSuccess) e = upload(&w->scales, s.data(), s.size(), w->device_bytes);
-                if (e == hipSuccess && has_zp) e = upload(&w->zp, z.data(), z.size(), w->device_bytes);
+                if (e == hipSuccess) e = upload(&w->scales, s.data(), s.size(), w->device_bytes, w->n_scales_dev);
+                if (e == hipSuccess && has_zp) e = upload(&w->zp, z.data(), z.size(), w->device_bytes, w->n_zp_dev);
                 w->stream_bytes = (count + 1) / 2 + 4 * N * G + (has_zp ? N * G : 0);
             } else {
                 w->path = Path::Int4NGroup;
@@ -394,21 +507,23 @@ tbh_status tbh_weight_create(tbh_device *dev, const tbh_qtensor_desc *desc, tbh_
                     if (nb * w->rows_per_nblock >= N) continue;
                     for (int64_t k = 0; k < K; ++k) t[nb * w->Kp + k] = d.scales[group_of(k, n)];
                 }
-                if (e == hipSuccess) e = upload(&w->scales, t.data(), t.size(), w->device_bytes);
+                if (e == hipSuccess) e = upload(&w->scales, t.data(), t.size(), w->device_bytes, w->n_scales_dev);
                 w->stream_bytes = (count + 1) / 2 + 4 * d.n_scales;
             }
         } else {
             w->path = Path::Generic;
             w->raw_bytes = d.data_bytes;
             w->n_scales = d.n_scales;
-            e = upload(&w->raw, d.data, (size_t)d.data_bytes, w->device_bytes);
-            if (e == hipSuccess) e = upload(&w->raw_scales, d.scales, (size_t)d.n_scales, w->device_bytes);
+            e = upload(&w->raw, d.data, (size_t)d.data_bytes, w->device_bytes, w->n_raw);
+            if (e == hipSuccess) e = upload(&w->raw_scales, d.scales, (size_t)d.n_scales, w->device_bytes, w->n_raw_scales);
             if (e == hipSuccess && has_zp)
-                e = upload(&w->raw_zp, d.zero_points, (size_t)d.n_scales, w->device_bytes);
+                e = upload(&w->raw_zp, d.zero_points, (size_t)d.n_scales, w->device_bytes, w->n_raw_zp);
             w->stream_bytes = d.data_bytes + 4 * d.n_scales + (has_zp ? d.n_scales : 0);
         }
     }
     if (e != hipSuccess) return hip_error(e, "tbh_weight_create: upload");
+    if (!weight_arrays_ok(*w))
+        return set_error(TBH_E_INVALID, "tbh_weight_create: internal layout inconsistency");
     *out = w.release();
     return TBH_OK;
 }
@@ -435,16 +550,66 @@ tbh_status tbh_weight_get_info(const tbh_weight *w, tbh_weight_info *info) {
     return TBH_OK;
 }
 
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// device-array consistency (checked before every launch)
+// ---------------------------------------------------------------------------
+namespace tbh {
+bool weight_arrays_ok(const tbh_weight &w) {
+    if (w.K <= 0 || w.N <= 0) return false;
+    const bool int4 = w.precision == TBH_PREC_INT4;
+    auto zp_ok = [&](int64_t want) { return w.zp == nullptr ? w.n_zp_dev == 0 : w.n_zp_dev == want; };
+    if (w.path == Path::Generic) {
+        const int64_t cnt = w.K * w.N;
+        const int64_t gs = w.group_size > 0 ? w.group_size : cnt;
+        const int64_t groups = (cnt + gs - 1) / gs;
+        return int4 && w.raw && w.raw_scales && w.n_raw == (cnt + 1) / 2 && w.n_raw_scales == groups &&
+               (w.raw_zp == nullptr || w.n_raw_zp == groups);
+    }
+    if (!w.data || !w.scales || w.Kp < w.K || w.Np < w.N) return false;
+    if (w.mfma_tiles) {
+        const int64_t tk = int4 ? kMfmaInt4TileK : kMfmaInt8TileK;
+        if (w.Kp % tk || w.Np % 16) return false;
+        const int64_t tiles = (w.Np / 16) * (w.Kp / tk);
+        if (w.n_data != tiles * 1024) return false;
+        const int64_t ns = (int4 && w.groups_per_row > 1) ? tiles * 64 : w.Np;
+        if (int4 && w.groups_per_row > 1 && w.Kp / kInt4ChunkElems < w.groups_per_row) return false;
+        return w.n_scales_dev == ns && zp_ok(ns);
+    }
+    if (!int4) return w.n_data == w.Np * w.Kp && w.row_bytes == w.Kp && w.n_scales_dev == w.Np && zp_ok(w.Np);
+    if (w.n_data != w.Np * w.Kp / 2 || w.row_bytes != w.Kp / 2 || w.Kp % kInt4ChunkElems) return false;
+    if (w.path == Path::Int4KGroup) {
+        const int64_t chunks = w.Kp / kInt4ChunkElems;
+        return w.groups_per_row >= 1 && (int64_t)w.chunks_per_group * w.groups_per_row == chunks &&
+               w.n_scales_dev == w.Np * w.groups_per_row && zp_ok(w.Np * w.groups_per_row);
+    }
+    if (w.path == Path::Int4NGroup) {
+        if (w.rows_per_nblock <= 0 || w.zp) return false;
+        const int64_t nb = (w.Np + w.rows_per_nblock - 1) / w.rows_per_nblock;
+        return w.n_scales_dev == nb * w.Kp;
+    }
+    return false;
+}
+}  // namespace tbh
+
+extern "C" {
+
 // ---------------------------------------------------------------------------
 // matmul
 // ---------------------------------------------------------------------------
 static tbh_status matmul_enqueue(const tbh_weight *w, const float *x, int64_t M, float *y,
                                  hipStream_t s) {
-    const int64_t rows = gemv_max_rows(*w);
+    if (!weight_arrays_ok(*w))
+        return set_error(TBH_E_INVALID, "weight device arrays are inconsistent with its layout");
+    const int64_t rows = w->mfma_tiles ? 8 : gemv_max_rows(*w);
     for (int64_t m0 = 0; m0 < M;) {
-        int64_t mc = rows > 0 ? std::min(rows, M - m0) : M - m0;
+        const int64_t mc = rows > 0 ? std::min(rows, M - m0) : M - m0;
         GemvArgs a{x + m0 * w->K, w->K, y + m0 * w->N, w->N, mc};
-        hipError_t e = rows > 0 ? launch_gemv(*w, a, s) : launch_generic(*w, a, s);
+        hipError_t e;
+        if (w->mfma_tiles) e = launch_mgemv(*w, a, s);
+        else if (rows > 0) e = launch_gemv(*w, a, s);
+        else e = launch_generic(*w, a, s);
         if (e != hipSuccess) return hip_error(e, "matmul kernel launch");
         m0 += mc;
     }
@@ -498,6 +663,8 @@ tbh_status tbh_matmul(tbh_device *dev, const float *x, int64_t M, int64_t K, con
 // ---------------------------------------------------------------------------
 tbh_status tbh_dequantize_device(const tbh_weight *w, float *out, void *stream) {
     if (!w || !out) return set_error(TBH_E_INVALID, "tbh_dequantize_device: NULL argument");
+    if (!weight_arrays_ok(*w))
+        return set_error(TBH_E_INVALID, "weight device arrays are inconsistent with its layout");
     tbh_status st = use_device(w->dev->ordinal);
     if (st != TBH_OK) return st;
     hipError_t e = launch_dequant(*w, out, (hipStream_t)stream);
@@ -508,6 +675,8 @@ tbh_status tbh_dequantize_device(const tbh_weight *w, float *out, void *stream) 
 tbh_status tbh_dequantize(tbh_device *dev, const tbh_weight *w, float *out) {
     if (!dev || !w || !out) return set_error(TBH_E_INVALID, "tbh_dequantize: NULL argument");
     if (w->dev != dev) return set_error(TBH_E_INVALID, "tbh_dequantize: weight belongs to another device");
+    if (!weight_arrays_ok(*w))
+        return set_error(TBH_E_INVALID, "weight device arrays are inconsistent with its layout");
     std::lock_guard<std::mutex> lock(dev->mu);
     tbh_status st = use_device(dev->ordinal);
     if (st != TBH_OK) return st;

@@ -20,6 +20,13 @@ constexpr int kInt4ChunkElems = 32;
 // Largest x tile (M * Kp fp32) the VALU GEMV keeps in LDS.
 constexpr int64_t kMaxLdsBytes = 64 * 1024;
 
+// MFMA GEMV tiles: 16 rows x 128 K (INT4) or x 64 K (INT8) per 1 KiB, and
+// the LDS budget of one stage of x fragments.
+constexpr int kMfmaInt4TileK = 128;
+constexpr int kMfmaInt8TileK = 64;
+constexpr int64_t kMgemvLdsBytes = 32 * 1024;
+constexpr int kMgemvDepth = 4;  // weight tiles in flight per wave
+
 enum class Path : int32_t {
     Int8Row = TBH_PATH_INT8_ROW,
     Int4KGroup = TBH_PATH_INT4_KGROUP,
@@ -52,6 +59,7 @@ struct tbh_weight {
     int64_t groups_per_row = 1;  // G (Int4KGroup)
     int32_t chunks_per_group = 1;
     int32_t rows_per_nblock = 1; // Int4NGroup
+    bool mfma_tiles = false;     // data in 1 KiB MFMA tiles (else K-contiguous rows)
 
     // generic path: the reference arrays as given
     int8_t *raw = nullptr;
@@ -59,6 +67,10 @@ struct tbh_weight {
     float *raw_scales = nullptr;
     int64_t n_scales = 0;
     int8_t *raw_zp = nullptr;
+
+    // element counts of the device arrays above, as uploaded
+    int64_t n_data = 0, n_scales_dev = 0, n_zp_dev = 0;
+    int64_t n_raw = 0, n_raw_scales = 0, n_raw_zp = 0;
 
     int64_t device_bytes = 0;
     int64_t stream_bytes = 0;
@@ -70,7 +82,11 @@ namespace tbh {
 tbh_status set_error(tbh_status st, const std::string &msg);
 tbh_status hip_error(hipError_t e, const char *what);
 
-// Kernel launchers.  All validate nothing: the API layer checks shapes.
+// Host-side check, before any launch, that the device arrays a weight's
+// kernels index exist and have the sizes those kernels assume.
+bool weight_arrays_ok(const tbh_weight &w);
+
+// Kernel launchers.  The API layer checks shapes and weight_arrays_ok first.
 struct GemvArgs {
     const float *x;
     int64_t ldx;
@@ -85,6 +101,9 @@ hipError_t launch_gemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s);
 // Largest number of x rows one launch_gemv call handles for this weight
 // (0 when the fast path cannot take it).
 int64_t gemv_max_rows(const tbh_weight &w);
+
+// MFMA dequant-GEMV for M <= 8 rows of x on MFMA-tiled weights (tbh_mgemv.hip).
+hipError_t launch_mgemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s);
 
 // Generic INT4 kernel over the reference flat layout (tbh_ref_kernels.hip).
 hipError_t launch_generic(const tbh_weight &w, const GemvArgs &a, hipStream_t s);

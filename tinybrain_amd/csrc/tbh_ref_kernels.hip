@@ -117,6 +117,49 @@ __global__ void dequant_int4_ngroup(const DequantParams p) {
     }
 }
 
+// INT8 MFMA tiles: element (k, n) is in tile (n / 16, k / 64), lane
+// n % 16 + 16 * ((k % 32) / 8), word 2 * ((k % 64) / 32) + (k % 8) / 4, byte
+// position {0, 2, 1, 3}[k % 4]; value q + 128.
+__global__ void dequant_int8_tiles(const DequantParams p) {
+    const int64_t total = p.K * p.N;
+    const int64_t SC = p.Kp / kMfmaInt8TileK;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t k = idx / p.N, n = idx - k * p.N;
+        const int l = (int)(n % 16) + 16 * (int)((k % 32) / 8);
+        const int word = 2 * (int)((k % 64) / 32) + (int)((k % 8) / 4);
+        const int j = (int)(k & 3);
+        const int bp = j == 1 ? 2 : (j == 2 ? 1 : j);
+        const int64_t off = ((n / 16) * SC + k / 64) * 1024 + 16 * l + 4 * word + bp;
+        const int q = (int)p.data[off] - 128;
+        const int z = p.zp ? (int)p.zp[n] : 0;
+        p.out[idx] = __fmul_rn((float)q - (float)z, p.scales[n]);
+    }
+}
+
+// INT4 MFMA tiles: element (k, n) is in tile (n / 16, k / 128), lane
+// n % 16 + 16 * ((k % 32) / 8), word (k % 128) / 32, nibble at bit offset
+// {0, 16, 4, 20, 8, 24, 12, 28}[k % 8]; value q + 8.  Scales are per row
+// (G == 1) or per (row, 32-element chunk) in tile order.
+__global__ void dequant_int4_tiles(const DequantParams p) {
+    const int64_t total = p.K * p.N;
+    const int64_t SC = p.Kp / kMfmaInt4TileK;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t k = idx / p.N, n = idx - k * p.N;
+        const int l = (int)(n % 16) + 16 * (int)((k % 32) / 8);
+        const int word = (int)((k % 128) / 32);
+        const int64_t tile = (n / 16) * SC + k / 128;
+        const uint32_t w = ((const uint32_t *)(p.data + tile * 1024))[4 * l + word];
+        const int e = (int)(k & 7);
+        const int shift = ((e & 1) << 4) | ((e >> 1) << 2);
+        const int q = (int)((w >> shift) & 0xFu) - 8;
+        const int64_t si = p.G == 1 ? n : (tile * 16 + n % 16) * 4 + word;
+        const int z = p.zp ? (int)p.zp[si] : 0;
+        p.out[idx] = __fmul_rn((float)q - (float)z, p.scales[si]);
+    }
+}
+
 __global__ void dequant_int4_generic(const DequantParams p) {
     const int64_t total = p.K * p.N;
     for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
@@ -169,6 +212,13 @@ hipError_t launch_dequant(const tbh_weight &w, float *out, hipStream_t s) {
     p.raw = w.raw;
     const int64_t total = w.K * w.N;
     const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 65536);
+    if (w.mfma_tiles) {
+        if (w.precision == TBH_PREC_INT8)
+            hipLaunchKernelGGL(dequant_int8_tiles, dim3(blocks), dim3(256), 0, s, p);
+        else
+            hipLaunchKernelGGL(dequant_int4_tiles, dim3(blocks), dim3(256), 0, s, p);
+        return hipGetLastError();
+    }
     switch (w.path) {
     case Path::Int8Row: hipLaunchKernelGGL(dequant_int8_row, dim3(blocks), dim3(256), 0, s, p); break;
     case Path::Int4KGroup: hipLaunchKernelGGL(dequant_int4_kgroup, dim3(blocks), dim3(256), 0, s, p); break;
