@@ -143,6 +143,32 @@ def test_int4_baseline_config1(backend, K, N):
     _check(backend, _product(qt, (K, N), T.Layout.NK_FLAT), qt, Ms=(1, 4, 8))
 
 
+# Burst GEMV (M <= 2, no zero points, 16-byte aligned x, K % 4 == 0): one case
+# per chunk-iteration count I = ceil(chunks / 64) = 1..6 and per rows-per-wave
+# U = 1..16, which the launch picks from N and the CU count (256 on MI355X).
+@pytest.mark.parametrize("prec,K,N", [
+    ("int4", 2048, 40960),   # I=1, U=16
+    ("int4", 2048, 20000),   # I=1, U=8
+    ("int4", 4096, 9000),    # I=2, U=4
+    ("int4", 5632, 3001),    # I=3, ragged N
+    ("int4", 8192, 1000),    # I=4
+    ("int4", 10240, 520),    # I=5
+    ("int4", 11008, 2048),   # I=6 (7B down projection)
+    ("int8", 1024, 40000),   # I=1, U=8
+    ("int8", 2048, 5632),    # I=2, U=2
+    ("int8", 5632, 2048),    # I=6 (1.1B down projection)
+    ("int8", 4000, 777),     # I=4, ragged N
+])
+def test_burst_shapes(backend, prec, K, N):
+    if prec == "int8":
+        oq = _int8_pc(41 + K, K, N)
+        pq = _product(oq, (K, N))
+    else:
+        oq = _int4_nk(43 + K, K, N, 32)
+        pq = _product(oq, (K, N), T.Layout.NK_FLAT)
+    _check(backend, pq, oq, Ms=(1, 2), cpu_path=False)
+
+
 @pytest.mark.parametrize("K,N,gs,path", [(256, 512, 32, "int4_ngroup"), (2048, 2048, 32, "int4_ngroup"),
                                          (128, 64, 128, "int4_ngroup"), (64, 96, 96, "int4_ngroup"),
                                          (40, 48, 48, "int4_ngroup"), (50, 40, 48, "generic"),

@@ -1,4 +1,4 @@
-// tbh_gemv.hip -- VALU dequant-GEMV for decode (M = 1..4 rows of x).
+// tbh_gemv.hip -- VALU dequant-GEMV for decode (M = 1..4 rows of x per launch).
 //
 // Replaces the MSL kernels matmul_int8_dequant / matmul_int4_dequant
 // (Sources/TinyBrainMetal/Shaders/Dequant.metal:49-79,
@@ -8,10 +8,15 @@
 // repack) with non-temporal 128-bit loads, so every load instruction moves
 // 1 KiB of contiguous HBM.
 //
-// Schedule: the grid is persistent (a few blocks per CU).  A wave walks a
-// sequence of work items -- (row group, chunk iteration) -- and issues the
-// loads of item t+1 before it computes item t, so HBM latency overlaps the
-// unpack/FMA work.  The first item's loads go out before x is staged in LDS.
+// Two schedules:
+//   * gemv_burst (M <= 2, no zero points, rows up to 64 * 6 chunks): one wave
+//     per U rows, every load of the wave issued at kernel start, so a launch
+//     puts the whole matrix's reads in flight at once and pays HBM latency
+//     about once -- the decode shapes are only 2-70 MB, a few microseconds
+//     of HBM time, so latency and ramp dominate otherwise;
+//   * gemv_valu (everything else): a persistent grid (a few blocks per CU)
+//     where a wave walks (row group, chunk iteration) items and issues the
+//     loads of item t+1 before it computes item t.
 //
 // Unpack (per 32-bit word of packed weights, values stored offset-binary):
 //   INT8: (w & 0x00FF00FF) | 0x64006400 is the f16 pair 1024 + (q+128);
@@ -55,9 +60,15 @@ struct KParams {
 };
 
 __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
-    uint32_t d;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(m), "v"(o));
-    return d;
+    return (a & m) | o;  // v_and_or_b32 when m and o are registers (see opaque)
+}
+
+// A constant the compiler may not fold: kept in a register, it lets
+// (a & m) | o select one v_and_or_b32 (VOP3 takes no literal on gfx9)
+// instead of v_and_b32 + v_or_b32 with literals.
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
 }
 
 __device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
@@ -209,7 +220,6 @@ __global__ __launch_bounds__(256) void gemv_valu(const KParams p) {
     constexpr int CS = CE + 4;               // padded LDS floats per chunk
     constexpr int V = pow2_ceil(M * R);      // values per lane to reduce
     extern __shared__ float4 xs4[];          // float4-typed: x reads are ds_read_b128
-    float *xs = reinterpret_cast<float *>(xs4);
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int GW = gridDim.x * 4;
@@ -246,9 +256,9 @@ __global__ __launch_bounds__(256) void gemv_valu(const KParams p) {
     else stage_x<PREC, M, false>(p, xs4, lds_row, tid);
     __syncthreads();
 
-    const uint32_t kMagic = 0x64006400u;
-    const uint32_t kLo = PREC == 8 ? 0x00FF00FFu : 0x000F000Fu;
-    const uint32_t kHi = 0x00F000F0u;
+    const uint32_t kMagic = opaque(0x64006400u);
+    const uint32_t kLo = opaque(PREC == 8 ? 0x00FF00FFu : 0x000F000Fu);
+    const uint32_t kHi = opaque(0x00F000F0u);
 
     float acc[M][R];
 #pragma unroll
@@ -378,6 +388,181 @@ __global__ __launch_bounds__(256) void gemv_valu(const KParams p) {
     }
 }
 
+// Workgroup barrier that orders LDS only: it does not wait for the global
+// loads still in flight, which a full __syncthreads() fence would.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// ---- burst kernel: every load of a wave in flight at once -----------------
+//
+// A wave owns U consecutive rows and reads all of them -- I 16-byte chunks
+// per row and lane, chunk c = lane + 64 i -- with loads issued back to back
+// at kernel start, ahead of any compute (U * I <= 16, so at most 64 VGPRs of
+// weights per lane).  The x loads go out first; x is written to LDS while
+// the weight loads are still in flight, behind a barrier that waits for LDS
+// only.  Compute then consumes the chunks in issue order, so each wait is
+// for the oldest outstanding load.  The grid is not persistent: one wave
+// per U rows, so a launch issues the whole matrix's reads in its first
+// microsecond when it fits the GPU, and HBM latency is paid about once.
+// INT8 rows (one scale per row) and INT4 K-groups without zero points.
+template <int PREC, int M, int U, int I>
+__global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
+    constexpr int CE = PREC == 8 ? 16 : 32;
+    constexpr int CS = CE + 4;
+    constexpr int V = M * U;           // M and U are powers of two
+    constexpr int XR = I * CE / 16;    // float4 x loads per thread and x row
+    extern __shared__ float4 xs4[];
+
+    constexpr int lds_row = 64 * I * CS;  // LDS floats per x row: every slot the loads cover
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int r0 = (blockIdx.x * 4 + wave) * U;
+
+    // ---- 1. x loads (16-byte aligned rows, K % 4 == 0; clamped addresses,
+    // zeroed beyond K).  No branches before the weight loads: a branch merge
+    // makes the compiler wait for every load issued before it.
+    float4 xv[M][XR];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        const float *xr = p.x + (int64_t)m * p.ldx;
+#pragma unroll
+        for (int r = 0; r < XR; ++r) {
+            const int k = 4 * (tid + 256 * r);
+            const float4 t = *(const float4 *)(xr + min(k, p.K - 4));  // x_vec4 holds
+            const bool in = k < p.K;
+            xv[m][r] = float4{in ? t.x : 0.f, in ? t.y : 0.f, in ? t.z : 0.f, in ? t.w : 0.f};
+        }
+    }
+
+    // ---- 2. all weight (and scale) loads of the wave, in consumption order
+    u32x4 w[I][U];
+    float s[I][U];
+#pragma unroll
+    for (int i = 0; i < I; ++i) {
+        const int c = min(lane + 64 * i, p.chunks - 1);  // idle lanes re-read a valid chunk
+        const int g = c / p.cpg;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t row = min(r0 + u, p.Np - 1);
+            w[i][u] = __builtin_nontemporal_load(
+                (const u32x4 *)(p.data + row * p.row_bytes + (int64_t)c * 16));
+            if (PREC == 4) s[i][u] = p.scales[row * p.G + g];
+        }
+    }
+    const int ridx = reduce_index<V>(lane);  // value this lane holds after the reduce
+    const float rs = PREC == 8 ? p.scales[min(r0 + ridx % U, p.Np - 1)] : 0.0f;
+    // Nothing that consumes a load may be scheduled above this point.
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- 3. x -> LDS (INT4 slots k % 4 in {2, 3} pre-divided by 16).  The
+    // stores are unconditional (zeros beyond K): a conditional store would let
+    // the compiler sink its x load behind the weight loads.
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int r = 0; r < XR; ++r) {
+            const int k = 4 * (tid + 256 * r);
+            float4 t = xv[m][r];
+            if (PREC == 4) { t.z *= 0.0625f; t.w *= 0.0625f; }
+            xs4[(m * lds_row + lds_index<CE>(k)) >> 2] = t;
+        }
+    lds_barrier();
+    if (r0 >= p.Np) return;  // idle wave of the last block (after the barrier)
+
+    // ---- 4. unpack and accumulate, chunk by chunk in issue order: the x
+    // elements of chunk c are read from LDS once, then every row's chunk is
+    // finished as soon as its load has landed.
+    const uint32_t kMagic = opaque(0x64006400u);
+    const uint32_t kLo = opaque(PREC == 8 ? 0x00FF00FFu : 0x000F000Fu);
+    const uint32_t kHi = opaque(0x00F000F0u);
+    float acc[M][U];
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc[m][u] = 0.0f;
+
+#pragma unroll
+    for (int i = 0; i < I; ++i) {
+        const int c = lane + 64 * i;
+        if (i < I - 1 || c < p.chunks) {
+            constexpr int XQ = CE / 4;  // float4 of x per chunk and x row
+            float4 xq[M][XQ];
+#pragma unroll
+            for (int m = 0; m < M; ++m)
+#pragma unroll
+                for (int q = 0; q < XQ; ++q) xq[m][q] = xs4[(m * lds_row + c * CS + 4 * q) >> 2];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                if (PREC == 8) {
+                    const h2 c8 = splat(-1152.0f);
+                    // two interleaved FMA chains per row: back-to-back dependent
+                    // v_fma_mix_f32 would need a wait state each
+                    float a0[M], a1[M];
+#pragma unroll
+                    for (int m = 0; m < M; ++m) { a0[m] = acc[m][u]; a1[m] = 0.0f; }
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        const uint32_t wv = w[i][u][d];
+                        const h2 p0 = as_h2(and_or(wv, kLo, kMagic)) + c8;
+                        const h2 p1 = as_h2(and_or(wv >> 8, kLo, kMagic)) + c8;
+#pragma unroll
+                        for (int m = 0; m < M; ++m) {
+                            a0[m] = fmix(p0.x, xq[m][d].x, a0[m]);
+                            a1[m] = fmix(p1.x, xq[m][d].z, a1[m]);
+                            a0[m] = fmix(p0.y, xq[m][d].y, a0[m]);
+                            a1[m] = fmix(p1.y, xq[m][d].w, a1[m]);
+                        }
+                    }
+#pragma unroll
+                    for (int m = 0; m < M; ++m) acc[m][u] = a0[m] + a1[m];
+                } else {
+                    const h2 c1 = splat(-1032.0f), c16 = splat(-1152.0f);
+                    // two interleaved FMA chains per row (see INT8)
+                    float a0[M], a1[M];
+#pragma unroll
+                    for (int m = 0; m < M; ++m) { a0[m] = 0.0f; a1[m] = 0.0f; }
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        const uint32_t wv = w[i][u][d];
+                        const uint32_t w8 = wv >> 8;
+                        const h2 p0 = as_h2(and_or(wv, kLo, kMagic)) + c1;
+                        const h2 p1 = as_h2(and_or(wv, kHi, kMagic)) + c16;
+                        const h2 p2 = as_h2(and_or(w8, kLo, kMagic)) + c1;
+                        const h2 p3 = as_h2(and_or(w8, kHi, kMagic)) + c16;
+#pragma unroll
+                        for (int m = 0; m < M; ++m) {
+                            const float4 xa = xq[m][2 * d], xb = xq[m][2 * d + 1];
+                            a0[m] = fmix(p0.x, xa.x, a0[m]);
+                            a1[m] = fmix(p2.x, xb.x, a1[m]);
+                            a0[m] = fmix(p0.y, xa.y, a0[m]);
+                            a1[m] = fmix(p2.y, xb.y, a1[m]);
+                            a0[m] = fmix(p1.x, xa.z, a0[m]);
+                            a1[m] = fmix(p3.x, xb.z, a1[m]);
+                            a0[m] = fmix(p1.y, xa.w, a0[m]);
+                            a1[m] = fmix(p3.y, xb.w, a1[m]);
+                        }
+                    }
+#pragma unroll
+                    for (int m = 0; m < M; ++m)
+                        acc[m][u] = __builtin_fmaf(s[i][u], a0[m] + a1[m], acc[m][u]);
+                }
+            }
+        }
+    }
+
+    // ---- 5. reduce across the wave and write
+    float v[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) v[j] = acc[j / U][j % U];
+    const float tot = reduce_multi<V>(v, lane);
+    if ((lane & (64 / V - 1)) == 0) {
+        const int m = ridx / U, n = r0 + ridx % U;
+        if (n < p.N) p.y[(int64_t)m * p.ldy + n] = PREC == 8 ? tot * rs : tot;
+    }
+}
+
 int64_t lds_bytes_for(const tbh_weight &w, int64_t M) {
     const int ce = w.precision == TBH_PREC_INT8 ? kInt8ChunkElems : kInt4ChunkElems;
     return M * (w.Kp / ce) * (ce + 4) * (int64_t)sizeof(float);
@@ -418,6 +603,56 @@ int env_int(const char *name, int dflt) {
     return v && *v ? std::atoi(v) : dflt;
 }
 
+// Burst-kernel shapes: chunk iterations per row I <= kBurstMaxI, rows per
+// wave U a power of two with U * I <= 16.
+constexpr int kBurstMaxI = 6;
+
+template <int PREC, int M, int U, int I>
+hipError_t launch_burst_one(const KParams &p, size_t lds, hipStream_t s) {
+    if constexpr (U * I > 16) {
+        return hipErrorInvalidValue;
+    } else {
+        const int64_t waves = (p.Np + U - 1) / U;
+        const unsigned blocks = (unsigned)((waves + 3) / 4);
+        hipLaunchKernelGGL((gemv_burst<PREC, M, U, I>), dim3(blocks), dim3(256), lds, s, p);
+        return hipGetLastError();
+    }
+}
+
+template <int PREC, int M, int I>
+hipError_t burst_u(int U, const KParams &p, size_t lds, hipStream_t s) {
+    switch (U) {
+    case 1: return launch_burst_one<PREC, M, 1, I>(p, lds, s);
+    case 2: return launch_burst_one<PREC, M, 2, I>(p, lds, s);
+    case 4: return launch_burst_one<PREC, M, 4, I>(p, lds, s);
+    case 8: return launch_burst_one<PREC, M, 8, I>(p, lds, s);
+    case 16: return launch_burst_one<PREC, M, 16, I>(p, lds, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+template <int PREC, int M>
+hipError_t burst_i(int I, int U, const KParams &p, size_t lds, hipStream_t s) {
+    switch (I) {
+    case 1: return burst_u<PREC, M, 1>(U, p, lds, s);
+    case 2: return burst_u<PREC, M, 2>(U, p, lds, s);
+    case 3: return burst_u<PREC, M, 3>(U, p, lds, s);
+    case 4: return burst_u<PREC, M, 4>(U, p, lds, s);
+    case 5: return burst_u<PREC, M, 5>(U, p, lds, s);
+    case 6: return burst_u<PREC, M, 6>(U, p, lds, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+template <int PREC>
+hipError_t burst_m(int M, int I, int U, const KParams &p, size_t lds, hipStream_t s) {
+    switch (M) {
+    case 1: return burst_i<PREC, 1>(I, U, p, lds, s);
+    case 2: return burst_i<PREC, 2>(I, U, p, lds, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
 }  // namespace
 
 int64_t gemv_max_rows(const tbh_weight &w) {
@@ -452,13 +687,33 @@ hipError_t launch_gemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s) {
     p.cpg = w.chunks_per_group;
     p.rpn = w.rows_per_nblock;
     p.x_vec4 = (w.K % 4 == 0 && a.ldx % 4 == 0 && ((uintptr_t)a.x & 15) == 0) ? 1 : 0;
+    const int64_t cus = std::max(1, w.dev->cu_count);
+
+    // Burst kernel: M <= 2, no zero points, rows of at most 64 * kBurstMaxI
+    // chunks, 16-byte aligned x rows with K % 4 == 0.  U: the largest power of two (U * I <= 16) that still leaves
+    // `waves_per_cu` waves per CU, so small matrices spread over the whole
+    // GPU and large ones keep 16 chunk loads in flight per lane.
+    static const int kernel_sel = env_int("TBH_GEMV_PERSISTENT", 0);
+    static const int burst_wpc = env_int("TBH_GEMV_WAVES_PER_CU", 16);
+    static const int u_force = env_int("TBH_GEMV_U", 0);
+    const int I = (p.chunks + 63) / 64;
+    const int ce = int8 ? kInt8ChunkElems : kInt4ChunkElems;
+    const int64_t blds = (int64_t)M * 64 * I * (ce + 4) * (int64_t)sizeof(float);
+    if (!kernel_sel && M <= 2 && w.zp == nullptr && I <= kBurstMaxI && p.x_vec4 &&
+        blds <= kMaxLdsBytes &&
+        (w.path == Path::Int8Row || w.path == Path::Int4KGroup)) {
+        int U = 1;
+        while (2 * U * I <= 16 && w.Np / (2 * U) >= burst_wpc * cus) U *= 2;
+        if (u_force > 0 && u_force * I <= 16 && (u_force & (u_force - 1)) == 0) U = u_force;
+        return w.path == Path::Int8Row ? burst_m<8>(M, I, U, p, (size_t)blds, s)
+                                       : burst_m<4>(M, I, U, p, (size_t)blds, s);
+    }
 
     // Persistent grid: a few 4-wave blocks per CU.  Rows per wave (R): as
     // many as still give every wave work, within the register budget
     // (M*R <= 16) and dividing the N-block height of the runtime layout.
     static const int bpc = env_int("TBH_GEMV_BLOCKS_PER_CU", 2);
     static const int r_force = env_int("TBH_GEMV_ROWS", 0);
-    const int64_t cus = std::max(1, w.dev->cu_count);
     const int64_t max_blocks = bpc * cus;
     int R = 8;
     while (R > 1 && (w.Np / R < 4 * max_blocks || M * R > 16 ||
