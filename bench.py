@@ -42,6 +42,15 @@ WORKLOADS = {
     "int8_pc_gemv_m1": ("int8", 0, [(5632, 2048)], 1),
 }
 
+# Prefill: x [M x K] bf16 N(0,1), one dequant-GEMM on
+# bf16 MFMA per step.  name: (precision, group, (N, K), M)
+PREFILL = {}
+for _m in (64, 128, 512, 2048):
+    PREFILL[f"prefill_int8_m{_m}"] = ("int8", 0, (5632, 2048), _m)
+    PREFILL[f"prefill_int4_m{_m}"] = ("int4", 32, (2048, 5632), _m)
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
+RIDGE_FLOP_PER_BYTE = MFMA_BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
+
 
 def alg_bytes(prec: str, gs: int, N: int, K: int, M: int) -> int:
     if prec == "int4":
@@ -115,12 +124,135 @@ def cpu_baseline(qts, shapes, M: int, budget_s: float = 15.0):
     }
 
 
+def prefill_bytes(prec: str, gs: int, N: int, K: int, M: int) -> int:
+    """W + S + 2*M*K (bf16 x) + 4*M*N (fp32 y)."""
+    return alg_bytes(prec, gs, N, K, 0) + 2 * M * K + 4 * M * N
+
+
+def cpu_baseline_prefill(qt, N, K, M, budget_s: float = 15.0):
+    """Reference CPU path on the same product: dequantize() single-threaded,
+    then sgemm of the (bf16-valued) fp32 activations on all host cores."""
+    import oracle as O
+
+    threads = min(os.cpu_count() or 1, 16)
+    oq = O.QTensor(qt.shape, qt.data, qt.scales, qt.zeroPoints, int(qt.mode), int(qt.precision),
+                   qt.groupSize)
+    x = np.random.default_rng(1).normal(size=(M, K)).astype(np.float32)
+    x = (x.view(np.uint32) & 0xFFFF0000).view(np.float32)   # bf16-valued
+    steps, t_deq, t_gemm = 0, 0.0, 0.0
+    t0 = time.perf_counter()
+    while True:
+        _, td, tg = O.matmul_quantized_cpu(x, oq, threads=threads)
+        t_deq += td
+        t_gemm += tg
+        steps += 1
+        if time.perf_counter() - t0 > budget_s or steps >= 20:
+            break
+    wall = time.perf_counter() - t0
+    return {
+        "value": round(2.0 * M * N * K * steps / wall / 1e12, 5),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{steps} GEMM(s) of the same shape; dequantize {t_deq:.2f}s single-threaded + "
+                  f"sgemm {t_gemm:.2f}s on {threads} threads",
+        "ms_per_step": round(1e3 * wall / steps, 3),
+    }
+
+
+def run_prefill(args, backend, T, torch):
+    prec, gs, (N, K), M = PREFILL[args.workload]
+    dev = torch.device("cuda", 0)
+    t_setup = time.perf_counter()
+    base = make_weight(prec, gs, N, K, seed=0x7B1A0030)
+    n_sets = max(2, int(np.ceil(args.pool_gib * 2**30 / alg_bytes(prec, gs, N, K, 0))))
+    pool = [T.DeviceWeight(backend, base) for _ in range(n_sets)]
+    setup_s = time.perf_counter() - t_setup
+    gen = torch.Generator(device=dev).manual_seed(3)
+    x = torch.randn((M, K), generator=gen, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    y = torch.empty((M, N), device=dev, dtype=torch.float32)
+    cap = torch.cuda.Stream(dev)
+    cap.wait_stream(torch.cuda.current_stream(dev))
+    for i in range(n_sets):
+        backend.matmul_bf16_device(x, pool[i], out=y, stream=cap)
+    torch.cuda.synchronize()
+    eager = y.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=cap):
+        for i in range(n_sets):
+            backend.matmul_bf16_device(x, pool[i], out=y, stream=cap)
+    for _ in range(2):
+        y.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        if not torch.equal(y, eager):
+            raise RuntimeError("graph replay differs from the eager launches")
+    reps = max(1, -(-args.steps // n_sets))
+    warm = max(1, -(-args.warmup // n_sets))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(cap):
+        for _ in range(warm):
+            graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record(cap)
+        for _ in range(reps):
+            graph.replay()
+        e1.record(cap)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    steps_done = reps * n_sets
+    kern_us = e0.elapsed_time(e1) * 1e3 / steps_done
+    flops = 2.0 * M * N * K
+    byts = prefill_bytes(prec, gs, N, K, M)
+    value = flops * steps_done / wall / 1e12
+    mfma_bound = flops / byts >= RIDGE_FLOP_PER_BYTE
+    if mfma_bound:
+        roof = {"bound": "mfma", "achieved": round(flops / kern_us / 1e6, 2),
+                "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s"}
+    else:
+        roof = {"bound": "hbm", "achieved": round(byts / kern_us / 1e3, 1),
+                "peak": HBM_PEAK_GBS, "unit": "GB/s"}
+    roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
+    roof.update({"traffic": None, "kernel": f"gemm_bf16 {N}x{K} M={M} ({pool[0].path})",
+                 "kernel_us": round(kern_us, 3), "alg_bytes_per_launch": byts,
+                 "flops_per_launch": int(flops)})
+    out = {
+        "metric": f"prefill dequant-GEMM TFLOP/s on bf16 MFMA ({prec.upper()}, M={M})",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": steps_done,
+        "warmup": warm * n_sets,
+        "ms_per_step": round(1e3 * wall / steps_done, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": args.workload,
+            "weights": "INT4 symmetric, group 32 along K (converter layout)" if prec == "int4"
+            else "INT8 symmetric per output channel",
+            "shape_NxK": f"{N}x{K}", "M": M,
+            "x": "bf16 (rounded from fp32 N(0,1)), W fp32 N(0,0.02) quantized",
+            "pool_sets": n_sets,
+        },
+        "roofline": roof,
+        "setup_s": round(setup_s, 1),
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline_prefill(base, N, K, M, args.cpu_budget)
+    print(json.dumps(out), flush=True)
+    backend.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="int4_g32_gemv_m1", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="int4_g32_gemv_m1", choices=sorted(WORKLOADS) + sorted(PREFILL))
     ap.add_argument("--pool-gib", type=float, default=2.2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
@@ -137,9 +269,11 @@ def main():
     import torch
     import tinybrain_amd as T
 
-    prec, gs, shapes, M = WORKLOADS[args.workload]
     torch.cuda.set_device(0)
     backend = T.HIPBackend(0)
+    if args.workload in PREFILL:
+        return run_prefill(args, backend, T, torch)
+    prec, gs, shapes, M = WORKLOADS[args.workload]
 
     # ---- weights: one quantized base per shape, copied into a >= 2 GiB pool
     t_setup = time.perf_counter()

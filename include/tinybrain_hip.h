@@ -158,6 +158,20 @@ tbh_status tbh_matmul(tbh_device *dev, const float *x, int64_t M, int64_t K,
 tbh_status tbh_matmul_device(const tbh_weight *w, const float *x, int64_t M,
                              int64_t K, float *y, void *stream);
 
+/* Prefill: the same product for M >= 64 rows of bf16 activations, on bf16
+ * MFMA.  The reference has no bf16 path; it multiplies
+ * fp32 activations by dequantize(w) with cblas_sgemm
+ * (QuantizedTensor.swift:640-642, Tensor.swift:839-861), which is the
+ * product computed here for x = the bf16 values widened to fp32: weight
+ * operands are exact (INT8: q - zp, scaled after accumulation; INT4:
+ * (q - zp) * scale rounded once in fp32, split into three bf16 pieces),
+ * accumulation is fp32.  x is [M, K] row-major bf16 bits (16-byte aligned,
+ * K % 8 == 0), y is [M, N] fp32, both device pointers; enqueued on `stream`.
+ * TBH_E_UNSUPPORTED for weights outside the INT8 row / INT4 K-group paths
+ * (tbh_weight_info.path) or for the MFMA tile layout. */
+tbh_status tbh_matmul_bf16_device(const tbh_weight *w, const uint16_t *x, int64_t M,
+                                  int64_t K, float *y, void *stream);
+
 /* ---- dequantize (verification) ----------------------------------------- */
 /* Replaces QuantizedTensor.dequantize() (QuantizedTensor.swift:182-286) for
  * the uploaded weight: writes the [K, N] row-major fp32 matrix that the

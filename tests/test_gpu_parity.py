@@ -332,3 +332,74 @@ def test_x_range_extremes(backend, tile_layout):
     for m in range(3):
         assert O.parity_errors(y[m:m + 1], y64[m:m + 1])["gated"] <= GATE, m
     assert np.all(y[3] == 0.0)
+
+
+# ---------------------------------------------------------------------------
+# prefill: bf16 activations on bf16 MFMA (tbh_matmul_bf16_device)
+# ---------------------------------------------------------------------------
+def _prefill_check(backend, pq, oq, M, seed):
+    import torch
+
+    K, N = pq.shape
+    W = _oracle_weight(oq, pq.layout)
+    x32 = O.fill_normal(seed, M * K).reshape(M, K)
+    xb = torch.from_numpy(x32).to(torch.bfloat16)          # round to nearest even
+    xf = xb.float().numpy()                                 # the exact values multiplied
+    y = backend.matmul_bf16_device(xb.cuda(), backend.weight(pq))
+    torch.cuda.synchronize()
+    err = O.parity_errors(y.cpu().numpy(), O.gemm_f64(xf, W))
+    assert err["gated"] <= GATE, (M, K, N, err)
+    return err
+
+
+@pytest.mark.parametrize("prec,K,N,M", [
+    ("int8", 2048, 5632, 64),     # BASELINE configs[3] shapes
+    ("int8", 2048, 5632, 512),
+    ("int4", 5632, 2048, 128),
+    ("int4", 5632, 2048, 512),
+    ("int8", 64, 40, 3),          # tiny, ragged tiles
+    ("int8", 1000, 777, 129),     # K not a multiple of 64, ragged M and N
+    ("int4", 96, 24, 70),
+    ("int4", 4096, 1000, 200),
+])
+def test_prefill_bf16(backend, prec, K, N, M):
+    if prec == "int8":
+        oq = _int8_pc(61 + K + M, K, N)
+        pq = _product(oq, (K, N))
+    else:
+        oq = _int4_nk(67 + K + M, K, N, 32)
+        pq = _product(oq, (K, N), T.Layout.NK_FLAT)
+    _prefill_check(backend, pq, oq, M, seed=5 + M)
+
+
+def test_prefill_bf16_large_m(backend):
+    # configs[3] at M = 2048 (INT4 g32, 2048 x 5632)
+    oq = _int4_nk(71, 5632, 2048, 32)
+    _prefill_check(backend, _product(oq, (5632, 2048), T.Layout.NK_FLAT), oq, 2048, seed=9)
+
+
+def test_prefill_bf16_zero_points_and_groups(backend):
+    qi = _int8_pc(73, 512, 96)
+    qi.zero_points = ((np.arange(96) % 9) - 4).astype(np.int8)
+    _prefill_check(backend, _product(qi, (512, 96)), qi, 65, seed=11)
+    q4 = _int4_nk(79, 512, 48, 64)                         # group 64 along K
+    q4.zero_points = ((np.arange(q4.scales.size) % 7) - 3).astype(np.int8)
+    _prefill_check(backend, _product(q4, (512, 48), T.Layout.NK_FLAT), q4, 64, seed=13)
+    q0 = _int4_nk(83, 256, 40, 256 * 40)                   # one group for the whole tensor
+    _prefill_check(backend, _product(q0, (256, 40), T.Layout.NK_FLAT), q0, 64, seed=17)
+
+
+def test_prefill_bf16_unsupported(backend):
+    import torch
+
+    qk = _int4_kn(89, 256, 512, 32)                        # runtime layout: N-groups
+    pq = _product(qk, (256, 512))
+    x = torch.zeros((64, 256), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(T.HIPBackendError) as e:
+        backend.matmul_bf16_device(x, backend.weight(pq))
+    assert e.value.status == _abi.E_UNSUPPORTED
+    qi = _int8_pc(97, 100, 16)                             # K % 8 != 0
+    x = torch.zeros((64, 100), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(T.HIPBackendError) as e:
+        backend.matmul_bf16_device(x, backend.weight(_product(qi, (100, 16))))
+    assert e.value.status == _abi.E_UNSUPPORTED

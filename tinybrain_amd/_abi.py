@@ -24,7 +24,7 @@ EXPORTS = [
     "tbh_abi_version", "tbh_last_error", "tbh_status_string",
     "tbh_device_open", "tbh_device_close", "tbh_device_get_info",
     "tbh_weight_create", "tbh_weight_destroy", "tbh_weight_get_info",
-    "tbh_matmul", "tbh_matmul_device",
+    "tbh_matmul", "tbh_matmul_device", "tbh_matmul_bf16_device",
     "tbh_dequantize", "tbh_dequantize_device",
 ]
 
@@ -86,11 +86,13 @@ def lib() -> ctypes.CDLL:
     L.tbh_weight_get_info.argtypes = [vp, ctypes.POINTER(WeightInfo)]
     L.tbh_matmul.argtypes = [vp, vp, i64, i64, vp, vp]
     L.tbh_matmul_device.argtypes = [vp, vp, i64, i64, vp, vp]
+    L.tbh_matmul_bf16_device.argtypes = [vp, vp, i64, i64, vp, vp]
     L.tbh_dequantize.argtypes = [vp, vp, vp]
     L.tbh_dequantize_device.argtypes = [vp, vp, vp]
     for name in ("tbh_device_open", "tbh_device_close", "tbh_device_get_info",
                  "tbh_weight_create", "tbh_weight_destroy", "tbh_weight_get_info",
-                 "tbh_matmul", "tbh_matmul_device", "tbh_dequantize", "tbh_dequantize_device"):
+                 "tbh_matmul", "tbh_matmul_device", "tbh_matmul_bf16_device",
+                 "tbh_dequantize", "tbh_dequantize_device"):
         getattr(L, name).restype = i32
     _lib = L
     return L

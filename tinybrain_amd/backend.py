@@ -163,6 +163,24 @@ class HIPBackend:
                                            out.data_ptr(), ctypes.c_void_p(s.cuda_stream)))
         return out
 
+    def matmul_bf16_device(self, x, weight: DeviceWeight, out=None, stream=None):
+        """Prefill: enqueue y = x . W for bf16 activations on bf16 MFMA.
+
+        x: bfloat16 [M, K] contiguous cuda tensor (K % 8 == 0); returns
+        float32 [M, N].  See tbh_matmul_bf16_device."""
+        import torch
+
+        if x.dim() != 2 or x.shape[1] != weight.K:
+            raise PreconditionFailure("Dimensions must match")
+        if x.dtype != torch.bfloat16 or not x.is_contiguous() or not x.is_cuda:
+            raise PreconditionFailure("x must be a contiguous bfloat16 device tensor")
+        if out is None:
+            out = torch.empty((x.shape[0], weight.N), dtype=torch.float32, device=x.device)
+        s = stream if stream is not None else torch.cuda.current_stream(x.device)
+        _check(self._lib.tbh_matmul_bf16_device(weight.handle, x.data_ptr(), x.shape[0], x.shape[1],
+                                                out.data_ptr(), ctypes.c_void_p(s.cuda_stream)))
+        return out
+
     def dequantize_device(self, weight: DeviceWeight, out=None, stream=None):
         import torch
 

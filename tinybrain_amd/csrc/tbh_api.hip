@@ -658,6 +658,29 @@ tbh_status tbh_matmul(tbh_device *dev, const float *x, int64_t M, int64_t K, con
     return TBH_OK;
 }
 
+tbh_status tbh_matmul_bf16_device(const tbh_weight *w, const uint16_t *x, int64_t M, int64_t K,
+                                  float *y, void *stream) {
+    if (!w) return set_error(TBH_E_INVALID, "tbh_matmul_bf16_device: weight is NULL");
+    if (M < 0) return set_error(TBH_E_INVALID, "tbh_matmul_bf16_device: M < 0");
+    if (K != w->K) return set_error(TBH_E_INVALID, "Dimensions must match (x K != weight K)");
+    if (M == 0) return TBH_OK;
+    if (!x || !y) return set_error(TBH_E_INVALID, "tbh_matmul_bf16_device: x or y is NULL");
+    if (!prefill_supported(*w))
+        return set_error(TBH_E_UNSUPPORTED,
+                         "tbh_matmul_bf16_device: needs an INT8 row or INT4 K-group weight in the "
+                         "row layout");
+    if (K % 8 != 0 || ((uintptr_t)x & 15) != 0)
+        return set_error(TBH_E_UNSUPPORTED,
+                         "tbh_matmul_bf16_device: needs K % 8 == 0 and a 16-byte aligned x");
+    if (!weight_arrays_ok(*w))
+        return set_error(TBH_E_INVALID, "weight device arrays are inconsistent with its layout");
+    tbh_status st = use_device(w->dev->ordinal);
+    if (st != TBH_OK) return st;
+    hipError_t e = launch_prefill(*w, x, K, M, y, w->N, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_error(e, "prefill kernel launch");
+    return TBH_OK;
+}
+
 // ---------------------------------------------------------------------------
 // dequantize
 // ---------------------------------------------------------------------------

@@ -108,6 +108,13 @@ hipError_t launch_mgemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s);
 // Generic INT4 kernel over the reference flat layout (tbh_ref_kernels.hip).
 hipError_t launch_generic(const tbh_weight &w, const GemvArgs &a, hipStream_t s);
 
+// Prefill dequant-GEMM on bf16 MFMA (tbh_prefill.hip): x [M][ldx] bf16
+// bits, y [M][ldy] fp32.  Needs prefill_supported(w), K % 8 == 0, ldx % 8
+// == 0 and a 16-byte aligned x.
+bool prefill_supported(const tbh_weight &w);
+hipError_t launch_prefill(const tbh_weight &w, const uint16_t *x, int64_t ldx, int64_t M, float *y,
+                          int64_t ldy, hipStream_t s);
+
 // Bit-exact dequantization to [K, N] row-major (tbh_ref_kernels.hip).
 hipError_t launch_dequant(const tbh_weight &w, float *out, hipStream_t s);
 
