@@ -48,6 +48,14 @@ PREFILL = {}
 for _m in (64, 128, 512, 2048):
     PREFILL[f"prefill_int8_m{_m}"] = ("int8", 0, (5632, 2048), _m)
     PREFILL[f"prefill_int4_m{_m}"] = ("int4", 32, (2048, 5632), _m)
+# Decode (BASELINE configs[2] and [5]): one token of a LLaMA-shaped model on
+# the GPU decode step.  name: (precision, group, config kwargs, context)
+DECODE = {
+    "decode_1p1b_int8": ("int8", 0, dict(num_layers=22, hidden=2048, num_heads=32, num_kv_heads=4,
+                                         intermediate=5632, vocab=32000), 512),
+    "decode_7b_int4": ("int4", 32, dict(num_layers=32, hidden=4096, num_heads=32, num_kv_heads=32,
+                                        intermediate=11008, vocab=32000), 512),
+}
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 RIDGE_FLOP_PER_BYTE = MFMA_BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
 
@@ -247,12 +255,149 @@ def run_prefill(args, backend, T, torch):
     backend.close()
 
 
+def decode_shapes(c):
+    """(K, N) of every projection of one layer, and of the LM head."""
+    H, I, kv = c["hidden"], c["intermediate"], c["hidden"] // c["num_heads"] * c["num_kv_heads"]
+    return [(H, H), (H, kv), (H, kv), (H, H), (H, I), (H, I), (I, H)], (H, c["vocab"])
+
+
+def decode_bytes(prec, gs, c, ctx):
+    """Algorithmic HBM bytes of one decode step: every GEMV's W + S + x + y,
+    plus the K and V cache rows attention reads (fp32, ctx positions)."""
+    layer, lm = decode_shapes(c)
+    b = c["num_layers"] * sum(alg_bytes(prec, gs, N, K, 1) for K, N in layer)
+    b += alg_bytes(prec, gs, lm[1], lm[0], 1)
+    kv = c["hidden"] // c["num_heads"] * c["num_kv_heads"]
+    return b + c["num_layers"] * 2 * ctx * kv * 4
+
+
+def cpu_baseline_decode(prec, gs, c, qts, budget_s: float = 15.0):
+    """Reference CPU path for one step: every projection is dequantize()
+    (single-threaded, fresh buffer) + sgemm on all host cores
+    (QuantizedTensor.swift:640-642).  Timed on one layer's seven projections
+    and the LM head; a step is num_layers layers + the LM head (attention,
+    norms and activations, which the CPU path also runs, are left out)."""
+    import oracle as O
+
+    threads = min(os.cpu_count() or 1, 16)
+    layer, lm = decode_shapes(c)
+    oq = [O.QTensor(q.shape, q.data, q.scales, q.zeroPoints, int(q.mode), int(q.precision), q.groupSize)
+          for q in qts]
+    t_layer = t_lm = 0.0
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        for (K, N), q in zip(layer, oq[:7]):
+            x = np.random.default_rng(K).normal(size=(1, K)).astype(np.float32)
+            t1 = time.perf_counter()
+            O.matmul_quantized_cpu(x, q, threads=threads)
+            t_layer += time.perf_counter() - t1
+        x = np.random.default_rng(7).normal(size=(1, lm[0])).astype(np.float32)
+        t1 = time.perf_counter()
+        O.matmul_quantized_cpu(x, oq[7], threads=threads)
+        t_lm += time.perf_counter() - t1
+        reps += 1
+        if time.perf_counter() - t0 > budget_s or reps >= 5:
+            break
+    step_s = (c["num_layers"] * t_layer + t_lm) / reps
+    return {
+        "value": round(1.0 / step_s, 4),
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{reps} pass(es) over one layer's 7 projections + the LM head, scaled to "
+                  f"{c['num_layers']} layers; projections only",
+        "ms_per_step": round(1e3 * step_s, 1),
+    }
+
+
+def run_decode(args, backend, T, torch):
+    prec, gs, c, ctx = DECODE[args.workload]
+    dev = torch.device("cuda", 0)
+    cfg = T.DecoderConfig(max_seq=ctx + args.warmup + args.steps + 8, **c)
+    layer, lm = decode_shapes(c)
+    t_setup = time.perf_counter()
+    # One random init per projection shape; every layer gets its own device
+    # copy, so a step streams all num_layers layers' weights from HBM.
+    qts = [make_weight(prec, gs, N, K, seed=0x7B1A0040 + j) for j, (K, N) in enumerate(layer)]
+    qts.append(make_weight(prec, gs, lm[1], lm[0], seed=0x7B1A0050))
+    rng = np.random.default_rng(5)
+    emb = rng.normal(0, 1, size=(c["vocab"], c["hidden"])).astype(np.float32)
+    norm = lambda: (1.0 + 0.1 * rng.normal(size=c["hidden"])).astype(np.float32)
+    dec = T.Decoder(backend, cfg, emb, norm(), qts[7])
+    for l in range(c["num_layers"]):
+        dec.set_layer(l, norm(), norm(), qts[:7])
+    setup_s = time.perf_counter() - t_setup
+
+    cap = torch.cuda.Stream(dev)
+    logits = torch.empty(c["vocab"], dtype=torch.float32, device=dev)
+    tok = 1
+    for _ in range(ctx):                      # fill the KV cache: context `ctx`
+        dec.step_device(tok, logits, cap)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=cap):
+        dec.step_device(tok, logits, cap)
+    dec.set_position(ctx)                     # capture does not run the step
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(cap):
+        for _ in range(args.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record(cap)
+        for _ in range(args.steps):
+            graph.replay()
+        e1.record(cap)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    if dec.position != ctx + args.warmup + args.steps:
+        raise RuntimeError("decode position did not advance once per replay")
+    step_us = e0.elapsed_time(e1) * 1e3 / args.steps
+    mean_ctx = ctx + args.warmup + (args.steps - 1) / 2.0 + 1
+    byts = decode_bytes(prec, gs, c, mean_ctx)
+    achieved = byts / step_us / 1e3
+    out = {
+        "metric": f"decode tokens/s, {c['num_layers']}-layer LLaMA shape ({prec.upper()}), 1 GPU",
+        "value": round(args.steps / wall, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(1e3 * wall / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": args.workload, **c, "context": ctx,
+            "weights": ("INT8 symmetric per output channel" if prec == "int8" else
+                        "INT4 symmetric, group 32 along K (converter layout)") +
+                       "; one random init per projection shape, a device copy per layer",
+            "batch": 1, "launches_per_step": 6 * c["num_layers"] + 3,
+        },
+        "roofline": {
+            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "decode step (graph of all launches)", "kernel_us": round(step_us, 2),
+            "alg_bytes_per_launch": int(byts),
+        },
+        "setup_s": round(setup_s, 1),
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline_decode(prec, gs, c, qts, args.cpu_budget)
+    print(json.dumps(out), flush=True)
+    dec.close()
+    backend.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="int4_g32_gemv_m1", choices=sorted(WORKLOADS) + sorted(PREFILL))
+    ap.add_argument("--workload", default="int4_g32_gemv_m1", choices=sorted(WORKLOADS) + sorted(PREFILL) + sorted(DECODE))
     ap.add_argument("--pool-gib", type=float, default=2.2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
@@ -273,6 +418,8 @@ def main():
     backend = T.HIPBackend(0)
     if args.workload in PREFILL:
         return run_prefill(args, backend, T, torch)
+    if args.workload in DECODE:
+        return run_decode(args, backend, T, torch)
     prec, gs, shapes, M = WORKLOADS[args.workload]
 
     # ---- weights: one quantized base per shape, copied into a >= 2 GiB pool

@@ -172,6 +172,56 @@ tbh_status tbh_matmul_device(const tbh_weight *w, const float *x, int64_t M,
 tbh_status tbh_matmul_bf16_device(const tbh_weight *w, const uint16_t *x, int64_t M,
                                   int64_t K, float *y, void *stream);
 
+/* ---- decode step (LLaMA-style models, one sequence) -------------------- */
+/* Replaces ModelRunner.step (Sources/TinyBrainRuntime/ModelRunner.swift:168-208)
+ * for the pre-norm LLaMA architecture (applyLayer :418-459, attention
+ * :496-592): RMSNorm, Q/K/V, RoPE, grouped-query attention over a KV cache,
+ * output projection and residual, RMSNorm, SwiGLU FFN and residual, final
+ * RMSNorm and the LM head, every projection on the quantized GEMV.  Gemma /
+ * Phi variants, biases and X-Ray observers are not covered.  The position is
+ * kept on the device and advanced by each step, so a step captured in a HIP
+ * graph replays as the next one. */
+typedef struct tbh_decoder tbh_decoder;
+typedef struct tbh_decoder_config {
+    int32_t num_layers;
+    int32_t hidden;          /* ModelConfig.hiddenDim */
+    int32_t num_heads;
+    int32_t num_kv_heads;
+    int32_t intermediate;    /* ModelConfig.intermediateDim */
+    int32_t vocab;
+    int32_t max_seq;         /* KV cache length, <= 16384 */
+    float rms_eps;           /* 1e-5 (Tensor.swift:1512) */
+    float rope_base;         /* 10000 (ModelRunner.swift:478) */
+} tbh_decoder_config;
+
+/* embeddings: [vocab][hidden] fp32 (ModelWeights.tokenEmbeddings);
+ * final_norm: [hidden]; lm_head: [hidden, vocab] (ModelWeights.output).
+ * Host pointers, copied. */
+tbh_status tbh_decoder_create(tbh_device *dev, const tbh_decoder_config *cfg,
+                              const float *embeddings, const float *final_norm,
+                              const tbh_qtensor_desc *lm_head, tbh_decoder **out);
+/* One TransformerLayerWeights (ModelWeights.swift): norms [hidden] and the
+ * seven projections as [K, N] quantized tensors (q [hidden, hidden], k and v
+ * [hidden, kv_dim], o [hidden, hidden], gate and up [hidden, intermediate],
+ * down [intermediate, hidden]).  Q|K|V and gate|up are concatenated along N
+ * into one repacked weight each.  Needs INT8 runtime-layout or INT4
+ * converter-layout (K-group) weights without zero points. */
+tbh_status tbh_decoder_set_layer(tbh_decoder *d, int32_t layer, const float *input_norm,
+                                 const float *post_attention_norm,
+                                 const tbh_qtensor_desc *q, const tbh_qtensor_desc *k,
+                                 const tbh_qtensor_desc *v, const tbh_qtensor_desc *o,
+                                 const tbh_qtensor_desc *gate, const tbh_qtensor_desc *up,
+                                 const tbh_qtensor_desc *down);
+tbh_status tbh_decoder_destroy(tbh_decoder *d);
+/* ModelRunner.reset (:213-216) is set_position(d, 0). */
+tbh_status tbh_decoder_set_position(tbh_decoder *d, int32_t position);
+tbh_status tbh_decoder_get_position(const tbh_decoder *d, int32_t *position);
+/* Enqueue one step for `token` on `stream`; logits: device [vocab] (NULL:
+ * internal buffer). */
+tbh_status tbh_decoder_step_device(tbh_decoder *d, int32_t token, float *logits, void *stream);
+/* Synchronous step; logits: host [vocab]. */
+tbh_status tbh_decoder_step(tbh_decoder *d, int32_t token, float *logits);
+
 /* ---- dequantize (verification) ----------------------------------------- */
 /* Replaces QuantizedTensor.dequantize() (QuantizedTensor.swift:182-286) for
  * the uploaded weight: writes the [K, N] row-major fp32 matrix that the

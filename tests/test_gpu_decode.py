@@ -1,0 +1,156 @@
+"""GPU decode step (tbh_decoder) against the decode-step oracle
+(oracle/decode_ref.py, ModelRunner.step restated in float64) on the same
+dequantized weights.  Gate: max|logit - ref| / max(|ref|, 1e-3 * max|ref|)
+<= 1e-3 at every step."""
+import numpy as np
+import pytest
+
+import oracle as O
+import tinybrain_amd as T
+from oracle.decode_ref import RefDecoder, RefLayer
+from tinybrain_amd import _abi
+
+pytestmark = pytest.mark.gpu
+
+GATE = 1e-3
+
+
+@pytest.fixture(scope="module")
+def backend():
+    b = T.HIPBackend(0)
+    yield b
+    b.close()
+
+
+def _weight(prec, seed, K, N, std=0.02):
+    """(product QuantizedTensor, dequantized [K, N] fp32) for one projection."""
+    if prec == "int8":
+        qt = O.quantize_per_channel(O.fill_normal(seed, K * N, std=std).reshape(K, N))
+        pq = T.QuantizedTensor((K, N), qt.data, qt.scales, qt.mode, qt.precision, qt.group_size,
+                               qt.zero_points, T.Layout.KN_FLAT)
+        return pq, O.dequantize(qt)
+    qt = O.quantize_int4(O.fill_normal(seed, N * K, std=std).reshape(N, K), 32, O.ROUND_SWIFT)
+    pq = T.QuantizedTensor((K, N), qt.data, qt.scales, qt.mode, qt.precision, qt.group_size,
+                           qt.zero_points, T.Layout.NK_FLAT)
+    return pq, np.ascontiguousarray(O.dequantize(qt).T)
+
+
+def _model(backend, cfg: T.DecoderConfig, prec: str, seed: int):
+    H, I, V, kv = cfg.hidden, cfg.intermediate, cfg.vocab, cfg.kv_dim
+    norm = lambda s: (1.0 + 0.1 * O.fill_normal(s, H)).astype(np.float32)
+    emb = O.fill_normal(seed, V * H).reshape(V, H)
+    fn = norm(seed + 1)
+    lm, lm_w = _weight(prec, seed + 2, H, V)
+    dec = T.Decoder(backend, cfg, emb, fn, lm)
+    layers = []
+    shapes = [(H, H), (H, kv), (H, kv), (H, H), (H, I), (H, I), (I, H)]
+    for l in range(cfg.num_layers):
+        ws = [_weight(prec, seed + 100 * (l + 1) + j, K, N) for j, (K, N) in enumerate(shapes)]
+        gi, gp = norm(seed + 100 * (l + 1) + 50), norm(seed + 100 * (l + 1) + 51)
+        dec.set_layer(l, gi, gp, [w[0] for w in ws])
+        layers.append(RefLayer(gi, gp, [w[1] for w in ws]))
+    ref = RefDecoder(cfg.num_layers, H, cfg.num_heads, cfg.num_kv_heads, I, V, emb, fn, lm_w, layers,
+                     cfg.rms_eps, cfg.rope_base)
+    return dec, ref
+
+
+def _gated(y, ref):
+    floor = 1e-3 * np.max(np.abs(ref))
+    return float(np.max(np.abs(y - ref) / np.maximum(np.abs(ref), floor)))
+
+
+SMALL = dict(num_layers=2, hidden=256, num_heads=4, num_kv_heads=2, intermediate=512, vocab=1000,
+             max_seq=32)
+
+
+@pytest.mark.parametrize("prec", ["int8", "int4"])
+def test_decode_small(backend, prec):
+    cfg = T.DecoderConfig(**SMALL)
+    dec, ref = _model(backend, cfg, prec, seed=11)
+    for i, tok in enumerate([5, 17, 3, 999, 0, 42, 7, 7, 512, 1]):
+        y = dec.step(tok)
+        r = ref.step(tok)
+        assert _gated(y, r) <= GATE, (i, tok, _gated(y, r))
+        assert dec.position == i + 1
+    dec.close()
+
+
+def test_decode_tinyllama_width(backend):
+    # TinyLlama-1.1B layer shapes with 2 of the 22 layers
+    cfg = T.DecoderConfig(num_layers=2, hidden=2048, num_heads=32, num_kv_heads=4, intermediate=5632,
+                          vocab=32000, max_seq=64)
+    dec, ref = _model(backend, cfg, "int8", seed=21)
+    for i, tok in enumerate([1, 31999, 450]):
+        y = dec.step(tok)
+        r = ref.step(tok)
+        assert _gated(y, r) <= GATE, (i, _gated(y, r))
+    dec.close()
+
+
+def test_decode_reset_is_deterministic(backend):
+    cfg = T.DecoderConfig(**SMALL)
+    dec, _ = _model(backend, cfg, "int8", seed=31)
+    a = [dec.step(t) for t in (4, 8, 15)]
+    dec.reset()
+    assert dec.position == 0
+    b = [dec.step(t) for t in (4, 8, 15)]
+    for x, y in zip(a, b):
+        np.testing.assert_array_equal(x, y)
+    dec.close()
+
+
+def test_decode_full_cache_is_an_error(backend):
+    cfg = T.DecoderConfig(**dict(SMALL, max_seq=3))
+    dec, _ = _model(backend, cfg, "int8", seed=41)
+    for t in (1, 2, 3):
+        dec.step(t)
+    with pytest.raises(T.HIPBackendError) as e:
+        dec.step(4)
+    assert e.value.status == _abi.E_INVALID
+    dec.set_position(0)
+    dec.step(1)                                   # usable again after a reset
+    dec.close()
+
+
+def test_decode_graph_replay_advances_position(backend):
+    import torch
+
+    cfg = T.DecoderConfig(**SMALL)
+    eager, _ = _model(backend, cfg, "int8", seed=51)
+    graphed, _ = _model(backend, cfg, "int8", seed=51)
+    want = [eager.step(9) for _ in range(5)]
+    logits = torch.empty(cfg.vocab, dtype=torch.float32, device="cuda")
+    s = torch.cuda.Stream()
+    graphed.step_device(9, logits, s)             # position 0, eager
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(logits.cpu().numpy(), want[0])
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        graphed.step_device(9, logits, s)
+    graphed.set_position(1)                       # capture does not run the step
+    for i in range(1, 5):
+        logits.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(logits.cpu().numpy(), want[i])
+    assert graphed.position == 5
+    eager.close()
+    graphed.close()
+
+
+def test_decode_runtime_int4_layout_is_unsupported(backend):
+    cfg = T.DecoderConfig(**dict(SMALL, num_layers=1))
+    H, kv, I = cfg.hidden, cfg.kv_dim, cfg.intermediate
+    lm, _ = _weight("int8", 1, H, cfg.vocab)
+    dec = T.Decoder(backend, cfg, O.fill_normal(2, cfg.vocab * H).reshape(cfg.vocab, H),
+                    np.ones(H, np.float32), lm)
+    ws = [_weight("int8", 3 + j, K, N)[0] for j, (K, N) in
+          enumerate([(H, H), (H, kv), (H, kv), (H, H), (H, I), (H, I), (I, H)])]
+    qk = O.quantize_int4(O.fill_normal(9, H * H).reshape(H, H), 32, O.ROUND_SWIFT)   # groups along N
+    ws[0] = T.QuantizedTensor((H, H), qk.data, qk.scales, qk.mode, qk.precision, qk.group_size,
+                              qk.zero_points, T.Layout.KN_FLAT)
+    with pytest.raises(T.HIPBackendError) as e:
+        dec.set_layer(0, np.ones(H, np.float32), np.ones(H, np.float32), ws)
+    assert e.value.status in (_abi.E_UNSUPPORTED, _abi.E_INVALID)
+    dec.close()

@@ -13,9 +13,10 @@ from .quantized import (Layout, PreconditionFailure, QuantizationMode,  # noqa: 
                         quantize, quantize_int4_flat, unpackInt4,
                         unpack_int4_array, pack_int4_array)
 from .backend import DeviceWeight, HIPBackend, HIPBackendError  # noqa: F401
+from .decoder import Decoder, DecoderConfig  # noqa: F401
 
 __all__ = [
-    "HIPBackend", "HIPBackendError", "DeviceWeight", "QuantizedTensor",
+    "HIPBackend", "HIPBackendError", "DeviceWeight", "QuantizedTensor", "Decoder", "DecoderConfig",
     "QuantizationMode", "QuantizationPrecision", "Layout", "PreconditionFailure",
     "quantize", "quantize_int4_flat", "packInt4", "unpackInt4",
 ]

@@ -26,6 +26,9 @@ EXPORTS = [
     "tbh_weight_create", "tbh_weight_destroy", "tbh_weight_get_info",
     "tbh_matmul", "tbh_matmul_device", "tbh_matmul_bf16_device",
     "tbh_dequantize", "tbh_dequantize_device",
+    "tbh_decoder_create", "tbh_decoder_set_layer", "tbh_decoder_destroy",
+    "tbh_decoder_set_position", "tbh_decoder_get_position",
+    "tbh_decoder_step_device", "tbh_decoder_step",
 ]
 
 
@@ -61,6 +64,20 @@ class WeightInfo(ctypes.Structure):
     ]
 
 
+class DecoderConfig(ctypes.Structure):
+    _fields_ = [
+        ("num_layers", ctypes.c_int32),
+        ("hidden", ctypes.c_int32),
+        ("num_heads", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("intermediate", ctypes.c_int32),
+        ("vocab", ctypes.c_int32),
+        ("max_seq", ctypes.c_int32),
+        ("rms_eps", ctypes.c_float),
+        ("rope_base", ctypes.c_float),
+    ]
+
+
 _lib = None
 
 
@@ -71,6 +88,14 @@ def lib() -> ctypes.CDLL:
         return _lib
     if not os.path.exists(LIB_PATH):
         raise OSError(f"{LIB_PATH} is not built; run `python -m tinybrain_amd.build`")
+    # One HIP runtime per process: PyTorch ships its own libamdhip64.so.7
+    # under the same soname as ROCm's, whichever loads first serves both, and
+    # torch cannot initialise its GPU support on a runtime it did not load.
+    # When torch is installed, load it first so the library binds to it.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     L = ctypes.CDLL(LIB_PATH)
     vp, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
     pp = ctypes.POINTER(ctypes.c_void_p)
@@ -89,6 +114,18 @@ def lib() -> ctypes.CDLL:
     L.tbh_matmul_bf16_device.argtypes = [vp, vp, i64, i64, vp, vp]
     L.tbh_dequantize.argtypes = [vp, vp, vp]
     L.tbh_dequantize_device.argtypes = [vp, vp, vp]
+    dp = ctypes.POINTER(QTensorDesc)
+    L.tbh_decoder_create.argtypes = [vp, ctypes.POINTER(DecoderConfig), vp, vp, dp, pp]
+    L.tbh_decoder_set_layer.argtypes = [vp, i32, vp, vp, dp, dp, dp, dp, dp, dp, dp]
+    L.tbh_decoder_destroy.argtypes = [vp]
+    L.tbh_decoder_set_position.argtypes = [vp, i32]
+    L.tbh_decoder_get_position.argtypes = [vp, ctypes.POINTER(i32)]
+    L.tbh_decoder_step_device.argtypes = [vp, i32, vp, vp]
+    L.tbh_decoder_step.argtypes = [vp, i32, vp]
+    for name in ("tbh_decoder_create", "tbh_decoder_set_layer", "tbh_decoder_destroy",
+                 "tbh_decoder_set_position", "tbh_decoder_get_position",
+                 "tbh_decoder_step_device", "tbh_decoder_step"):
+        getattr(L, name).restype = i32
     for name in ("tbh_device_open", "tbh_device_close", "tbh_device_get_info",
                  "tbh_weight_create", "tbh_weight_destroy", "tbh_weight_get_info",
                  "tbh_matmul", "tbh_matmul_device", "tbh_matmul_bf16_device",

@@ -57,7 +57,17 @@ struct KParams {
     int32_t cpg;     // chunks per K-group
     int32_t rpn;     // rows per N-block (INT4 runtime layout)
     int32_t x_vec4;  // x rows are 16-byte aligned and K % 4 == 0
+    // fused decode prologue / epilogue (gemv_burst with M = 1 only)
+    const float *x2;   // PRO_SILU_MUL: second input (x = silu(x) * x2)
+    const float *g;    // PRO_RMSNORM: norm weight [K]
+    float eps;         // PRO_RMSNORM: epsilon
 };
+
+enum { PRO_NONE = 0, PRO_RMSNORM = 1, PRO_SILU_MUL = 2 };
+enum { EPI_STORE = 0, EPI_ACCUMULATE = 1 };
+
+// expf at full precision (not the hardware exp2 approximation).
+__device__ __forceinline__ float __expf_exact(float v) { return expf(v); }
 
 __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
     return (a & m) | o;  // v_and_or_b32 when m and o are registers (see opaque)
@@ -408,13 +418,15 @@ __device__ __forceinline__ void lds_barrier() {
 // per U rows, so a launch issues the whole matrix's reads in its first
 // microsecond when it fits the GPU, and HBM latency is paid about once.
 // INT8 rows (one scale per row) and INT4 K-groups without zero points.
-template <int PREC, int M, int U, int I>
+template <int PREC, int M, int U, int I, int PRO, int EPI>
 __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
     constexpr int CE = PREC == 8 ? 16 : 32;
     constexpr int CS = CE + 4;
     constexpr int V = M * U;           // M and U are powers of two
     constexpr int XR = I * CE / 16;    // float4 x loads per thread and x row
+    static_assert(PRO == PRO_NONE || M == 1, "fused prologues take one x row");
     extern __shared__ float4 xs4[];
+    __shared__ float red[4];
 
     constexpr int lds_row = 64 * I * CS;  // LDS floats per x row: every slot the loads cover
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -435,6 +447,17 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
             xv[m][r] = float4{in ? t.x : 0.f, in ? t.y : 0.f, in ? t.z : 0.f, in ? t.w : 0.f};
         }
     }
+    float4 av[XR];  // PRO_RMSNORM: g;  PRO_SILU_MUL: x2
+    if constexpr (PRO != PRO_NONE) {
+        const float *ar = PRO == PRO_RMSNORM ? p.g : p.x2;
+#pragma unroll
+        for (int r = 0; r < XR; ++r) {
+            const int k = 4 * (tid + 256 * r);
+            const float4 t = *(const float4 *)(ar + min(k, p.K - 4));
+            const bool in = k < p.K;
+            av[r] = float4{in ? t.x : 0.f, in ? t.y : 0.f, in ? t.z : 0.f, in ? t.w : 0.f};
+        }
+    }
 
     // ---- 2. all weight (and scale) loads of the wave, in consumption order
     u32x4 w[I][U];
@@ -453,8 +476,41 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
     }
     const int ridx = reduce_index<V>(lane);  // value this lane holds after the reduce
     const float rs = PREC == 8 ? p.scales[min(r0 + ridx % U, p.Np - 1)] : 0.0f;
+    const float yin = EPI == EPI_ACCUMULATE ? p.y[min(r0 + ridx % U, p.N - 1)] : 0.0f;
     // Nothing that consumes a load may be scheduled above this point.
     __builtin_amdgcn_sched_barrier(0);
+
+    // ---- fused prologue: x <- rmsnorm(x) * g or silu(x) * x2 (reference
+    // order of operations: Tensor.swift:1543-1556, :1135-1141;
+    // ModelRunner.swift:449-451)
+    if constexpr (PRO == PRO_RMSNORM) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int r = 0; r < XR; ++r)
+            ss += xv[0][r].x * xv[0][r].x + xv[0][r].y * xv[0][r].y + xv[0][r].z * xv[0][r].z +
+                  xv[0][r].w * xv[0][r].w;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+        if (lane == 0) red[wave] = ss;
+        lds_barrier();
+        ss = (red[0] + red[1]) + (red[2] + red[3]);
+        const float inv = 1.0f / __builtin_sqrtf(ss / (float)p.K + p.eps);
+#pragma unroll
+        for (int r = 0; r < XR; ++r) {
+            xv[0][r].x = xv[0][r].x * inv * av[r].x;
+            xv[0][r].y = xv[0][r].y * inv * av[r].y;
+            xv[0][r].z = xv[0][r].z * inv * av[r].z;
+            xv[0][r].w = xv[0][r].w * inv * av[r].w;
+        }
+    } else if constexpr (PRO == PRO_SILU_MUL) {
+#pragma unroll
+        for (int r = 0; r < XR; ++r) {
+            xv[0][r].x = xv[0][r].x / (1.0f + __expf_exact(-xv[0][r].x)) * av[r].x;
+            xv[0][r].y = xv[0][r].y / (1.0f + __expf_exact(-xv[0][r].y)) * av[r].y;
+            xv[0][r].z = xv[0][r].z / (1.0f + __expf_exact(-xv[0][r].z)) * av[r].z;
+            xv[0][r].w = xv[0][r].w / (1.0f + __expf_exact(-xv[0][r].w)) * av[r].w;
+        }
+    }
 
     // ---- 3. x -> LDS (INT4 slots k % 4 in {2, 3} pre-divided by 16).  The
     // stores are unconditional (zeros beyond K): a conditional store would let
@@ -559,7 +615,8 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
     const float tot = reduce_multi<V>(v, lane);
     if ((lane & (64 / V - 1)) == 0) {
         const int m = ridx / U, n = r0 + ridx % U;
-        if (n < p.N) p.y[(int64_t)m * p.ldy + n] = PREC == 8 ? tot * rs : tot;
+        const float v = PREC == 8 ? tot * rs : tot;
+        if (n < p.N) p.y[(int64_t)m * p.ldy + n] = EPI == EPI_ACCUMULATE ? yin + v : v;
     }
 }
 
@@ -607,39 +664,39 @@ int env_int(const char *name, int dflt) {
 // wave U a power of two with U * I <= 16.
 constexpr int kBurstMaxI = 6;
 
-template <int PREC, int M, int U, int I>
+template <int PREC, int M, int U, int I, int PRO, int EPI>
 hipError_t launch_burst_one(const KParams &p, size_t lds, hipStream_t s) {
     if constexpr (U * I > 16) {
         return hipErrorInvalidValue;
     } else {
         const int64_t waves = (p.Np + U - 1) / U;
         const unsigned blocks = (unsigned)((waves + 3) / 4);
-        hipLaunchKernelGGL((gemv_burst<PREC, M, U, I>), dim3(blocks), dim3(256), lds, s, p);
+        hipLaunchKernelGGL((gemv_burst<PREC, M, U, I, PRO, EPI>), dim3(blocks), dim3(256), lds, s, p);
         return hipGetLastError();
     }
 }
 
-template <int PREC, int M, int I>
+template <int PREC, int M, int I, int PRO, int EPI>
 hipError_t burst_u(int U, const KParams &p, size_t lds, hipStream_t s) {
     switch (U) {
-    case 1: return launch_burst_one<PREC, M, 1, I>(p, lds, s);
-    case 2: return launch_burst_one<PREC, M, 2, I>(p, lds, s);
-    case 4: return launch_burst_one<PREC, M, 4, I>(p, lds, s);
-    case 8: return launch_burst_one<PREC, M, 8, I>(p, lds, s);
-    case 16: return launch_burst_one<PREC, M, 16, I>(p, lds, s);
+    case 1: return launch_burst_one<PREC, M, 1, I, PRO, EPI>(p, lds, s);
+    case 2: return launch_burst_one<PREC, M, 2, I, PRO, EPI>(p, lds, s);
+    case 4: return launch_burst_one<PREC, M, 4, I, PRO, EPI>(p, lds, s);
+    case 8: return launch_burst_one<PREC, M, 8, I, PRO, EPI>(p, lds, s);
+    case 16: return launch_burst_one<PREC, M, 16, I, PRO, EPI>(p, lds, s);
     default: return hipErrorInvalidValue;
     }
 }
 
-template <int PREC, int M>
+template <int PREC, int M, int PRO, int EPI>
 hipError_t burst_i(int I, int U, const KParams &p, size_t lds, hipStream_t s) {
     switch (I) {
-    case 1: return burst_u<PREC, M, 1>(U, p, lds, s);
-    case 2: return burst_u<PREC, M, 2>(U, p, lds, s);
-    case 3: return burst_u<PREC, M, 3>(U, p, lds, s);
-    case 4: return burst_u<PREC, M, 4>(U, p, lds, s);
-    case 5: return burst_u<PREC, M, 5>(U, p, lds, s);
-    case 6: return burst_u<PREC, M, 6>(U, p, lds, s);
+    case 1: return burst_u<PREC, M, 1, PRO, EPI>(U, p, lds, s);
+    case 2: return burst_u<PREC, M, 2, PRO, EPI>(U, p, lds, s);
+    case 3: return burst_u<PREC, M, 3, PRO, EPI>(U, p, lds, s);
+    case 4: return burst_u<PREC, M, 4, PRO, EPI>(U, p, lds, s);
+    case 5: return burst_u<PREC, M, 5, PRO, EPI>(U, p, lds, s);
+    case 6: return burst_u<PREC, M, 6, PRO, EPI>(U, p, lds, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -647,10 +704,21 @@ hipError_t burst_i(int I, int U, const KParams &p, size_t lds, hipStream_t s) {
 template <int PREC>
 hipError_t burst_m(int M, int I, int U, const KParams &p, size_t lds, hipStream_t s) {
     switch (M) {
-    case 1: return burst_i<PREC, 1>(I, U, p, lds, s);
-    case 2: return burst_i<PREC, 2>(I, U, p, lds, s);
+    case 1: return burst_i<PREC, 1, PRO_NONE, EPI_STORE>(I, U, p, lds, s);
+    case 2: return burst_i<PREC, 2, PRO_NONE, EPI_STORE>(I, U, p, lds, s);
     default: return hipErrorInvalidValue;
     }
+}
+
+// The fused decode variants (M = 1): the prologue / epilogue pairs a decode
+// step uses.
+template <int PREC>
+hipError_t burst_fused(int pro, int epi, int I, int U, const KParams &p, size_t lds, hipStream_t s) {
+    if (pro == PRO_RMSNORM && epi == EPI_STORE) return burst_i<PREC, 1, PRO_RMSNORM, EPI_STORE>(I, U, p, lds, s);
+    if (pro == PRO_NONE && epi == EPI_ACCUMULATE) return burst_i<PREC, 1, PRO_NONE, EPI_ACCUMULATE>(I, U, p, lds, s);
+    if (pro == PRO_SILU_MUL && epi == EPI_ACCUMULATE)
+        return burst_i<PREC, 1, PRO_SILU_MUL, EPI_ACCUMULATE>(I, U, p, lds, s);
+    return hipErrorInvalidValue;
 }
 
 }  // namespace
@@ -662,12 +730,9 @@ int64_t gemv_max_rows(const tbh_weight &w) {
     return 0;
 }
 
-hipError_t launch_gemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s) {
-    const int M = (int)a.M;
-    if (M < 1 || M > 4) return hipErrorInvalidValue;
-    const int64_t lds = lds_bytes_for(w, M);
-    if (lds > kMaxLdsBytes) return hipErrorInvalidValue;
+namespace {
 
+KParams make_params(const tbh_weight &w, const GemvArgs &a) {
     KParams p{};
     p.x = a.x;
     p.ldx = a.ldx;
@@ -687,26 +752,77 @@ hipError_t launch_gemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s) {
     p.cpg = w.chunks_per_group;
     p.rpn = w.rows_per_nblock;
     p.x_vec4 = (w.K % 4 == 0 && a.ldx % 4 == 0 && ((uintptr_t)a.x & 15) == 0) ? 1 : 0;
-    const int64_t cus = std::max(1, w.dev->cu_count);
+    p.x2 = a.x;
+    p.g = a.x;
+    p.eps = 0.0f;
+    return p;
+}
 
-    // Burst kernel: M <= 2, no zero points, rows of at most 64 * kBurstMaxI
-    // chunks, 16-byte aligned x rows with K % 4 == 0.  U: the largest power of two (U * I <= 16) that still leaves
-    // `waves_per_cu` waves per CU, so small matrices spread over the whole
-    // GPU and large ones keep 16 chunk loads in flight per lane.
+// Burst kernel eligibility: M <= 2, no zero points, rows of at most
+// 64 * kBurstMaxI chunks, 16-byte aligned x rows with K % 4 == 0, x tile in
+// LDS.  U: the largest power of two (U * I <= 16) that still leaves
+// `waves_per_cu` waves per CU, so small matrices spread over the whole GPU
+// and large ones keep up to 16 chunk loads in flight per lane.
+bool burst_shape(const tbh_weight &w, const KParams &p, int M, int *I_out, int *U_out,
+                 int64_t *lds_out) {
     static const int kernel_sel = env_int("TBH_GEMV_PERSISTENT", 0);
     static const int burst_wpc = env_int("TBH_GEMV_WAVES_PER_CU", 16);
     static const int u_force = env_int("TBH_GEMV_U", 0);
     const int I = (p.chunks + 63) / 64;
-    const int ce = int8 ? kInt8ChunkElems : kInt4ChunkElems;
+    const int ce = w.precision == TBH_PREC_INT8 ? kInt8ChunkElems : kInt4ChunkElems;
     const int64_t blds = (int64_t)M * 64 * I * (ce + 4) * (int64_t)sizeof(float);
-    if (!kernel_sel && M <= 2 && w.zp == nullptr && I <= kBurstMaxI && p.x_vec4 &&
-        blds <= kMaxLdsBytes &&
-        (w.path == Path::Int8Row || w.path == Path::Int4KGroup)) {
-        int U = 1;
-        while (2 * U * I <= 16 && w.Np / (2 * U) >= burst_wpc * cus) U *= 2;
-        if (u_force > 0 && u_force * I <= 16 && (u_force & (u_force - 1)) == 0) U = u_force;
-        return w.path == Path::Int8Row ? burst_m<8>(M, I, U, p, (size_t)blds, s)
-                                       : burst_m<4>(M, I, U, p, (size_t)blds, s);
+    if (kernel_sel || M > 2 || w.zp != nullptr || I > kBurstMaxI || !p.x_vec4 ||
+        blds > kMaxLdsBytes || !(w.path == Path::Int8Row || w.path == Path::Int4KGroup) ||
+        w.mfma_tiles)
+        return false;
+    const int64_t cus = std::max(1, w.dev->cu_count);
+    int U = 1;
+    while (2 * U * I <= 16 && w.Np / (2 * U) >= burst_wpc * cus) U *= 2;
+    if (u_force > 0 && u_force * I <= 16 && (u_force & (u_force - 1)) == 0) U = u_force;
+    *I_out = I;
+    *U_out = U;
+    *lds_out = blds;
+    return true;
+}
+
+}  // namespace
+
+bool gemv_fused_supported(const tbh_weight &w) {
+    GemvArgs a{nullptr, w.K, nullptr, w.N, 1};
+    KParams p = make_params(w, a);
+    p.x_vec4 = w.K % 4 == 0;  // the caller's buffers are 16-byte aligned
+    int I, U;
+    int64_t lds;
+    return burst_shape(w, p, 1, &I, &U, &lds);
+}
+
+hipError_t launch_gemv_fused(const tbh_weight &w, const FusedGemvArgs &f, hipStream_t s) {
+    GemvArgs a{f.x, w.K, f.y, w.N, 1};
+    KParams p = make_params(w, a);
+    p.x2 = f.x2 ? f.x2 : f.x;
+    p.g = f.g ? f.g : f.x;
+    p.eps = f.eps;
+    if ((f.x2 && ((uintptr_t)f.x2 & 15)) || (f.g && ((uintptr_t)f.g & 15))) return hipErrorInvalidValue;
+    int I, U;
+    int64_t lds;
+    if (!burst_shape(w, p, 1, &I, &U, &lds)) return hipErrorInvalidValue;
+    return w.precision == TBH_PREC_INT8 ? burst_fused<8>(f.prologue, f.epilogue, I, U, p, (size_t)lds, s)
+                                        : burst_fused<4>(f.prologue, f.epilogue, I, U, p, (size_t)lds, s);
+}
+
+hipError_t launch_gemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s) {
+    const int M = (int)a.M;
+    if (M < 1 || M > 4) return hipErrorInvalidValue;
+    const int64_t lds = lds_bytes_for(w, M);
+    if (lds > kMaxLdsBytes) return hipErrorInvalidValue;
+    KParams p = make_params(w, a);
+    const int64_t cus = std::max(1, w.dev->cu_count);
+    {
+        int I, U;
+        int64_t blds;
+        if (burst_shape(w, p, M, &I, &U, &blds))
+            return w.path == Path::Int8Row ? burst_m<8>(M, I, U, p, (size_t)blds, s)
+                                           : burst_m<4>(M, I, U, p, (size_t)blds, s);
     }
 
     // Persistent grid: a few 4-wave blocks per CU.  Rows per wave (R): as

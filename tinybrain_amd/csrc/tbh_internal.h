@@ -102,6 +102,23 @@ hipError_t launch_gemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s);
 // (0 when the fast path cannot take it).
 int64_t gemv_max_rows(const tbh_weight &w);
 
+// Fused decode GEMV (M = 1, tbh_gemv.hip): y = W . pro(x) (+ y).
+//   prologue 0: x as given; 1: rmsnorm(x) * g with epsilon eps
+//   (Tensor.swift:1543-1556); 2: silu(x) * x2 (Tensor.swift:1135-1141,
+//   ModelRunner.swift:449-451).  epilogue 0: store; 1: y += result
+//   (the residual adds, ModelRunner.swift:434, :457).
+struct FusedGemvArgs {
+    const float *x;
+    const float *x2;
+    const float *g;
+    float eps;
+    float *y;
+    int prologue;
+    int epilogue;
+};
+bool gemv_fused_supported(const tbh_weight &w);
+hipError_t launch_gemv_fused(const tbh_weight &w, const FusedGemvArgs &f, hipStream_t s);
+
 // MFMA dequant-GEMV for M <= 8 rows of x on MFMA-tiled weights (tbh_mgemv.hip).
 hipError_t launch_mgemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s);
 
