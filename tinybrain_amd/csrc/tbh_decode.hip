@@ -14,10 +14,10 @@
 //     h += W_down . (silu(gate) * up)                          (:449-457)
 //   logits = W_lm . rmsnorm(h) * g_final                       (:186-199)
 //
-// Six launches per layer: Q|K|V and gate|up are each one weight
+// Five launches per layer: Q|K|V and gate|up are each one weight
 // (concatenated along N at set-up), RMSNorm and SiLU*up run in the GEMV's x
-// staging, the residual adds in its epilogue, and two attention kernels do
-// RoPE, the cache append, softmax over position slices and their combination.  The token position lives
+// staging, the residual adds in its epilogue, and one attention kernel does
+// RoPE, the cache append, softmax and the context.  The token position lives
 // in device memory and the step ends with a one-thread kernel that advances
 // it, so a captured step replays as the next one.
 #include <cmath>
@@ -43,8 +43,6 @@ struct tbh_decoder {
     float *vcache = nullptr;
     float *h = nullptr, *qkv = nullptr, *ctx = nullptr, *gu = nullptr, *logits = nullptr;
     int32_t *pos = nullptr;      // [0] position, [1] overflow flag
-    float *attn_part = nullptr;  // attention slice partials
-    int32_t attn_splits = 1;
     std::vector<void *> allocs;
 };
 
@@ -56,223 +54,166 @@ struct AttnParams {
     float *kcache, *vcache;  // this layer
     float *ctx;
     int32_t *pos;            // [0] position, [1] overflow flag
-    float *part;             // [num_heads][S][head_dim + 2] partial (max, sum, context)
-    int32_t nh, nkv, hd, kvd, hidden, max_seq, S;
+    int32_t nh, nkv, hd, kvd, hidden, max_seq;
     float rope_base, scale;
 };
 
-constexpr int kMaxSplits = 16;
+constexpr int kAttnThreads = 512;
+constexpr int kAttnUnits = 20;  // K and V float4 loads per thread per batch
+constexpr int kMaxHd = 128;
 
-// LDS floats of one attention block: q [rep][hd+4], K tile [tc][hd+4],
-// V tile [tc][hd], scores [rep][tc], new k and v [hd] each, per-head running
-// max / sum / rescale [rep] each.  Rows of q and K are padded by four floats
-// (16 bytes, so rows stay float4-aligned) to spread the (head, position) dot
-// products over the banks.
-__host__ __device__ inline int attn_tile(int hd) { return hd <= 64 ? 64 : 4096 / hd; }
-__host__ __device__ inline int attn_lds_floats(int rep, int hd) {
-    const int tc = attn_tile(hd);
-    return rep * (hd + 4) + tc * (hd + 4) + tc * hd + rep * tc + 2 * hd + 3 * rep;
+// Positions one batch covers: every thread loads kAttnUnits float4 of K and
+// of V, so a batch is kAttnUnits * kAttnThreads / (hd / 4) positions.
+__host__ __device__ inline int attn_batch(int hd) { return kAttnUnits * kAttnThreads / (hd / 4); }
+// LDS floats: q, new k, new v [hd] each; wave partials [8]; per-thread
+// context partials [kAttnThreads][4].
+__host__ __device__ inline int attn_lds_floats(int hd) { return 3 * hd + 8 + 4 * kAttnThreads; }
+
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// Grid (num_kv_heads, S): block (g, s) serves every query head of KV group g
-// (ModelRunner.swift:524-536: kvHead = head / repeats) over the s-th slice of
-// positions 0..pos, with a running max / sum / context per head (the
-// softmax of :545-551 taken over the slice), K and V tiles staged in LDS once
-// for all heads of the group, and writes its (max, sum, context) partials;
-// attention_combine merges them.  The block whose slice holds `pos` appends
-// the RoPE'd k and the v of position pos (:470-494, :503-516) to the cache;
-// every block computes its own copy of them, so none waits for another.
-__global__ __launch_bounds__(256) void attention_step(const AttnParams a) {
+// One block per query head h, KV group h / (num_heads / num_kv_heads)
+// (ModelRunner.swift:524-536).  RoPE (interleaved pairs, theta =
+// base^(-i/hd), fp32; :470-494) on q and the new k; the first head of each
+// group appends the new k and v to the cache at pos (:503-516) and every
+// block uses its own copy for position pos.  Positions go in batches: each
+// thread issues all its K and V loads of a batch together (thread <-> one
+// float4 column of hd/4 and positions tid/(hd/4) + i * 512/(hd/4)), scores
+// them against q with the hd/4 lanes of a row summed by shuffles, and the
+// block keeps a running max / sum / context (the softmax of :545-551) over
+// the batches.  One launch produces the context; HBM latency is paid about
+// once per batch.
+__global__ __launch_bounds__(kAttnThreads) void attention_head(const AttnParams a) {
     extern __shared__ float lds[];
-    const int g = blockIdx.x, sl = blockIdx.y, tid = threadIdx.x;
-    const int rep = a.nh / a.nkv, hd = a.hd, hp = hd + 4, tc = attn_tile(hd);
-    float *qs = lds;                    // [rep][hp]
-    float *kb = qs + rep * hp;          // [tc][hp]
-    float *vb = kb + tc * hp;           // [tc][hd]
-    float *sc = vb + tc * hd;           // [rep][tc]
-    float *kn = sc + rep * tc;          // [hd] new k (RoPE'd)
-    float *vn = kn + hd;                // [hd] new v
-    float *mrun = vn + hd;              // [rep] running max
-    float *lrun = mrun + rep;           // [rep] running sum
-    float *alpha = lrun + rep;          // [rep] rescale of this tile
+    const int h = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int rep = a.nh / a.nkv, kvh = h / rep, hd = a.hd, H4 = hd / 4;
+    float *qs = lds;              // [hd]
+    float *kn = qs + hd;          // [hd]
+    float *vn = kn + hd;          // [hd]
+    float *red = vn + hd;         // [8]
+    float4 *cs = (float4 *)(red + 8);  // [kAttnThreads]
+
+    // Everything that does not depend on the position is loaded before it:
+    // this thread's RoPE pair and v element, and the first batch's K / V rows
+    // 0..NB-1 (in bounds whatever the position; rows past it are masked).
+    const int NB = attn_batch(hd);
+    const int d4 = tid % H4, j0 = tid / H4, jstep = kAttnThreads / H4;
+    const int64_t col = (int64_t)kvh * hd + 4 * d4;
+    float4 kv[kAttnUnits], vv[kAttnUnits];
+    auto load_batch = [&](int b0, int nb) {
+#pragma unroll
+        for (int i = 0; i < kAttnUnits; ++i) {
+            const int64_t row = (int64_t)(b0 + min(j0 + i * jstep, nb - 1)) * a.kvd + col;
+            kv[i] = *(const float4 *)&a.kcache[row];
+            vv[i] = *(const float4 *)&a.vcache[row];
+        }
+    };
+    load_batch(0, min(NB, a.max_seq));
+    const float *qin = a.qkv + (int64_t)h * hd;
+    const float *kin = a.qkv + a.hidden + kvh * hd;
+    const float *vin = a.qkv + a.hidden + a.kvd + kvh * hd;
+    const int jr = tid < hd ? tid : 0, ir = 2 * (jr % (hd / 2));
+    const float *src = jr < hd / 2 ? qin : kin;
+    const float x0 = src[ir], x1 = src[ir + 1];
+    const float vx = vin[jr];
 
     const int pos = a.pos[0];
     if (pos < 0 || pos >= a.max_seq) {  // cache full: flag it, write nothing
-        if (g == 0 && sl == 0 && tid == 0) a.pos[1] = 1;
+        if (h == 0 && tid == 0) a.pos[1] = 1;
         return;
     }
     const int n = pos + 1;
-    const int chunk = (n + a.S - 1) / a.S;
-    const int t0 = min(n, sl * chunk), t1 = min(n, t0 + chunk);
-
-    // RoPE (interleaved pairs, theta = base^(-i/hd), fp32) on the group's q
-    // heads and on the new k; copy the new v
-    const float *qin = a.qkv + (int64_t)g * rep * hd;
-    const float *kin = a.qkv + a.hidden + g * hd;
-    const float *vin = a.qkv + a.hidden + a.kvd + g * hd;
-    for (int j = tid; j < (rep + 1) * (hd / 2); j += 256) {
-        const int r = j / (hd / 2), i = 2 * (j % (hd / 2));
-        const float theta = powf(a.rope_base, -((float)i / (float)hd));
+    if (tid < hd) {
+        const float theta = powf(a.rope_base, -((float)ir / (float)hd));
         const float ang = (float)pos * theta;
-        const float c = cosf(ang), s = sinf(ang);
-        const float *src = r < rep ? qin + r * hd : kin;
-        float *dst = r < rep ? qs + r * hp : kn;
-        const float x0 = src[i], x1 = src[i + 1];
-        dst[i] = x0 * c - x1 * s;
-        dst[i + 1] = x0 * s + x1 * c;
+        const float c = cosf(ang), sn = sinf(ang);
+        float *dst = jr < hd / 2 ? qs : kn;
+        dst[ir] = x0 * c - x1 * sn;
+        dst[ir + 1] = x0 * sn + x1 * c;
+        vn[tid] = vx;
     }
-    for (int d = tid; d < hd; d += 256) vn[d] = vin[d];
-    for (int r = tid; r < rep; r += 256) {
-        mrun[r] = -INFINITY;
-        lrun[r] = 0.0f;
+    lds_barrier();
+    if (h % rep == 0)
+        for (int d = tid; d < hd; d += kAttnThreads) {
+            a.kcache[(int64_t)pos * a.kvd + kvh * hd + d] = kn[d];
+            a.vcache[(int64_t)pos * a.kvd + kvh * hd + d] = vn[d];
+        }
+    const float4 q4 = *(const float4 *)&qs[4 * d4];
+    const float4 kn4 = *(const float4 *)&kn[4 * d4], vn4 = *(const float4 *)&vn[4 * d4];
+
+    float M = -INFINITY, L = 0.0f;
+    float4 C = float4{0.f, 0.f, 0.f, 0.f};
+    for (int b0 = 0; b0 < n; b0 += NB) {
+        const int nb = min(NB, n - b0);
+        if (b0 > 0) load_batch(b0, nb);
+        // scores of this thread's positions (the hd/4 lanes of a row summed)
+        float sc[kAttnUnits];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < kAttnUnits; ++i) {
+            const int j = j0 + i * jstep;
+            const float4 k4 = b0 + j == pos ? kn4 : kv[i];
+            float dot = q4.x * k4.x;
+            dot = __builtin_fmaf(q4.y, k4.y, dot);
+            dot = __builtin_fmaf(q4.z, k4.z, dot);
+            dot = __builtin_fmaf(q4.w, k4.w, dot);
+            for (int o = 1; o < H4; o <<= 1) dot += __shfl_xor(dot, o);
+            sc[i] = j < nb ? dot * a.scale : -INFINITY;
+            mx = fmaxf(mx, sc[i]);
+        }
+        // block max of the batch
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        if (lane == 0) red[wave] = mx;
+        lds_barrier();
+        mx = red[0];
+        for (int w = 1; w < kAttnThreads / 64; ++w) mx = fmaxf(mx, red[w]);
+        const float mnew = fmaxf(M, mx);
+        const float f = expf(M - mnew);
+        float ps = 0.0f;
+        float4 cb = float4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < kAttnUnits; ++i) {
+            const int j = j0 + i * jstep;
+            const float p = j < nb ? expf(sc[i] - mnew) : 0.0f;
+            const float4 v4 = b0 + j == pos ? vn4 : vv[i];
+            ps += d4 == 0 ? p : 0.0f;  // one copy per position
+            cb.x = __builtin_fmaf(p, v4.x, cb.x);
+            cb.y = __builtin_fmaf(p, v4.y, cb.y);
+            cb.z = __builtin_fmaf(p, v4.z, cb.z);
+            cb.w = __builtin_fmaf(p, v4.w, cb.w);
+        }
+        // block sum of the batch
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ps += __shfl_xor(ps, o);
+        lds_barrier();  // every wave has read red[] (the max)
+        if (lane == 0) red[wave] = ps;
+        lds_barrier();
+        ps = 0.0f;
+        for (int w = 0; w < kAttnThreads / 64; ++w) ps += red[w];
+        L = L * f + ps;
+        M = mnew;
+        C = float4{__builtin_fmaf(C.x, f, cb.x), __builtin_fmaf(C.y, f, cb.y),
+                   __builtin_fmaf(C.z, f, cb.z), __builtin_fmaf(C.w, f, cb.w)};
+        lds_barrier();  // red[] free for the next batch
     }
-    __syncthreads();
-    if (pos >= t0 && pos < t1)
-        for (int d = tid; d < hd; d += 256) {
-            a.kcache[(int64_t)pos * a.kvd + g * hd + d] = kn[d];
-            a.vcache[(int64_t)pos * a.kvd + g * hd + d] = vn[d];
+    // context: sum the partials of the threads that share a float4 column
+    cs[tid] = C;
+    lds_barrier();
+    if (tid < H4) {
+        float4 r = float4{0.f, 0.f, 0.f, 0.f};
+        for (int k = 0; k < jstep; ++k) {
+            const float4 c = cs[tid + k * H4];
+            r.x += c.x;
+            r.y += c.y;
+            r.z += c.z;
+            r.w += c.w;
         }
-
-    // this thread's context accumulator: head r4 = tid / (hd/4), dims 4*(tid % (hd/4))..+3
-    // (rep * hd <= 1024: one float4 per thread)
-    const int pairs4 = rep * hd / 4;
-    float4 acc = float4{0.f, 0.f, 0.f, 0.f};
-    const int lane32 = tid & 31;
-
-    for (int c0 = t0; c0 < t1; c0 += tc) {
-        const int cl = min(tc, t1 - c0);
-        // K, V rows of the tile -> LDS.  All of a thread's global loads go out
-        // first (tc * hd <= 4096: at most four float4 of each per thread, on
-        // clamped in-range rows); row pos is then taken from this block's copy.
-        const int hd4 = hd / 4, nld = cl * hd4;
-        float4 kv[4], vv[4];
-#pragma unroll
-        for (int it = 0; it < 4; ++it) {
-            const int j = min(tid + 256 * it, nld - 1);
-            const int64_t row = (int64_t)(c0 + j / hd4) * a.kvd + g * hd + 4 * (j % hd4);
-            kv[it] = *(const float4 *)&a.kcache[row];
-            vv[it] = *(const float4 *)&a.vcache[row];
-        }
-#pragma unroll
-        for (int it = 0; it < 4; ++it) {
-            const int j = tid + 256 * it;
-            if (j < nld) {
-                const int t = j / hd4, d4 = j % hd4;
-                const bool cur = c0 + t == pos;
-                const float4 kl = *(const float4 *)&kn[4 * d4], vl = *(const float4 *)&vn[4 * d4];
-                *(float4 *)&kb[t * hp + 4 * d4] = cur ? kl : kv[it];
-                *(float4 *)&vb[t * hd + 4 * d4] = cur ? vl : vv[it];
-            }
-        }
-        __syncthreads();
-        // scores of the tile, one (head, position) per thread, d in order
-        for (int j = tid; j < rep * cl; j += 256) {
-            const int r = j / cl, t = j % cl;
-            const float4 *qr = (const float4 *)&qs[r * hp], *kr = (const float4 *)&kb[t * hp];
-            float dot = 0.0f;
-#pragma unroll 4
-            for (int d4 = 0; d4 < hd / 4; ++d4) {
-                const float4 q = qr[d4], k = kr[d4];
-                dot = __builtin_fmaf(q.x, k.x, dot);
-                dot = __builtin_fmaf(q.y, k.y, dot);
-                dot = __builtin_fmaf(q.z, k.z, dot);
-                dot = __builtin_fmaf(q.w, k.w, dot);
-            }
-            sc[r * tc + t] = dot * a.scale;
-        }
-        __syncthreads();
-        // running max and sum per head, 32 lanes per head; sc <- exp(score - max)
-        for (int r0 = 0; r0 < rep; r0 += 8) {
-            const int r = r0 + (tid >> 5);
-            float mx = -INFINITY;
-            if (r < rep)
-                for (int t = lane32; t < cl; t += 32) mx = fmaxf(mx, sc[r * tc + t]);
-#pragma unroll
-            for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 32));
-            float l = 0.0f;
-            if (r < rep) {
-                mx = fmaxf(mx, mrun[r]);
-                for (int t = lane32; t < cl; t += 32) {
-                    const float e = expf(sc[r * tc + t] - mx);
-                    sc[r * tc + t] = e;
-                    l += e;
-                }
-            }
-#pragma unroll
-            for (int o = 16; o > 0; o >>= 1) l += __shfl_xor(l, o, 32);
-            __syncthreads();  // every lane has read mrun[r] before it changes
-            if (r < rep && lane32 == 0) {
-                const float f = expf(mrun[r] - mx);
-                alpha[r] = f;
-                lrun[r] = lrun[r] * f + l;
-                mrun[r] = mx;
-            }
-        }
-        __syncthreads();
-        if (tid < pairs4) {
-            const int r = tid / (hd / 4), d = 4 * (tid % (hd / 4));
-            const float f = alpha[r];
-            float4 v = float4{acc.x * f, acc.y * f, acc.z * f, acc.w * f};
-#pragma unroll 4
-            for (int t = 0; t < cl; ++t) {
-                const float p = sc[r * tc + t];
-                const float4 x = *(const float4 *)&vb[t * hd + d];
-                v.x = __builtin_fmaf(p, x.x, v.x);
-                v.y = __builtin_fmaf(p, x.y, v.y);
-                v.z = __builtin_fmaf(p, x.z, v.z);
-                v.w = __builtin_fmaf(p, x.w, v.w);
-            }
-            acc = v;
-        }
-        __syncthreads();
-    }
-
-    // partials of this slice
-    const int W = hd + 2;
-    if (tid < pairs4) {
-        const int r = tid / (hd / 4), d = 4 * (tid % (hd / 4));
-        float *pp = a.part + ((int64_t)(g * rep + r) * a.S + sl) * W;
-        pp[2 + d] = acc.x;
-        pp[3 + d] = acc.y;
-        pp[4 + d] = acc.z;
-        pp[5 + d] = acc.w;
-        if (d == 0) {
-            pp[0] = mrun[r];
-            pp[1] = lrun[r];
-        }
-    }
-}
-
-// Combines the S slices of attention_step into the context of one query head
-// per block: context = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s.  A
-// kernel of its own, so the slices' writes are visible without device-scope
-// fences in the slice kernel.
-__global__ __launch_bounds__(256) void attention_combine(const AttnParams a) {
-    const int h = blockIdx.x, W = a.hd + 2;
-    if (a.pos[1]) return;  // the slice kernel saw a full cache and wrote nothing
-    const float *pp = a.part + (int64_t)h * a.S * W;
-    for (int d = threadIdx.x; d < a.hd; d += 256) {
-        float m[kMaxSplits], l[kMaxSplits], c[kMaxSplits];
-#pragma unroll
-        for (int j = 0; j < kMaxSplits; ++j) {
-            const bool in = j < a.S;
-            const int jj = in ? j : 0;
-            const float mj = pp[jj * W], lj = pp[jj * W + 1], cj = pp[jj * W + 2 + d];
-            m[j] = in ? mj : -INFINITY;
-            l[j] = in ? lj : 0.0f;
-            c[j] = in ? cj : 0.0f;
-        }
-        float M = -INFINITY;
-#pragma unroll
-        for (int j = 0; j < kMaxSplits; ++j) M = fmaxf(M, m[j]);
-        float L = 0.0f, C = 0.0f;
-#pragma unroll
-        for (int j = 0; j < kMaxSplits; ++j) {
-            const float f = m[j] == -INFINITY ? 0.0f : expf(m[j] - M);
-            L = __builtin_fmaf(f, l[j], L);
-            C = __builtin_fmaf(f, c[j], C);
-        }
-        a.ctx[h * a.hd + d] = C / L;
+        const float inv = 1.0f / L;
+        *(float4 *)&a.ctx[h * hd + 4 * tid] = float4{r.x * inv, r.y * inv, r.z * inv, r.w * inv};
     }
 }
 
@@ -438,11 +379,9 @@ tbh_status tbh_decoder_create(tbh_device *dev, const tbh_decoder_config *cfg, co
         return set_error(TBH_E_UNSUPPORTED,
                          "tbh_decoder_create: needs head_dim % 4 == 0, head_dim <= 256, hidden and "
                          "intermediate multiples of 4, (heads per KV head) * head_dim <= 1024");
-    {
-        const int64_t lds = (int64_t)attn_lds_floats(c.num_heads / c.num_kv_heads, hd) * (int64_t)sizeof(float);
-        if (lds > 64 * 1024)
-            return set_error(TBH_E_UNSUPPORTED, "tbh_decoder_create: attention tile exceeds 64 KiB of LDS");
-    }
+    if (hd > kMaxHd || hd % 16 != 0)
+        return set_error(TBH_E_UNSUPPORTED,
+                         "tbh_decoder_create: attention needs head_dim a multiple of 16, <= 128");
     std::unique_ptr<tbh_decoder> d(new tbh_decoder);
     d->dev = dev;
     d->cfg = c;
@@ -465,11 +404,6 @@ tbh_status tbh_decoder_create(tbh_device *dev, const tbh_decoder_config *cfg, co
     if ((st = dmalloc(d.get(), &d->gu, 2 * (size_t)c.intermediate)) != TBH_OK) return st;
     if ((st = dmalloc(d.get(), &d->logits, (size_t)c.vocab)) != TBH_OK) return st;
     if ((st = dmalloc(d.get(), &d->pos, 2)) != TBH_OK) return st;
-    // attention slices: up to 256 blocks per launch, at least 8 positions each
-    d->attn_splits =
-        std::max(1, std::min({kMaxSplits, 256 / c.num_kv_heads, std::max(1, c.max_seq / 8)}));
-    const size_t part = (size_t)c.num_heads * d->attn_splits * (hd + 2);
-    if ((st = dmalloc(d.get(), &d->attn_part, part)) != TBH_OK) return st;
     if (hipMemcpy(d->emb, embeddings, (size_t)c.vocab * H * sizeof(float), hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(d->norms + 2 * L * H, final_norm, H * sizeof(float), hipMemcpyHostToDevice) != hipSuccess ||
         hipMemset(d->pos, 0, 2 * sizeof(int32_t)) != hipSuccess ||
@@ -576,10 +510,7 @@ tbh_status tbh_decoder_step_device(tbh_decoder *d, int32_t token, float *logits,
     ap.max_seq = c.max_seq;
     ap.rope_base = c.rope_base;
     ap.scale = 1.0f / std::sqrt((float)d->head_dim);
-    ap.part = d->attn_part;
-    ap.S = d->attn_splits;
-    const size_t attn_lds =
-        (size_t)attn_lds_floats(c.num_heads / c.num_kv_heads, d->head_dim) * sizeof(float);
+    const size_t attn_lds = (size_t)attn_lds_floats(d->head_dim) * sizeof(float);
     hipError_t e = hipSuccess;
     for (int32_t l = 0; l < c.num_layers && e == hipSuccess; ++l) {
         const auto &L = d->layers[(size_t)l];
@@ -588,9 +519,7 @@ tbh_status tbh_decoder_step_device(tbh_decoder *d, int32_t token, float *logits,
         if (e != hipSuccess) break;
         ap.kcache = d->kcache + (size_t)l * c.max_seq * d->kv_dim;
         ap.vcache = d->vcache + (size_t)l * c.max_seq * d->kv_dim;
-        hipLaunchKernelGGL(attention_step, dim3((unsigned)c.num_kv_heads, (unsigned)d->attn_splits),
-                           dim3(256), attn_lds, s, ap);
-        hipLaunchKernelGGL(attention_combine, dim3((unsigned)c.num_heads), dim3(256), 0, s, ap);
+        hipLaunchKernelGGL(attention_head, dim3((unsigned)c.num_heads), dim3(kAttnThreads), attn_lds, s, ap);
         e = launch_gemv_fused(*L.o, FusedGemvArgs{d->ctx, nullptr, nullptr, 0.0f, d->h, 0, 1}, s);
         if (e != hipSuccess) break;
         e = launch_gemv_fused(*L.gu, FusedGemvArgs{d->h, nullptr, g_post, c.rms_eps, d->gu, 1, 0}, s);
