@@ -222,6 +222,52 @@ tbh_status tbh_decoder_step_device(tbh_decoder *d, int32_t token, float *logits,
 /* Synchronous step; logits: host [vocab]. */
 tbh_status tbh_decoder_step(tbh_decoder *d, int32_t token, float *logits);
 
+/* ---- TBF v1 model files ------------------------------------------------ */
+/* Reader of the .tbf files ModelWeights.save writes and ModelWeights.load
+ * reads (Sources/TinyBrainRuntime/ModelWeights.swift:376-488, :496-798), and
+ * Scripts/convert_model.py:462-706 writes.  The file is memory-mapped and
+ * every field bounds-checked (malformed: TBH_E_INVALID).  Descriptors and
+ * fp32 pointers point into the mapping and stay valid until tbh_tbf_close. */
+typedef struct tbh_tbf tbh_tbf;
+typedef struct tbh_tbf_config {    /* ModelConfig (ModelRunner.swift:26-120) */
+    int32_t num_layers;
+    int32_t hidden;
+    int32_t num_heads;
+    int32_t num_kv_heads;          /* default num_heads */
+    int32_t vocab;
+    int32_t max_seq;
+    int32_t intermediate;          /* default 4 * hidden */
+    float partial_rotary_factor;   /* default 1.0 */
+    char architecture[16];         /* default "llama" */
+} tbh_tbf_config;
+typedef struct tbh_tbf_tensor_info {
+    const char *name;              /* owned by the file handle */
+    int32_t ndim;
+    int32_t quantized;             /* has a quantization metadata entry */
+    int64_t dims[4];
+    int64_t offset;                /* absolute file offset of the blob */
+    int64_t bytes;
+} tbh_tbf_tensor_info;
+
+tbh_status tbh_tbf_open(const char *path, tbh_tbf **out);
+tbh_status tbh_tbf_close(tbh_tbf *f);
+tbh_status tbh_tbf_get_config(const tbh_tbf *f, tbh_tbf_config *cfg);
+int32_t tbh_tbf_tensor_count(const tbh_tbf *f);
+tbh_status tbh_tbf_tensor(const tbh_tbf *f, int32_t index, tbh_tbf_tensor_info *t);
+tbh_status tbh_tbf_find(const tbh_tbf *f, const char *name, int32_t *index);
+/* The quantized tensor as ModelWeights.load builds it (:676-685): precision
+ * 2 is INT4 (layout NK_FLAT when the converter wrote it, mode byte 3;
+ * KN_FLAT when ModelWeights.save did, mode byte 2); INT8 mode 2 is
+ * per-channel, other INT8 modes symmetric. */
+tbh_status tbh_tbf_qtensor(const tbh_tbf *f, int32_t index, tbh_qtensor_desc *desc);
+tbh_status tbh_tbf_floats(const tbh_tbf *f, int32_t index, const float **data, int64_t *count);
+/* A decoder for a LLaMA-architecture file (ModelWeights.load followed by
+ * ModelRunner): every quantized projection repacked once; max_seq 0 = the
+ * file's maxSeqLen.  TBH_E_UNSUPPORTED for other architectures, biases or an
+ * ungated FFN. */
+tbh_status tbh_tbf_load_decoder(tbh_device *dev, const tbh_tbf *f, int32_t max_seq,
+                                tbh_decoder **out);
+
 /* ---- dequantize (verification) ----------------------------------------- */
 /* Replaces QuantizedTensor.dequantize() (QuantizedTensor.swift:182-286) for
  * the uploaded weight: writes the [K, N] row-major fp32 matrix that the

@@ -154,3 +154,35 @@ def test_decode_runtime_int4_layout_is_unsupported(backend):
         dec.set_layer(0, np.ones(H, np.float32), np.ones(H, np.float32), ws)
     assert e.value.status in (_abi.E_UNSUPPORTED, _abi.E_INVALID)
     dec.close()
+
+
+def _dequant_kn(q: T.QuantizedTensor) -> np.ndarray:
+    """Logical [K, N] fp32 weight of a product QuantizedTensor (oracle dequantize)."""
+    K, N = q.shape
+    if q.layout == T.Layout.NK_FLAT:
+        oq = O.QTensor((N, K), q.data, q.scales, q.zeroPoints, int(q.mode), int(q.precision), q.groupSize)
+        return np.ascontiguousarray(O.dequantize(oq).T)
+    oq = O.QTensor((K, N), q.data, q.scales, q.zeroPoints, int(q.mode), int(q.precision), q.groupSize)
+    return O.dequantize(oq)
+
+
+@pytest.mark.parametrize("fname", ["converter_tiny_int8.tbf", "converter_tiny_int4.tbf"])
+def test_decode_from_converter_tbf_file(backend, fname):
+    # ModelWeights.load + ModelRunner.step on a file the reference converter wrote
+    import os
+
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", fname)
+    with T.TBFFile(path) as f:
+        c = f.config
+        dec = f.load_decoder(backend, max_seq=16)
+        names = ["attn_q", "attn_k", "attn_v", "attn_o", "ffn_gate", "ffn_up", "ffn_down"]
+        layers = [RefLayer(f.floats(f"layer_{l}_ln_input"), f.floats(f"layer_{l}_ln_post"),
+                           [_dequant_kn(f.quantized(f"layer_{l}_{n}")) for n in names])
+                  for l in range(c["numLayers"])]
+        ref = RefDecoder(c["numLayers"], c["hiddenDim"], c["numHeads"], c["numKVHeads"],
+                         c["intermediateDim"], c["vocabSize"], f.floats("embeddings"),
+                         f.floats("final_norm"), _dequant_kn(f.quantized("output")), layers)
+        for i, tok in enumerate([3, 39, 0, 17, 17]):
+            y, r = dec.step(tok), ref.step(tok)
+            assert _gated(y, r) <= GATE, (fname, i, _gated(y, r))
+        dec.close()

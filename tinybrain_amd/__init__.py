@@ -14,9 +14,10 @@ from .quantized import (Layout, PreconditionFailure, QuantizationMode,  # noqa: 
                         unpack_int4_array, pack_int4_array)
 from .backend import DeviceWeight, HIPBackend, HIPBackendError  # noqa: F401
 from .decoder import Decoder, DecoderConfig  # noqa: F401
+from .tbf import TBFFile  # noqa: F401
 
 __all__ = [
-    "HIPBackend", "HIPBackendError", "DeviceWeight", "QuantizedTensor", "Decoder", "DecoderConfig",
+    "HIPBackend", "HIPBackendError", "DeviceWeight", "QuantizedTensor", "Decoder", "DecoderConfig", "TBFFile",
     "QuantizationMode", "QuantizationPrecision", "Layout", "PreconditionFailure",
     "quantize", "quantize_int4_flat", "packInt4", "unpackInt4",
 ]

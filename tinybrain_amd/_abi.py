@@ -29,6 +29,8 @@ EXPORTS = [
     "tbh_decoder_create", "tbh_decoder_set_layer", "tbh_decoder_destroy",
     "tbh_decoder_set_position", "tbh_decoder_get_position",
     "tbh_decoder_step_device", "tbh_decoder_step",
+    "tbh_tbf_open", "tbh_tbf_close", "tbh_tbf_get_config", "tbh_tbf_tensor_count",
+    "tbh_tbf_tensor", "tbh_tbf_find", "tbh_tbf_qtensor", "tbh_tbf_floats", "tbh_tbf_load_decoder",
 ]
 
 
@@ -78,6 +80,31 @@ class DecoderConfig(ctypes.Structure):
     ]
 
 
+class TBFConfig(ctypes.Structure):
+    _fields_ = [
+        ("num_layers", ctypes.c_int32),
+        ("hidden", ctypes.c_int32),
+        ("num_heads", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("vocab", ctypes.c_int32),
+        ("max_seq", ctypes.c_int32),
+        ("intermediate", ctypes.c_int32),
+        ("partial_rotary_factor", ctypes.c_float),
+        ("architecture", ctypes.c_char * 16),
+    ]
+
+
+class TBFTensor(ctypes.Structure):
+    _fields_ = [
+        ("name", ctypes.c_char_p),
+        ("ndim", ctypes.c_int32),
+        ("quantized", ctypes.c_int32),
+        ("dims", ctypes.c_int64 * 4),
+        ("offset", ctypes.c_int64),
+        ("bytes", ctypes.c_int64),
+    ]
+
+
 _lib = None
 
 
@@ -122,6 +149,19 @@ def lib() -> ctypes.CDLL:
     L.tbh_decoder_get_position.argtypes = [vp, ctypes.POINTER(i32)]
     L.tbh_decoder_step_device.argtypes = [vp, i32, vp, vp]
     L.tbh_decoder_step.argtypes = [vp, i32, vp]
+    L.tbh_tbf_open.argtypes = [ctypes.c_char_p, pp]
+    L.tbh_tbf_close.argtypes = [vp]
+    L.tbh_tbf_get_config.argtypes = [vp, ctypes.POINTER(TBFConfig)]
+    L.tbh_tbf_tensor_count.argtypes = [vp]
+    L.tbh_tbf_tensor_count.restype = i32
+    L.tbh_tbf_tensor.argtypes = [vp, i32, ctypes.POINTER(TBFTensor)]
+    L.tbh_tbf_find.argtypes = [vp, ctypes.c_char_p, ctypes.POINTER(i32)]
+    L.tbh_tbf_qtensor.argtypes = [vp, i32, dp]
+    L.tbh_tbf_floats.argtypes = [vp, i32, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(i64)]
+    L.tbh_tbf_load_decoder.argtypes = [vp, vp, i32, pp]
+    for name in ("tbh_tbf_open", "tbh_tbf_close", "tbh_tbf_get_config", "tbh_tbf_tensor",
+                 "tbh_tbf_find", "tbh_tbf_qtensor", "tbh_tbf_floats", "tbh_tbf_load_decoder"):
+        getattr(L, name).restype = i32
     for name in ("tbh_decoder_create", "tbh_decoder_set_layer", "tbh_decoder_destroy",
                  "tbh_decoder_set_position", "tbh_decoder_get_position",
                  "tbh_decoder_step_device", "tbh_decoder_step"):

@@ -65,6 +65,16 @@ class Decoder:
         _check(self._lib.tbh_decoder_create(backend._dev, ctypes.byref(cfg), emb.ctypes.data,
                                             fn.ctypes.data, ctypes.byref(desc), ctypes.byref(self._h)))
 
+    @classmethod
+    def _adopt(cls, backend: HIPBackend, config: DecoderConfig, handle: ctypes.c_void_p) -> "Decoder":
+        """Wrap a decoder the library built (tbh_tbf_load_decoder)."""
+        d = cls.__new__(cls)
+        d._lib = _abi.lib()
+        d.backend = backend
+        d.config = config
+        d._h = handle
+        return d
+
     def set_layer(self, layer: int, input_norm: np.ndarray, post_attention_norm: np.ndarray,
                   projections: Sequence[QuantizedTensor]) -> None:
         """projections: q, k, v, o, gate, up, down (TransformerLayerWeights)."""
