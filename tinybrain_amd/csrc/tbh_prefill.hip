@@ -31,6 +31,7 @@ typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kBK = 64;           // K per staged step (two MFMA K-steps of 32)
 constexpr int kRowPad = 8;        // bf16 of padding per LDS row (16 bytes)
 constexpr int kLdsRow = kBK + kRowPad;
+constexpr int kDepth = 2;         // K steps whose global loads are in flight at once
 
 struct PParams {
     const uint16_t *x;   // bf16 bits, [M][ldx]
@@ -70,7 +71,7 @@ __device__ __forceinline__ float trunc_bf16(float v) {
     return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v) & 0xFFFF0000u);
 }
 
-template <int PREC, int BM, int BN>
+template <int PREC, int BM, int BN, bool ZP>
 __global__ __launch_bounds__(256) void gemm_bf16(const PParams p) {
     constexpr int CE = PREC == 8 ? 16 : 32;       // elements per chunk
     constexpr int NS = PREC == 8 ? 1 : 3;         // bf16 pieces per weight
@@ -91,22 +92,26 @@ __global__ __launch_bounds__(256) void gemm_bf16(const PParams p) {
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
     const int nsteps = (p.chunks * CE + kBK - 1) / kBK;
 
-    // ---- global -> registers for one step
-    u32x4 xr[XPT];
-    u32x4 wr[WPT];
-    float sr[WPT];
-    float zr[WPT];
-    auto load_step = [&](int t) {
+    // ---- global -> registers for one step, into register stage d of kDepth:
+    // the loads of steps t+1 .. t+kDepth-1 are in flight while step t runs
+    u32x4 xr[kDepth][XPT];
+    bool xin[kDepth][XPT];   // segment within K, applied at the LDS store
+    u32x4 wr[kDepth][WPT];
+    float sr[kDepth][WPT];
+    int8_t zq[kDepth][WPT];
+    // Only addresses are computed here; everything that uses a loaded value
+    // (masks, conversions) happens in store_step, kDepth - 1 steps later.
+    auto load_step = [&](int t, int d) {
         const int k0 = t * kBK;
 #pragma unroll
         for (int j = 0; j < XPT; ++j) {
             const int s = tid + 256 * j;
             const int row = s / (kBK / 8), kq = s % (kBK / 8);
-            const int m = m0 + row, k = k0 + 8 * kq;
-            const bool in = m < p.M && k < p.K;  // K % 8 == 0: a segment is all in or out
-            const uint16_t *src = p.x + (int64_t)(in ? m : 0) * p.ldx + (in ? k : 0);
-            const u32x4 v = *(const u32x4 *)src;
-            xr[j] = in ? v : u32x4{0, 0, 0, 0};
+            const int m = min(m0 + row, p.M - 1), k = k0 + 8 * kq;
+            // K % 8 == 0: a segment is all in or out.  Rows past M read row
+            // M-1 (finite values; their outputs are never stored).
+            xin[d][j] = k < p.K;
+            xr[d][j] = *(const u32x4 *)(p.x + (int64_t)m * p.ldx + (k < p.K ? k : 0));
         }
 #pragma unroll
         for (int j = 0; j < WPT; ++j) {
@@ -114,30 +119,27 @@ __global__ __launch_bounds__(256) void gemm_bf16(const PParams p) {
             const int row = s / CPR, c = t * CPR + s % CPR;
             const int n = n0 + row;
             const bool in = s < WCH && n < p.Np && c < p.chunks;
+            // Out-of-range chunks read a valid chunk: rows past N are never
+            // stored and K padding meets x = 0, so the values do not matter.
             const int64_t nn = in ? n : 0, cc = in ? c : 0;
-            const u32x4 v = __builtin_nontemporal_load(
-                (const u32x4 *)(p.data + nn * p.row_bytes + cc * 16));
-            wr[j] = in ? v : u32x4{PREC == 8 ? 0x80808080u : 0x88888888u,
-                                   PREC == 8 ? 0x80808080u : 0x88888888u,
-                                   PREC == 8 ? 0x80808080u : 0x88888888u,
-                                   PREC == 8 ? 0x80808080u : 0x88888888u};  // q = 0
+            wr[d][j] = __builtin_nontemporal_load((const u32x4 *)(p.data + nn * p.row_bytes + cc * 16));
             if (PREC == 4) {
                 const int64_t gi = nn * p.G + cc / p.cpg;
-                sr[j] = p.scales[gi];
-                zr[j] = p.zp ? (float)p.zp[gi] : 0.0f;
-            } else {
-                zr[j] = p.zp ? (float)p.zp[nn] : 0.0f;
+                sr[d][j] = p.scales[gi];
+                if (ZP) zq[d][j] = p.zp[gi];
+            } else if (ZP) {
+                zq[d][j] = p.zp[nn];
             }
         }
     };
 
     // ---- registers -> LDS (x as is; weights dequantized to bf16 pieces)
-    auto store_step = [&]() {
+    auto store_step = [&](int d) {
 #pragma unroll
         for (int j = 0; j < XPT; ++j) {
             const int s = tid + 256 * j;
             const int row = s / (kBK / 8), kq = s % (kBK / 8);
-            *(u32x4 *)&xs[row * kLdsRow + 8 * kq] = xr[j];
+            *(u32x4 *)&xs[row * kLdsRow + 8 * kq] = xin[d][j] ? xr[d][j] : u32x4{0, 0, 0, 0};
         }
 #pragma unroll
         for (int j = 0; j < WPT; ++j) {
@@ -147,28 +149,28 @@ __global__ __launch_bounds__(256) void gemm_bf16(const PParams p) {
                 uint16_t *dst = &ws[row * kLdsRow + cl * CE];
                 if (PREC == 8) {
                     // bytes {0,2,1,3} of each word are k+{0,1,2,3}; value u - 128 - zp
-                    const float off = 128.0f + zr[j];
+                    const float off = 128.0f + (ZP ? (float)zq[d][j] : 0.0f);
                     uint32_t o[8];
 #pragma unroll
-                    for (int d = 0; d < 4; ++d) {
-                        const uint32_t w = wr[j][d];
+                    for (int q = 0; q < 4; ++q) {
+                        const uint32_t w = wr[d][j][q];
                         const float f0 = ubyte<0>(w) - off;
                         const float f1 = ubyte<2>(w) - off;
                         const float f2 = ubyte<1>(w) - off;
                         const float f3 = ubyte<3>(w) - off;
-                        o[2 * d] = pack_hi16(f0, f1);
-                        o[2 * d + 1] = pack_hi16(f2, f3);
+                        o[2 * q] = pack_hi16(f0, f1);
+                        o[2 * q + 1] = pack_hi16(f2, f3);
                     }
                     *(u32x4 *)dst = u32x4{o[0], o[1], o[2], o[3]};
                     *(u32x4 *)(dst + 8) = u32x4{o[4], o[5], o[6], o[7]};
                 } else {
                     // nibble of k % 8 at bit {0,16,4,20,8,24,12,28}; value
                     // (u - 8 - zp) * scale, one fp32 rounding
-                    const float off = 8.0f + zr[j];
-                    const float sc = sr[j];
+                    const float off = 8.0f + (ZP ? (float)zq[d][j] : 0.0f);
+                    const float sc = sr[d][j];
 #pragma unroll
-                    for (int d = 0; d < 4; ++d) {
-                        const uint32_t w = wr[j][d];
+                    for (int q = 0; q < 4; ++q) {
+                        const uint32_t w = wr[d][j][q];
                         uint32_t oh[4], om[4], ol[4];
 #pragma unroll
                         for (int e = 0; e < 8; e += 2) {
@@ -182,9 +184,9 @@ __global__ __launch_bounds__(256) void gemm_bf16(const PParams p) {
                             om[e >> 1] = pack_hi16(g0, g1);
                             ol[e >> 1] = pack_hi16(r0 - g0, r1 - g1);
                         }
-                        *(u32x4 *)(dst + 8 * d) = u32x4{oh[0], oh[1], oh[2], oh[3]};
-                        *(u32x4 *)(dst + BN * kLdsRow + 8 * d) = u32x4{om[0], om[1], om[2], om[3]};
-                        *(u32x4 *)(dst + 2 * BN * kLdsRow + 8 * d) = u32x4{ol[0], ol[1], ol[2], ol[3]};
+                        *(u32x4 *)(dst + 8 * q) = u32x4{oh[0], oh[1], oh[2], oh[3]};
+                        *(u32x4 *)(dst + BN * kLdsRow + 8 * q) = u32x4{om[0], om[1], om[2], om[3]};
+                        *(u32x4 *)(dst + 2 * BN * kLdsRow + 8 * q) = u32x4{ol[0], ol[1], ol[2], ol[3]};
                     }
                 }
             }
@@ -197,31 +199,40 @@ __global__ __launch_bounds__(256) void gemm_bf16(const PParams p) {
 #pragma unroll
         for (int b = 0; b < TN; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    load_step(0);
-    for (int t = 0; t < nsteps; ++t) {
-        store_step();
-        lds_barrier();
-        if (t + 1 < nsteps) load_step(t + 1);
+    // Steps are padded to a multiple of kDepth and every iteration loads and
+    // computes unconditionally: steps past K read clamped addresses and meet
+    // x = 0, so they add nothing, and the loop body has no branches at which
+    // the compiler would have to wait for every load in flight.
+    const int nsteps_pad = ((nsteps + kDepth - 1) / kDepth) * kDepth;
 #pragma unroll
-        for (int ks = 0; ks < kBK / 32; ++ks) {
-            const int kofs = ks * 32 + 8 * (lane >> 4);
-            bf16x8 af[TM];
+    for (int d = 0; d < kDepth; ++d) load_step(d, d);
+    for (int t0 = 0; t0 < nsteps_pad; t0 += kDepth) {
 #pragma unroll
-            for (int a = 0; a < TM; ++a)
-                af[a] = *(const bf16x8 *)&xs[(wm * WM + a * 16 + (lane & 15)) * kLdsRow + kofs];
+        for (int d = 0; d < kDepth; ++d) {
+            store_step(d);
+            lds_barrier();
+            load_step(t0 + d + kDepth, d);
 #pragma unroll
-            for (int ps = 0; ps < NS; ++ps) {
+            for (int ks = 0; ks < kBK / 32; ++ks) {
+                const int kofs = ks * 32 + 8 * (lane >> 4);
+                bf16x8 af[TM];
 #pragma unroll
-                for (int b = 0; b < TN; ++b) {
-                    const bf16x8 bfr = *(const bf16x8 *)&ws[ps * BN * kLdsRow +
-                                                            (wn * WN + b * 16 + (lane & 15)) * kLdsRow + kofs];
+                for (int a = 0; a < TM; ++a)
+                    af[a] = *(const bf16x8 *)&xs[(wm * WM + a * 16 + (lane & 15)) * kLdsRow + kofs];
 #pragma unroll
-                    for (int a = 0; a < TM; ++a)
-                        acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[a], bfr, acc[a][b], 0, 0, 0);
+                for (int ps = 0; ps < NS; ++ps) {
+#pragma unroll
+                    for (int b = 0; b < TN; ++b) {
+                        const bf16x8 bfr = *(const bf16x8 *)&ws[ps * BN * kLdsRow +
+                                                                (wn * WN + b * 16 + (lane & 15)) * kLdsRow + kofs];
+#pragma unroll
+                        for (int a = 0; a < TM; ++a)
+                            acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[a], bfr, acc[a][b], 0, 0, 0);
+                    }
                 }
             }
+            lds_barrier();
         }
-        lds_barrier();
     }
 
     // ---- epilogue: lane holds C[4 (lane / 16) + e][lane % 16] of each tile
@@ -243,7 +254,10 @@ __global__ __launch_bounds__(256) void gemm_bf16(const PParams p) {
 template <int PREC, int BM, int BN>
 hipError_t launch_tile(const PParams &p, hipStream_t s) {
     const dim3 grid((unsigned)((p.Np + BN - 1) / BN), (unsigned)((p.M + BM - 1) / BM));
-    hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN>), grid, dim3(256), 0, s, p);
+    if (p.zp)
+        hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, true>), grid, dim3(256), 0, s, p);
+    else
+        hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, false>), grid, dim3(256), 0, s, p);
     return hipGetLastError();
 }
 
