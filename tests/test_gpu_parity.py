@@ -389,6 +389,52 @@ def test_prefill_bf16_zero_points_and_groups(backend):
     _prefill_check(backend, _product(q0, (256, 40), T.Layout.NK_FLAT), q0, 64, seed=17)
 
 
+def test_prefill_bf16_split_k_determinism_and_graphs(backend):
+    # M = 64 gives fewer output tiles than CUs, so the launch splits K and
+    # sums the splits in a second kernel, in a fixed order.
+    import torch
+
+    K, N, M = 5632, 2048, 64
+    oq = _int4_nk(101, K, N, 32)
+    w = backend.weight(_product(oq, (K, N), T.Layout.NK_FLAT))
+    xb = torch.from_numpy(O.fill_normal(19, M * K).reshape(M, K)).to(torch.bfloat16)
+    ref = O.gemm_f64(xb.float().numpy(), _oracle_weight(oq, T.Layout.NK_FLAT))
+    x = xb.cuda()
+    a = backend.matmul_bf16_device(x, w)
+    b = backend.matmul_bf16_device(x, w)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(a.cpu().numpy(), b.cpu().numpy())
+    assert O.parity_errors(a.cpu().numpy(), ref)["gated"] <= GATE
+
+    # Captured on a stream that has no workspace yet: the launch runs unsplit.
+    # Captured again after an eager call has sized it: the split launch.
+    s = torch.cuda.Stream()
+    y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    for phase in range(2):
+        if phase == 1:
+            with torch.cuda.stream(s):
+                backend.matmul_bf16_device(x, w, out=y)
+            torch.cuda.synchronize()
+            eager = y.cpu().numpy().copy()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            backend.matmul_bf16_device(x, w, out=y)
+        first = None
+        for _ in range(3):
+            y.zero_()
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            got = y.cpu().numpy()
+            assert O.parity_errors(got, ref)["gated"] <= GATE, phase
+            if first is None:
+                first = got.copy()
+            np.testing.assert_array_equal(got, first)
+        if phase == 1:
+            np.testing.assert_array_equal(first, eager)
+        del g
+
+
 def test_prefill_bf16_unsupported(backend):
     import torch
 

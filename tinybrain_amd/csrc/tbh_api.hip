@@ -118,6 +118,10 @@ tbh_status tbh_device_close(tbh_device *dev) {
     use_device(dev->ordinal);
     if (dev->stream) hipStreamSynchronize(dev->stream);
     if (dev->stage) hipFree(dev->stage);
+    for (auto &ws : dev->workspaces) {
+        hipStreamSynchronize(ws.stream);
+        hipFree(ws.ptr);
+    }
     if (dev->stream) hipStreamDestroy(dev->stream);
     delete dev;
     return TBH_OK;
@@ -590,6 +594,31 @@ bool weight_arrays_ok(const tbh_weight &w) {
         return w.n_scales_dev == nb * w.Kp;
     }
     return false;
+}
+
+void *stream_workspace(tbh_device *dev, hipStream_t s, size_t bytes) {
+    std::lock_guard<std::mutex> lock(dev->ws_mu);
+    tbh_device::Workspace *ws = nullptr;
+    for (auto &e : dev->workspaces)
+        if (e.stream == s) ws = &e;
+    if (ws && ws->bytes >= bytes) return ws->ptr;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return nullptr;
+    if (!ws) {
+        dev->workspaces.push_back({s, nullptr, 0});
+        ws = &dev->workspaces.back();
+    }
+    // The previous buffer may still be read by work queued on this stream.
+    if (ws->ptr && (hipStreamSynchronize(s) != hipSuccess || hipFree(ws->ptr) != hipSuccess)) return nullptr;
+    ws->ptr = nullptr;
+    ws->bytes = 0;
+    const size_t grown = (bytes + (size_t(1) << 20) - 1) & ~((size_t(1) << 20) - 1);
+    if (hipMalloc(&ws->ptr, grown) != hipSuccess) {
+        ws->ptr = nullptr;
+        return nullptr;
+    }
+    ws->bytes = grown;
+    return ws->ptr;
 }
 }  // namespace tbh
 

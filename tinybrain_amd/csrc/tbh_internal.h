@@ -6,6 +6,7 @@
 #include <cstdint>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "tinybrain_hip.h"
 
@@ -43,6 +44,16 @@ struct tbh_device {
     std::mutex mu;               // serialises tbh_matmul / tbh_dequantize
     void *stage = nullptr;       // device staging for the host-pointer calls
     size_t stage_bytes = 0;
+
+    // Per-stream device workspaces (split-K partial sums of the prefill
+    // GEMM): calls on different streams never share one.
+    struct Workspace {
+        hipStream_t stream;
+        void *ptr;
+        size_t bytes;
+    };
+    std::mutex ws_mu;
+    std::vector<Workspace> workspaces;
 };
 
 struct tbh_weight {
@@ -131,6 +142,12 @@ hipError_t launch_generic(const tbh_weight &w, const GemvArgs &a, hipStream_t s)
 bool prefill_supported(const tbh_weight &w);
 hipError_t launch_prefill(const tbh_weight &w, const uint16_t *x, int64_t ldx, int64_t M, float *y,
                           int64_t ldy, hipStream_t s);
+
+// Device workspace of at least `bytes` owned by (dev, stream), grown on
+// demand (tbh_api.hip).  Growing synchronises the stream first.  Returns
+// nullptr when it would have to grow while the stream is being captured into
+// a graph, or when the allocation fails.
+void *stream_workspace(tbh_device *dev, hipStream_t s, size_t bytes);
 
 // Bit-exact dequantization to [K, N] row-major (tbh_ref_kernels.hip).
 hipError_t launch_dequant(const tbh_weight &w, float *out, hipStream_t s);

@@ -14,12 +14,16 @@
 // run.  Weight operands are exact:
 //   * INT8 (one scale per row): q - zp is an integer of magnitude <= 255,
 //     exact in bf16; the row scale multiplies the fp32 result once.
-//   * INT4 K-groups: v = (q - zp) * scale is formed in fp32 with the
-//     reference's single rounding, then split into three bf16 pieces
-//     v = hi + mid + lo by truncation (24 significant bits), and each piece
-//     is one MFMA.  The products x * piece are exact in fp32.
-// Accumulation is fp32 in the MFMA.
+//   * INT4 K-groups: groups are whole multiples of 32 along K, so each
+//     32-deep MFMA K-slice lies in one group.  The slice's MFMA takes the
+//     integer q - zp (exact in bf16) into a zeroed accumulator, and the
+//     group scale multiplies that partial product once before it is added
+//     to the tile's accumulator.
+// Accumulation is fp32.
 #include "tbh_internal.h"
+
+#include <algorithm>
+#include <cstdlib>
 
 namespace tbh {
 namespace {
@@ -36,8 +40,10 @@ constexpr int kDepth = 2;         // K steps whose global loads are in flight at
 struct PParams {
     const uint16_t *x;   // bf16 bits, [M][ldx]
     int64_t ldx;
-    float *y;
+    float *y;            // [M][ldy]; with split-K, split z writes y + z * split_stride
     int64_t ldy;
+    int64_t split_stride;
+    int32_t split_steps; // K steps per split (a multiple of kDepth)
     const uint8_t *data;
     int64_t row_bytes;
     const float *scales;
@@ -67,14 +73,9 @@ __device__ __forceinline__ float ubyte(uint32_t w) {
     return (float)((w >> (8 * J)) & 0xFFu);
 }
 
-__device__ __forceinline__ float trunc_bf16(float v) {
-    return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v) & 0xFFFF0000u);
-}
-
 template <int PREC, int BM, int BN, bool ZP>
 __global__ __launch_bounds__(256) void gemm_bf16(const PParams p) {
     constexpr int CE = PREC == 8 ? 16 : 32;       // elements per chunk
-    constexpr int NS = PREC == 8 ? 1 : 3;         // bf16 pieces per weight
     constexpr int CPR = kBK / CE;                 // chunks per row per step
     constexpr int WCH = BN * CPR;                 // weight chunks per step
     constexpr int WPT = (WCH + 255) / 256;        // per thread (last may idle)
@@ -85,12 +86,24 @@ __global__ __launch_bounds__(256) void gemm_bf16(const PParams p) {
     static_assert(XSEG % 256 == 0, "BM must be a multiple of 32");
 
     __shared__ __attribute__((aligned(16))) uint16_t xs[BM * kLdsRow];
-    __shared__ __attribute__((aligned(16))) uint16_t ws[NS * BN * kLdsRow];
+    __shared__ __attribute__((aligned(16))) uint16_t ws[BN * kLdsRow];
+    __shared__ float ssc[PREC == 4 ? BN * CPR : 1];   // INT4: scale of each (row, K-slice)
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int wm = wave >> 1, wn = wave & 1;
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
     const int nsteps = (p.chunks * CE + kBK - 1) / kBK;
+    // This block's K steps [t_begin, t_end); x past kend reads as zero, so
+    // the padded steps at a split's end add nothing.
+    const int t_begin = blockIdx.z * p.split_steps;
+    const int t_end = min(nsteps, t_begin + p.split_steps);
+    const int kend = min(p.K, t_end * kBK);
+
+    // INT8 row scales of this lane's output columns, loaded before the K loop
+    float scn[TN];
+#pragma unroll
+    for (int b = 0; b < TN; ++b)
+        scn[b] = PREC == 8 ? p.scales[min(n0 + wn * WN + b * 16 + (lane & 15), p.Np - 1)] : 1.0f;
 
     // ---- global -> registers for one step, into register stage d of kDepth:
     // the loads of steps t+1 .. t+kDepth-1 are in flight while step t runs
@@ -110,7 +123,7 @@ __global__ __launch_bounds__(256) void gemm_bf16(const PParams p) {
             const int m = min(m0 + row, p.M - 1), k = k0 + 8 * kq;
             // K % 8 == 0: a segment is all in or out.  Rows past M read row
             // M-1 (finite values; their outputs are never stored).
-            xin[d][j] = k < p.K;
+            xin[d][j] = k < kend;
             xr[d][j] = *(const u32x4 *)(p.x + (int64_t)m * p.ldx + (k < p.K ? k : 0));
         }
 #pragma unroll
@@ -164,30 +177,20 @@ __global__ __launch_bounds__(256) void gemm_bf16(const PParams p) {
                     *(u32x4 *)dst = u32x4{o[0], o[1], o[2], o[3]};
                     *(u32x4 *)(dst + 8) = u32x4{o[4], o[5], o[6], o[7]};
                 } else {
-                    // nibble of k % 8 at bit {0,16,4,20,8,24,12,28}; value
-                    // (u - 8 - zp) * scale, one fp32 rounding
+                    // nibble of k % 8 at bit {0,16,4,20,8,24,12,28}; value u - 8 - zp
                     const float off = 8.0f + (ZP ? (float)zq[d][j] : 0.0f);
-                    const float sc = sr[d][j];
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
                         const uint32_t w = wr[d][j][q];
-                        uint32_t oh[4], om[4], ol[4];
+                        uint32_t o[4];
 #pragma unroll
-                        for (int e = 0; e < 8; e += 2) {
-                            const int sh0 = ((e >> 1) << 2), sh1 = 16 + ((e >> 1) << 2);
-                            const float v0 = __fmul_rn((float)((w >> sh0) & 15u) - off, sc);
-                            const float v1 = __fmul_rn((float)((w >> sh1) & 15u) - off, sc);
-                            const float h0 = trunc_bf16(v0), h1 = trunc_bf16(v1);
-                            const float r0 = v0 - h0, r1 = v1 - h1;
-                            const float g0 = trunc_bf16(r0), g1 = trunc_bf16(r1);
-                            oh[e >> 1] = pack_hi16(h0, h1);
-                            om[e >> 1] = pack_hi16(g0, g1);
-                            ol[e >> 1] = pack_hi16(r0 - g0, r1 - g1);
+                        for (int e = 0; e < 4; ++e) {
+                            const uint32_t u = (w >> (4 * e)) & 0x000F000Fu;
+                            o[e] = pack_hi16(ubyte<0>(u) - off, ubyte<2>(u) - off);
                         }
-                        *(u32x4 *)(dst + 8 * q) = u32x4{oh[0], oh[1], oh[2], oh[3]};
-                        *(u32x4 *)(dst + BN * kLdsRow + 8 * q) = u32x4{om[0], om[1], om[2], om[3]};
-                        *(u32x4 *)(dst + 2 * BN * kLdsRow + 8 * q) = u32x4{ol[0], ol[1], ol[2], ol[3]};
+                        *(u32x4 *)(dst + 8 * q) = u32x4{o[0], o[1], o[2], o[3]};
                     }
+                    ssc[s] = sr[d][j];
                 }
             }
         }
@@ -203,10 +206,10 @@ __global__ __launch_bounds__(256) void gemm_bf16(const PParams p) {
     // computes unconditionally: steps past K read clamped addresses and meet
     // x = 0, so they add nothing, and the loop body has no branches at which
     // the compiler would have to wait for every load in flight.
-    const int nsteps_pad = ((nsteps + kDepth - 1) / kDepth) * kDepth;
+    const int t_stop = t_begin + ((t_end - t_begin + kDepth - 1) / kDepth) * kDepth;
 #pragma unroll
-    for (int d = 0; d < kDepth; ++d) load_step(d, d);
-    for (int t0 = 0; t0 < nsteps_pad; t0 += kDepth) {
+    for (int d = 0; d < kDepth; ++d) load_step(t_begin + d, d);
+    for (int t0 = t_begin; t0 < t_stop; t0 += kDepth) {
 #pragma unroll
         for (int d = 0; d < kDepth; ++d) {
             store_step(d);
@@ -220,14 +223,22 @@ __global__ __launch_bounds__(256) void gemm_bf16(const PParams p) {
                 for (int a = 0; a < TM; ++a)
                     af[a] = *(const bf16x8 *)&xs[(wm * WM + a * 16 + (lane & 15)) * kLdsRow + kofs];
 #pragma unroll
-                for (int ps = 0; ps < NS; ++ps) {
-#pragma unroll
-                    for (int b = 0; b < TN; ++b) {
-                        const bf16x8 bfr = *(const bf16x8 *)&ws[ps * BN * kLdsRow +
-                                                                (wn * WN + b * 16 + (lane & 15)) * kLdsRow + kofs];
+                for (int b = 0; b < TN; ++b) {
+                    const int wrow = wn * WN + b * 16 + (lane & 15);
+                    const bf16x8 bfr = *(const bf16x8 *)&ws[wrow * kLdsRow + kofs];
+                    if (PREC == 8) {
 #pragma unroll
                         for (int a = 0; a < TM; ++a)
                             acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[a], bfr, acc[a][b], 0, 0, 0);
+                    } else {
+                        const float sc = ssc[wrow * CPR + ks];
+#pragma unroll
+                        for (int a = 0; a < TM; ++a) {
+                            const f32x4 part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                af[a], bfr, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) acc[a][b][e] = __builtin_fmaf(part[e], sc, acc[a][b][e]);
+                        }
                     }
                 }
             }
@@ -236,24 +247,61 @@ __global__ __launch_bounds__(256) void gemm_bf16(const PParams p) {
     }
 
     // ---- epilogue: lane holds C[4 (lane / 16) + e][lane % 16] of each tile
+    float *out = p.y + (int64_t)blockIdx.z * p.split_stride;
+    const int mrow = m0 + wm * WM + 4 * (lane >> 4), ncol = n0 + wn * WN + (lane & 15);
+    if (m0 + BM <= p.M && n0 + BN <= p.N) {
+        // whole tile in range: no per-element branches
 #pragma unroll
-    for (int b = 0; b < TN; ++b) {
-        const int n = n0 + wn * WN + b * 16 + (lane & 15);
-        if (n >= p.N) continue;
-        const float sc = PREC == 8 ? p.scales[n] : 1.0f;
+        for (int b = 0; b < TN; ++b)
 #pragma unroll
-        for (int a = 0; a < TM; ++a)
+            for (int a = 0; a < TM; ++a)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int m = m0 + wm * WM + a * 16 + 4 * (lane >> 4) + e;
-                if (m < p.M) p.y[(int64_t)m * p.ldy + n] = PREC == 8 ? acc[a][b][e] * sc : acc[a][b][e];
-            }
+                for (int e = 0; e < 4; ++e)
+                    out[(int64_t)(mrow + a * 16 + e) * p.ldy + ncol + b * 16] = acc[a][b][e] * scn[b];
+    } else {
+#pragma unroll
+        for (int b = 0; b < TN; ++b) {
+            const int n = ncol + b * 16;
+            if (n >= p.N) continue;
+#pragma unroll
+            for (int a = 0; a < TM; ++a)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int m = mrow + a * 16 + e;
+                    if (m < p.M) out[(int64_t)m * p.ldy + n] = acc[a][b][e] * scn[b];
+                }
+        }
+    }
+}
+
+// y = sum over splits of the partial tiles, in split order (deterministic).
+__global__ __launch_bounds__(256) void split_sum4(const float4 *__restrict__ part, int64_t stride4, int splits,
+                                                  float4 *__restrict__ y, int64_t n4) {
+    for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256) {
+        float4 v = part[i];
+        for (int z = 1; z < splits; ++z) {
+            const float4 u = part[z * stride4 + i];
+            v.x += u.x;
+            v.y += u.y;
+            v.z += u.z;
+            v.w += u.w;
+        }
+        y[i] = v;
+    }
+}
+
+__global__ __launch_bounds__(256) void split_sum(const float *__restrict__ part, int64_t stride, int splits,
+                                                 float *__restrict__ y, int64_t n) {
+    for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+        float v = part[i];
+        for (int z = 1; z < splits; ++z) v += part[z * stride + i];
+        y[i] = v;
     }
 }
 
 template <int PREC, int BM, int BN>
-hipError_t launch_tile(const PParams &p, hipStream_t s) {
-    const dim3 grid((unsigned)((p.Np + BN - 1) / BN), (unsigned)((p.M + BM - 1) / BM));
+hipError_t launch_tile(const PParams &p, int splits, hipStream_t s) {
+    const dim3 grid((unsigned)((p.Np + BN - 1) / BN), (unsigned)((p.M + BM - 1) / BM), (unsigned)splits);
     if (p.zp)
         hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, true>), grid, dim3(256), 0, s, p);
     else
@@ -261,14 +309,69 @@ hipError_t launch_tile(const PParams &p, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Blocks a split-K launch aims for, per CU (TBH_PREFILL_BLOCKS_PER_CU
+// overrides the default of 2; 0 disables split-K).
+int blocks_per_cu() {
+    static const int v = [] {
+        const char *e = std::getenv("TBH_PREFILL_BLOCKS_PER_CU");
+        return e ? std::max(0, std::atoi(e)) : 2;
+    }();
+    return v;
+}
+
+constexpr int kMinSplitSteps = 4;  // K steps of 64 a split keeps at least
+
+template <int PREC, int BM, int BN>
+hipError_t launch_split(const tbh_weight &w, PParams p, int64_t tiles, hipStream_t s) {
+    const int nsteps = (int)((p.chunks * (PREC == 8 ? kInt8ChunkElems : kInt4ChunkElems) + kBK - 1) / kBK);
+    const int64_t cus = std::max(1, w.dev->cu_count);
+    int splits = 1, sps = nsteps;
+    if (tiles < cus && p.ldy == p.N && blocks_per_cu() > 0) {
+        const int64_t want = (blocks_per_cu() * cus + tiles - 1) / tiles;
+        sps = (int)std::max<int64_t>(kMinSplitSteps, (nsteps + want - 1) / want);
+        sps = (sps + kDepth - 1) / kDepth * kDepth;
+        splits = (nsteps + sps - 1) / sps;
+    }
+    float *const y = p.y;
+    const int64_t n = (int64_t)p.M * p.N;
+    float *part = nullptr;
+    if (splits > 1) {
+        part = (float *)stream_workspace(w.dev, s, (size_t)(splits * n) * sizeof(float));
+        if (!part) {          // no workspace (graph capture before any eager call): one pass
+            splits = 1;
+            sps = nsteps;
+        }
+    }
+    p.split_steps = sps;
+    if (splits > 1) {
+        p.y = part;
+        p.split_stride = n;
+    }
+    hipError_t e = launch_tile<PREC, BM, BN>(p, splits, s);
+    if (e != hipSuccess || splits == 1) return e;
+    const int64_t grid_cap = 4 * cus;
+    if (n % 4 == 0 && ((uintptr_t)y & 15) == 0) {
+        const int64_t n4 = n / 4;
+        hipLaunchKernelGGL(split_sum4, dim3((unsigned)std::min(grid_cap, (n4 + 255) / 256)), dim3(256), 0, s,
+                           (const float4 *)part, n4, splits, (float4 *)y, n4);
+    } else {
+        hipLaunchKernelGGL(split_sum, dim3((unsigned)std::min(grid_cap, (n + 255) / 256)), dim3(256), 0, s,
+                           (const float *)part, n, splits, y, n);
+    }
+    return hipGetLastError();
+}
+
 template <int PREC>
-hipError_t launch_prec(const PParams &p, int64_t cus, hipStream_t s) {
-    // Largest tile that still gives every CU a block.
+hipError_t launch_prec(const tbh_weight &w, const PParams &p, hipStream_t s) {
+    // Largest tile that still gives every CU a block; below that, 64 x 64
+    // tiles split along K.
+    const int64_t cus = std::max(1, w.dev->cu_count);
     const int64_t t128 = ((p.Np + 127) / 128) * ((p.M + 127) / 128);
     const int64_t t64x128 = ((p.Np + 127) / 128) * ((p.M + 63) / 64);
-    if (t128 >= cus) return launch_tile<PREC, 128, 128>(p, s);
-    if (t64x128 >= cus) return launch_tile<PREC, 64, 128>(p, s);
-    return launch_tile<PREC, 64, 64>(p, s);
+    const int64_t t64 = ((p.Np + 63) / 64) * ((p.M + 63) / 64);
+    if (t128 >= cus) return launch_split<PREC, 128, 128>(w, p, t128, s);
+    if (t64x128 >= cus) return launch_split<PREC, 64, 128>(w, p, t64x128, s);
+    return launch_split<PREC, 64, 64>(w, p, t64, s);
 }
 
 }  // namespace
@@ -299,8 +402,7 @@ hipError_t launch_prefill(const tbh_weight &w, const uint16_t *x, int64_t ldx, i
     p.chunks = (int32_t)(w.Kp / (int8 ? kInt8ChunkElems : kInt4ChunkElems));
     p.G = (int32_t)w.groups_per_row;
     p.cpg = w.chunks_per_group;
-    const int64_t cus = std::max(1, w.dev->cu_count);
-    return int8 ? launch_prec<8>(p, cus, s) : launch_prec<4>(p, cus, s);
+    return int8 ? launch_prec<8>(w, p, s) : launch_prec<4>(w, p, s);
 }
 
 }  // namespace tbh
