@@ -278,6 +278,60 @@ tbh_status tbh_tbf_load_decoder(tbh_device *dev, const tbh_tbf *f, int32_t max_s
 tbh_status tbh_dequantize(tbh_device *dev, const tbh_weight *w, float *out);
 tbh_status tbh_dequantize_device(const tbh_weight *w, float *out, void *stream);
 
+/* ---- the other backend protocols (Backend.swift:177-228) --------------- */
+/* Each op has a host-pointer call (synchronous, serialised per device, like
+ * tbh_matmul) and a _device call (device pointers, enqueued on a hipStream_t
+ * and returning after the launch).  Sizes of 0 are no-ops.  Results are fp32
+ * computed in fp32. */
+
+/* SoftmaxBackend.softmax (Backend.swift:180-186; MetalBackend.swift:1073-1134,
+ * Shaders/Softmax.metal): each of `rows` rows of `cols` elements becomes
+ * exp(x - max) / (sum + 1e-7), the epsilon of Tensor.softmaxCPU
+ * (Tensor.swift:1271-1330). */
+tbh_status tbh_softmax(tbh_device *dev, const float *x, int64_t rows, int64_t cols, float *y);
+tbh_status tbh_softmax_device(tbh_device *dev, const float *x, int64_t rows, int64_t cols, float *y,
+                              void *stream);
+
+/* RMSNormBackend.rmsnorm (Backend.swift:188-199; MetalBackend.swift:1146-1207):
+ * per row of `hidden` elements, y = x * (1 / sqrt(sum(x^2) / hidden + eps)) *
+ * weight, as Tensor.rmsNormCPU (Tensor.swift:1538-1556). */
+tbh_status tbh_rmsnorm(tbh_device *dev, const float *x, int64_t rows, int64_t hidden, const float *weight,
+                       float eps, float *y);
+tbh_status tbh_rmsnorm_device(tbh_device *dev, const float *x, int64_t rows, int64_t hidden,
+                              const float *weight, float eps, float *y, void *stream);
+
+/* ActivationBackend (Backend.swift:222-228): silu y = x / (1 + exp(-x))
+ * (Tensor.swift:1135-1141); gelu, tanh form, y = 0.5 x (1 + tanh(sqrt(2/pi)
+ * (x + 0.044715 x^3))) (Tensor.swift:1107-1121). */
+tbh_status tbh_silu(tbh_device *dev, const float *x, int64_t n, float *y);
+tbh_status tbh_silu_device(tbh_device *dev, const float *x, int64_t n, float *y, void *stream);
+tbh_status tbh_gelu(tbh_device *dev, const float *x, int64_t n, float *y);
+tbh_status tbh_gelu_device(tbh_device *dev, const float *x, int64_t n, float *y, void *stream);
+
+/* AttentionBackend.attention (Backend.swift:201-220; MetalBackend.swift:1381-1525,
+ * Shaders/FlashAttention.metal).  q [batch][seq_len][num_heads * head_dim],
+ * k and v [batch][kv_len][num_kv_heads * head_dim], optional additive mask
+ * [kv_len] shared by every query (0 attends, -inf ignores), out shaped like
+ * q.  Query head h reads key/value head h / (num_heads / num_kv_heads);
+ * scores are q.k / sqrt(head_dim) + mask; out = sum(p v) / (sum(p) + 1e-7)
+ * with p = exp(score - max) over all kv_len positions.  A row whose
+ * positions are all masked gives NaN, as the reference's CPU attention does;
+ * kv_len 0 gives zeros. 
+ * num_heads must be a multiple of num_kv_heads; head_dim <= 256. */
+typedef struct tbh_attention_shape {
+    int64_t batch;
+    int64_t seq_len;
+    int64_t kv_len;
+    int32_t head_dim;
+    int32_t num_heads;
+    int32_t num_kv_heads;
+} tbh_attention_shape;
+
+tbh_status tbh_attention(tbh_device *dev, const tbh_attention_shape *shape, const float *q, const float *k,
+                         const float *v, const float *mask, float *out);
+tbh_status tbh_attention_device(tbh_device *dev, const tbh_attention_shape *shape, const float *q,
+                                const float *k, const float *v, const float *mask, float *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

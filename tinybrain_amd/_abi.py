@@ -31,7 +31,21 @@ EXPORTS = [
     "tbh_decoder_step_device", "tbh_decoder_step",
     "tbh_tbf_open", "tbh_tbf_close", "tbh_tbf_get_config", "tbh_tbf_tensor_count",
     "tbh_tbf_tensor", "tbh_tbf_find", "tbh_tbf_qtensor", "tbh_tbf_floats", "tbh_tbf_load_decoder",
+    "tbh_softmax", "tbh_softmax_device", "tbh_rmsnorm", "tbh_rmsnorm_device",
+    "tbh_silu", "tbh_silu_device", "tbh_gelu", "tbh_gelu_device",
+    "tbh_attention", "tbh_attention_device",
 ]
+
+
+class AttentionShape(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int64),
+        ("seq_len", ctypes.c_int64),
+        ("kv_len", ctypes.c_int64),
+        ("head_dim", ctypes.c_int32),
+        ("num_heads", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+    ]
 
 
 class QTensorDesc(ctypes.Structure):
@@ -159,6 +173,17 @@ def lib() -> ctypes.CDLL:
     L.tbh_tbf_qtensor.argtypes = [vp, i32, dp]
     L.tbh_tbf_floats.argtypes = [vp, i32, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(i64)]
     L.tbh_tbf_load_decoder.argtypes = [vp, vp, i32, pp]
+    f32 = ctypes.c_float
+    L.tbh_softmax.argtypes = [vp, vp, i64, i64, vp]
+    L.tbh_softmax_device.argtypes = [vp, vp, i64, i64, vp, vp]
+    L.tbh_rmsnorm.argtypes = [vp, vp, i64, i64, vp, f32, vp]
+    L.tbh_rmsnorm_device.argtypes = [vp, vp, i64, i64, vp, f32, vp, vp]
+    for op in ("silu", "gelu"):
+        getattr(L, "tbh_" + op).argtypes = [vp, vp, i64, vp]
+        getattr(L, "tbh_" + op + "_device").argtypes = [vp, vp, i64, vp, vp]
+    sp = ctypes.POINTER(AttentionShape)
+    L.tbh_attention.argtypes = [vp, sp, vp, vp, vp, vp, vp]
+    L.tbh_attention_device.argtypes = [vp, sp, vp, vp, vp, vp, vp, vp]
     for name in ("tbh_tbf_open", "tbh_tbf_close", "tbh_tbf_get_config", "tbh_tbf_tensor",
                  "tbh_tbf_find", "tbh_tbf_qtensor", "tbh_tbf_floats", "tbh_tbf_load_decoder"):
         getattr(L, name).restype = i32
@@ -169,7 +194,10 @@ def lib() -> ctypes.CDLL:
     for name in ("tbh_device_open", "tbh_device_close", "tbh_device_get_info",
                  "tbh_weight_create", "tbh_weight_destroy", "tbh_weight_get_info",
                  "tbh_matmul", "tbh_matmul_device", "tbh_matmul_bf16_device",
-                 "tbh_dequantize", "tbh_dequantize_device"):
+                 "tbh_dequantize", "tbh_dequantize_device",
+                 "tbh_softmax", "tbh_softmax_device", "tbh_rmsnorm", "tbh_rmsnorm_device",
+                 "tbh_silu", "tbh_silu_device", "tbh_gelu", "tbh_gelu_device",
+                 "tbh_attention", "tbh_attention_device"):
         getattr(L, name).restype = i32
     _lib = L
     return L

@@ -17,6 +17,12 @@ implements it (Sources/TinyBrainMetal/MetalBackend.swift:894-1048):
   * results are returned host-resident (numpy), because the reference's
     TensorStorage can only sync from an MTLBuffer (TensorStorage.swift:82-97).
 
+The same class also implements the reference's other backend protocols
+(Backend.swift:177-228) -- SoftmaxBackend.softmax, RMSNormBackend.rmsnorm,
+ActivationBackend.silu / gelu and AttentionBackend.attention -- with the
+shape rules of MetalBackend's implementations (MetalBackend.swift:1062-1260,
+1362-1525).
+
 All compute runs in libtinybrain_hip.so; nothing here computes a product.
 """
 from __future__ import annotations
@@ -190,6 +196,147 @@ class HIPBackend:
         s = stream if stream is not None else torch.cuda.current_stream(out.device)
         _check(self._lib.tbh_dequantize_device(weight.handle, out.data_ptr(),
                                                ctypes.c_void_p(s.cuda_stream)))
+        return out
+
+    # -- SoftmaxBackend / RMSNormBackend / ActivationBackend / AttentionBackend --
+    def softmax(self, input: np.ndarray) -> np.ndarray:
+        """Softmax along the last dimension, rows summing to 1
+        (MetalBackend.swift:1073-1134; empty input is returned as is)."""
+        x = np.ascontiguousarray(input, np.float32)
+        if x.size == 0:
+            return x
+        if x.ndim == 0:
+            raise PreconditionFailure("Cannot apply softmax to empty tensor")
+        y = np.empty_like(x)
+        cols = x.shape[-1]
+        _check(self._lib.tbh_softmax(self._dev, x.ctypes.data, x.size // cols, cols, y.ctypes.data))
+        return y
+
+    def rmsnorm(self, input: np.ndarray, weight: np.ndarray, eps: float = 1e-5) -> np.ndarray:
+        """x / rms(x) * weight per row of a [tokens, hidden] tensor
+        (MetalBackend.swift:1146-1207)."""
+        x = np.ascontiguousarray(input, np.float32)
+        g = np.ascontiguousarray(weight, np.float32).reshape(-1)
+        if x.ndim != 2:
+            raise PreconditionFailure("rmsnorm input must be 2-D [tokens, hidden]")
+        if g.size != x.shape[1]:
+            raise PreconditionFailure("weight size must equal hiddenDim")
+        y = np.empty_like(x)
+        _check(self._lib.tbh_rmsnorm(self._dev, x.ctypes.data, x.shape[0], x.shape[1], g.ctypes.data,
+                                     float(eps), y.ctypes.data))
+        return y
+
+    def _elementwise(self, fn, input: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(input, np.float32)
+        if x.size == 0:
+            return x
+        y = np.empty_like(x)
+        _check(fn(self._dev, x.ctypes.data, x.size, y.ctypes.data))
+        return y
+
+    def silu(self, input: np.ndarray) -> np.ndarray:
+        """out = x * sigmoid(x) (MetalBackend.swift:1214-1216)."""
+        return self._elementwise(self._lib.tbh_silu, input)
+
+    def gelu(self, input: np.ndarray) -> np.ndarray:
+        """GELU, tanh approximation (MetalBackend.swift:1221-1223)."""
+        return self._elementwise(self._lib.tbh_gelu, input)
+
+    @staticmethod
+    def _attention_shape(q, k, v, mask, headDim, numHeads, numKVHeads):
+        if not (numHeads >= numKVHeads and numKVHeads > 0 and numHeads % numKVHeads == 0):
+            raise PreconditionFailure("numHeads must be a multiple of numKVHeads")
+        if q.ndim == 3:
+            batch, seq, kv = q.shape[0], q.shape[1], k.shape[1]
+        else:
+            batch, seq, kv = 1, q.shape[0], k.shape[0]
+        if (q.shape[-1] != numHeads * headDim or k.shape[-1] != numKVHeads * headDim
+                or tuple(v.shape) != tuple(k.shape) or k.ndim != q.ndim
+                or (q.ndim == 3 and k.shape[0] != batch)):
+            raise PreconditionFailure("attention: query/keys/values shapes do not match the heads")
+        if mask is not None and (mask.numel() if hasattr(mask, "numel") else mask.size) != kv:
+            raise PreconditionFailure("attention: mask must have kvSeqLen elements")
+        return _abi.AttentionShape(batch, seq, kv, headDim, numHeads, numKVHeads)
+
+    def attention(self, query: np.ndarray, keys: np.ndarray, values: np.ndarray,
+                  mask: Optional[np.ndarray], headDim: int, numHeads: int, numKVHeads: int) -> np.ndarray:
+        """softmax(Q K^T / sqrt(headDim) + mask) V per head with GQA
+        (MetalBackend.swift:1381-1525); returns an array shaped like query."""
+        q = np.ascontiguousarray(query, np.float32)
+        k = np.ascontiguousarray(keys, np.float32)
+        v = np.ascontiguousarray(values, np.float32)
+        m = None if mask is None else np.ascontiguousarray(mask, np.float32).reshape(-1)
+        sh = self._attention_shape(q, k, v, m, headDim, numHeads, numKVHeads)
+        out = np.empty_like(q)
+        _check(self._lib.tbh_attention(self._dev, ctypes.byref(sh), q.ctypes.data, k.ctypes.data,
+                                       v.ctypes.data, None if m is None else m.ctypes.data, out.ctypes.data))
+        return out
+
+    # device-resident variants: contiguous float32 torch tensors on this device
+    def _stream(self, t, stream):
+        import torch
+
+        return ctypes.c_void_p((stream if stream is not None else torch.cuda.current_stream(t.device)).cuda_stream)
+
+    @staticmethod
+    def _dev_tensor(t):
+        import torch
+
+        if t.dtype != torch.float32 or not t.is_contiguous() or not t.is_cuda:
+            raise PreconditionFailure("expected a contiguous float32 device tensor")
+        return t
+
+    def softmax_device(self, x, out=None, stream=None):
+        import torch
+
+        x = self._dev_tensor(x)
+        out = torch.empty_like(x) if out is None else self._dev_tensor(out)
+        if x.numel():
+            cols = x.shape[-1]
+            _check(self._lib.tbh_softmax_device(self._dev, x.data_ptr(), x.numel() // cols, cols,
+                                                out.data_ptr(), self._stream(x, stream)))
+        return out
+
+    def rmsnorm_device(self, x, weight, eps: float = 1e-5, out=None, stream=None):
+        import torch
+
+        x, weight = self._dev_tensor(x), self._dev_tensor(weight)
+        if x.dim() != 2 or weight.numel() != x.shape[1]:
+            raise PreconditionFailure("rmsnorm: x [tokens, hidden] and weight [hidden]")
+        out = torch.empty_like(x) if out is None else self._dev_tensor(out)
+        _check(self._lib.tbh_rmsnorm_device(self._dev, x.data_ptr(), x.shape[0], x.shape[1], weight.data_ptr(),
+                                            float(eps), out.data_ptr(), self._stream(x, stream)))
+        return out
+
+    def silu_device(self, x, out=None, stream=None):
+        import torch
+
+        x = self._dev_tensor(x)
+        out = torch.empty_like(x) if out is None else self._dev_tensor(out)
+        _check(self._lib.tbh_silu_device(self._dev, x.data_ptr(), x.numel(), out.data_ptr(),
+                                         self._stream(x, stream)))
+        return out
+
+    def gelu_device(self, x, out=None, stream=None):
+        import torch
+
+        x = self._dev_tensor(x)
+        out = torch.empty_like(x) if out is None else self._dev_tensor(out)
+        _check(self._lib.tbh_gelu_device(self._dev, x.data_ptr(), x.numel(), out.data_ptr(),
+                                         self._stream(x, stream)))
+        return out
+
+    def attention_device(self, query, keys, values, mask, headDim: int, numHeads: int, numKVHeads: int,
+                         out=None, stream=None):
+        import torch
+
+        q, k, v = self._dev_tensor(query), self._dev_tensor(keys), self._dev_tensor(values)
+        m = None if mask is None else self._dev_tensor(mask)
+        sh = self._attention_shape(q, k, v, m, headDim, numHeads, numKVHeads)
+        out = torch.empty_like(q) if out is None else self._dev_tensor(out)
+        _check(self._lib.tbh_attention_device(self._dev, ctypes.byref(sh), q.data_ptr(), k.data_ptr(),
+                                              v.data_ptr(), None if m is None else m.data_ptr(),
+                                              out.data_ptr(), self._stream(q, stream)))
         return out
 
     def close(self) -> None:

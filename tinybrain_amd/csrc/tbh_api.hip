@@ -63,7 +63,7 @@ using namespace tbh;
     } while (0)
 
 // Makes the weight's device current on the calling thread.
-static tbh_status use_device(int32_t ordinal) {
+tbh_status tbh::use_device(int32_t ordinal) {
     int cur = -1;
     TBH_HIP(hipGetDevice(&cur), "hipGetDevice");
     if (cur != ordinal) TBH_HIP(hipSetDevice(ordinal), "hipSetDevice");

@@ -92,6 +92,8 @@ namespace tbh {
 // Thread-local error reporting (tbh_api.hip).
 tbh_status set_error(tbh_status st, const std::string &msg);
 tbh_status hip_error(hipError_t e, const char *what);
+// Makes `ordinal` the calling thread's current HIP device (tbh_api.hip).
+tbh_status use_device(int32_t ordinal);
 
 // Host-side check, before any launch, that the device arrays a weight's
 // kernels index exist and have the sizes those kernels assume.
