@@ -56,6 +56,16 @@ DECODE = {
     "decode_7b_int4": ("int4", 32, dict(num_layers=32, hidden=4096, num_heads=32, num_kv_heads=32,
                                         intermediate=11008, vocab=32000), 512),
 }
+# The other backend protocols (softmax, RMSNorm, SiLU/GELU, attention) at the
+# shapes either side of the GEMV in a 1.1B-shaped model: one launch per step
+# over a >= 2 GiB rotating pool of inputs.  name: (op, shape kwargs)
+OPS = {
+    "op_softmax_256x32000": ("softmax", dict(rows=256, cols=32000)),          # logits of 256 tokens
+    "op_rmsnorm_2048x2048": ("rmsnorm", dict(rows=2048, hidden=2048)),        # 2048-token prefill
+    "op_silu_2048x5632": ("silu", dict(n=2048 * 5632)),
+    "op_gelu_2048x5632": ("gelu", dict(n=2048 * 5632)),
+    "op_attention_decode_ctx4096": ("attention", dict(batch=1, seq=1, kv=4096, hd=64, nh=32, nkv=4)),
+}
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 RIDGE_FLOP_PER_BYTE = MFMA_BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
 
@@ -392,12 +402,145 @@ def run_decode(args, backend, T, torch):
     backend.close()
 
 
+def op_sizes(op, c):
+    """(input floats, output floats, algorithmic bytes) of one launch: each
+    input read once and each output written once."""
+    if op == "softmax":
+        n_in, n_out, extra = c["rows"] * c["cols"], c["rows"] * c["cols"], 0
+    elif op == "rmsnorm":
+        n_in, n_out, extra = c["rows"] * c["hidden"], c["rows"] * c["hidden"], c["hidden"]
+    elif op in ("silu", "gelu"):
+        n_in, n_out, extra = c["n"], c["n"], 0
+    else:
+        q = c["batch"] * c["seq"] * c["nh"] * c["hd"]
+        kv = c["batch"] * c["kv"] * c["nkv"] * c["hd"]
+        n_in, n_out, extra = q + 2 * kv, q, 0
+    return n_in, n_out, 4 * (n_in + n_out + extra)
+
+
+def cpu_baseline_op(op, c, budget_s):
+    """The float64 oracle of the reference's CPU path (numpy, one thread) on
+    the same shape, repeated until about budget_s seconds."""
+    import oracle.ops_ref as R
+
+    rng = np.random.default_rng(5)
+    if op == "softmax":
+        x = rng.normal(size=(c["rows"], c["cols"])).astype(np.float32)
+        fn = lambda: R.softmax(x)
+    elif op == "rmsnorm":
+        x = rng.normal(size=(c["rows"], c["hidden"])).astype(np.float32)
+        w = np.ones(c["hidden"], np.float32)
+        fn = lambda: R.rmsnorm(x, w)
+    elif op in ("silu", "gelu"):
+        x = rng.normal(size=c["n"]).astype(np.float32)
+        fn = lambda: getattr(R, op)(x)
+    else:
+        q = rng.normal(size=(c["batch"], c["seq"], c["nh"] * c["hd"])).astype(np.float32)
+        k = rng.normal(size=(c["batch"], c["kv"], c["nkv"] * c["hd"])).astype(np.float32)
+        fn = lambda: R.attention(q, k, k, None, c["hd"], c["nh"], c["nkv"])
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    bytes_per = op_sizes(op, c)[2]
+    return {"value": round(bytes_per * n / el / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{n} full launches of the same shape through oracle/ops_ref.py (numpy float64), "
+                      f"{el:.1f} s"}
+
+
+def run_op(args, backend, T, torch):
+    op, c = OPS[args.workload]
+    dev = torch.device("cuda", 0)
+    n_in, n_out, byts = op_sizes(op, c)
+    n_sets = max(2, int(np.ceil(args.pool_gib * 2**30 / (4 * (n_in + n_out)))))
+    gen = torch.Generator(device=dev).manual_seed(4)
+    ins = [torch.randn(n_in, generator=gen, device=dev, dtype=torch.float32) for _ in range(n_sets)]
+    outs = [torch.empty(n_out, device=dev, dtype=torch.float32) for _ in range(n_sets)]
+    g = torch.ones(c.get("hidden", 1), device=dev, dtype=torch.float32)
+    cap = torch.cuda.Stream(dev)
+
+    def launch(i):
+        x, y = ins[i], outs[i]
+        if op == "softmax":
+            backend.softmax_device(x.view(c["rows"], c["cols"]), out=y.view(c["rows"], c["cols"]), stream=cap)
+        elif op == "rmsnorm":
+            backend.rmsnorm_device(x.view(c["rows"], c["hidden"]), g, 1e-5,
+                                   out=y.view(c["rows"], c["hidden"]), stream=cap)
+        elif op in ("silu", "gelu"):
+            getattr(backend, op + "_device")(x, out=y, stream=cap)
+        else:
+            q_n = c["batch"] * c["seq"] * c["nh"] * c["hd"]
+            kv_n = c["batch"] * c["kv"] * c["nkv"] * c["hd"]
+            q = x[:q_n].view(c["batch"], c["seq"], c["nh"] * c["hd"])
+            k = x[q_n:q_n + kv_n].view(c["batch"], c["kv"], c["nkv"] * c["hd"])
+            v = x[q_n + kv_n:].view(c["batch"], c["kv"], c["nkv"] * c["hd"])
+            backend.attention_device(q, k, v, None, c["hd"], c["nh"], c["nkv"],
+                                     out=y.view(c["batch"], c["seq"], c["nh"] * c["hd"]), stream=cap)
+
+    cap.wait_stream(torch.cuda.current_stream(dev))
+    for i in range(n_sets):
+        launch(i)
+    torch.cuda.synchronize()
+    eager = outs[0].clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=cap):
+        for i in range(n_sets):
+            launch(i)
+    outs[0].zero_()
+    graph.replay()
+    torch.cuda.synchronize()
+    if not torch.equal(outs[0], eager):
+        raise RuntimeError("graph replay differs from the eager launches")
+    reps = max(1, -(-args.steps // n_sets))
+    warm = max(1, -(-args.warmup // n_sets))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(cap):
+        for _ in range(warm):
+            graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record(cap)
+        for _ in range(reps):
+            graph.replay()
+        e1.record(cap)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    steps_done = reps * n_sets
+    kern_us = e0.elapsed_time(e1) * 1e3 / steps_done
+    achieved = byts / kern_us / 1e3
+    out = {
+        "metric": f"{op} GB/s (algorithmic bytes: inputs read once, outputs written once)",
+        "value": round(byts * steps_done / wall / 1e9, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps_done,
+        "warmup": warm * n_sets,
+        "ms_per_step": round(1e3 * wall / steps_done, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": args.workload, "op": op, **c, "pool_sets": n_sets},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": f"tbh_{op}", "kernel_us": round(kern_us, 3), "alg_bytes_per_launch": byts},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline_op(op, c, args.cpu_budget)
+    print(json.dumps(out), flush=True)
+    backend.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="int4_g32_gemv_m1", choices=sorted(WORKLOADS) + sorted(PREFILL) + sorted(DECODE))
+    ap.add_argument("--workload", default="int4_g32_gemv_m1", choices=sorted(WORKLOADS) + sorted(PREFILL) + sorted(DECODE) + sorted(OPS))
     ap.add_argument("--pool-gib", type=float, default=2.2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
@@ -420,6 +563,8 @@ def main():
         return run_prefill(args, backend, T, torch)
     if args.workload in DECODE:
         return run_decode(args, backend, T, torch)
+    if args.workload in OPS:
+        return run_op(args, backend, T, torch)
     prec, gs, shapes, M = WORKLOADS[args.workload]
 
     # ---- weights: one quantized base per shape, copied into a >= 2 GiB pool

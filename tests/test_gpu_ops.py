@@ -127,6 +127,9 @@ ATTN_CASES = [
     (None, 4, 70, 256, 2, 1),        # head_dim 256 (four elements per lane)
     (None, 6, 65, 80, 4, 2),         # head_dim 80: partial second lane group
     (None, 9, 33, 6, 3, 3),          # head_dim 6: scalar loads
+    (None, 1, 4096, 64, 32, 4),      # long decode context: many key-position splits
+    (2, 3, 300, 32, 32, 2),          # 16 query heads per key/value head: two head groups
+    (None, 2, 200, 64, 12, 1),       # 12 query heads per key/value head: a partial group
 ]
 
 

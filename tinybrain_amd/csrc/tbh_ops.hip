@@ -9,10 +9,18 @@
 // and the partial results meet through cross-lane reductions.  Softmax keeps
 // a running (max, sum) pair per thread, so x is read twice (once for the
 // pair, once for the output) instead of the reference kernel's three reads
-// and two writes.  Attention gives each (batch, query, head) row one wave:
-// a lane scores one key position of a 64-position tile, the wave keeps an
-// online softmax across tiles, and each lane accumulates head_dim / 64
-// output elements from coalesced value rows.
+// and two writes.
+//
+// Attention (head_dim % 4 == 0): a block serves the query heads (up to 8)
+// that share one key/value head, so each key and value row is read once per
+// group rather than once per query head.  When there are too few (query,
+// key/value head) groups to fill the chip, the key positions are split over
+// several blocks, each writing a partial (max, sum, output) per head to a
+// workspace, and a second kernel merges them (split-KV decoding).  Inside a
+// block, a pass scores 256 positions (one per thread, 16-byte key loads,
+// queries broadcast from LDS), keeps an online softmax per head across
+// passes, and accumulates p * v with 16-byte value loads.  Other head
+// dimensions take a one-wave-per-row kernel.
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -277,6 +285,402 @@ __global__ __launch_bounds__(256) void attention_rows(const AttnArgs a) {
     }
 }
 
+constexpr int kGrpHeads = 8;   // query heads one block serves
+constexpr int kPass = 256;     // positions scored per pass, one per thread
+constexpr int kRedPad = 4 * kGrpHeads + 1;
+
+struct GrpArgs {
+    AttnArgs a;
+    int32_t rep;       // query heads per key/value head
+    int32_t hchunks;   // ceil(rep / kGrpHeads)
+    int32_t splits;    // blocks per group along the key positions
+    int64_t chunk;     // positions per split
+    int64_t units;     // batch * seq_len * nkv * hchunks
+    float *part;       // splits > 1: [units * splits][2 * kGrpHeads + kGrpHeads * hd]
+};
+
+__global__ __launch_bounds__(256) void attention_group(const GrpArgs g) {
+    const AttnArgs &a = g.a;
+    __shared__ __attribute__((aligned(16))) float qs[kGrpHeads][kAttnMaxHeadDim];
+    __shared__ float ps[kGrpHeads][kPass];
+    __shared__ float redm[4][kGrpHeads], reds[4][kGrpHeads];
+    __shared__ float red_o[256 * kRedPad];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int64_t unit = blockIdx.x / g.splits;
+    const int split = (int)(blockIdx.x % g.splits);
+    const int hc = (int)(unit % g.hchunks);
+    const int64_t grp = unit / g.hchunks;                 // (batch * seq_len + query) * nkv + kvh
+    const int kvh = (int)(grp % a.nkv);
+    const int64_t bq = grp / a.nkv;
+    const int64_t b = bq / a.seq_len;
+    const int nhb = min(kGrpHeads, g.rep - hc * kGrpHeads);
+    const int head0 = kvh * g.rep + hc * kGrpHeads;
+    const int hd = a.hd, hd4 = hd / 4;
+    const int64_t kvd = (int64_t)a.nkv * hd;
+    const float *kb = a.k + b * a.kv_len * kvd + (int64_t)kvh * hd;
+    const float *vb = a.v + b * a.kv_len * kvd + (int64_t)kvh * hd;
+    const float *qb = a.q + bq * a.nh * hd + (int64_t)head0 * hd;
+    for (int o = tid; o < kGrpHeads * hd; o += 256) {
+        const int h = o / hd;
+        qs[h][o % hd] = h < nhb ? qb[o] : 0.0f;
+    }
+    const int64_t c0 = split * g.chunk, c1 = min(a.kv_len, c0 + g.chunk);
+    // value phase mapping: lane = pp * lpr + d4
+    const int lpr = hd4, ppi = 64 / lpr;
+    const int pp = lane / lpr, d4 = lane % lpr;
+    const bool vlane = pp < ppi;
+
+    float m[kGrpHeads], l[kGrpHeads];
+    float4 acc[kGrpHeads];
+#pragma unroll
+    for (int h = 0; h < kGrpHeads; ++h) {
+        m[h] = -INFINITY;
+        l[h] = 0.0f;
+        acc[h] = float4{0.f, 0.f, 0.f, 0.f};
+    }
+    __syncthreads();
+    for (int64_t p0 = c0; p0 < c1; p0 += kPass) {
+        // ---- scores of position p0 + tid for every head of the group
+        const int64_t t = p0 + tid;
+        const bool valid = t < c1;
+        float sc[kGrpHeads];
+#pragma unroll
+        for (int h = 0; h < kGrpHeads; ++h) sc[h] = 0.0f;
+        if (valid) {
+            const float4 *kr = (const float4 *)(kb + t * kvd);
+#pragma unroll 4
+            for (int i = 0; i < hd4; ++i) {
+                const float4 kv = kr[i];
+#pragma unroll
+                for (int h = 0; h < kGrpHeads; ++h) {
+                    const float4 qv = *(const float4 *)&qs[h][4 * i];
+                    sc[h] += qv.x * kv.x + qv.y * kv.y + qv.z * kv.z + qv.w * kv.w;
+                }
+            }
+        }
+        const float mk = (valid && a.mask) ? a.mask[t] : 0.0f;
+#pragma unroll
+        for (int h = 0; h < kGrpHeads; ++h) {
+            sc[h] = valid ? sc[h] * a.scale + mk : -INFINITY;
+            const float wm = wave_max(sc[h]);
+            if (lane == 0) redm[wave][h] = wm;
+        }
+        __syncthreads();
+        float corr[kGrpHeads];
+#pragma unroll
+        for (int h = 0; h < kGrpHeads; ++h) {
+            const float pm = fmaxf(fmaxf(redm[0][h], redm[1][h]), fmaxf(redm[2][h], redm[3][h]));
+            const float nm = fmaxf(m[h], pm);
+            corr[h] = nm == -INFINITY ? 1.0f : expf(m[h] - nm);
+            const float pv = nm == -INFINITY ? 0.0f : expf(sc[h] - nm);
+            ps[h][tid] = pv;
+            const float ws = wave_sum(pv);
+            if (lane == 0) reds[wave][h] = ws;
+            m[h] = nm;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int h = 0; h < kGrpHeads; ++h) {
+            l[h] = l[h] * corr[h] + ((reds[0][h] + reds[1][h]) + (reds[2][h] + reds[3][h]));
+            acc[h].x *= corr[h];
+            acc[h].y *= corr[h];
+            acc[h].z *= corr[h];
+            acc[h].w *= corr[h];
+        }
+        // ---- p * v over this wave's 64 positions of the pass
+        if (vlane) {
+#pragma unroll 4
+            for (int r = pp; r < 64; r += ppi) {
+                const int tp = wave * 64 + r;
+                if (p0 + tp >= c1) break;
+                const float4 v = *(const float4 *)(vb + (p0 + tp) * kvd + 4 * d4);
+#pragma unroll
+                for (int h = 0; h < kGrpHeads; ++h) {
+                    const float pr = ps[h][tp];
+                    acc[h].x += pr * v.x;
+                    acc[h].y += pr * v.y;
+                    acc[h].z += pr * v.z;
+                    acc[h].w += pr * v.w;
+                }
+            }
+        }
+        __syncthreads();   // ps and redm are rewritten by the next pass
+    }
+
+    // ---- sum the value accumulators over lanes and waves
+#pragma unroll
+    for (int h = 0; h < kGrpHeads; ++h) {
+        red_o[tid * kRedPad + 4 * h + 0] = vlane ? acc[h].x : 0.0f;
+        red_o[tid * kRedPad + 4 * h + 1] = vlane ? acc[h].y : 0.0f;
+        red_o[tid * kRedPad + 4 * h + 2] = vlane ? acc[h].z : 0.0f;
+        red_o[tid * kRedPad + 4 * h + 3] = vlane ? acc[h].w : 0.0f;
+    }
+    __syncthreads();
+    float *part = g.splits > 1 ? g.part + (unit * g.splits + split) * (2 * kGrpHeads + kGrpHeads * hd) : nullptr;
+    if (part && tid < kGrpHeads) {
+        // m and l are uniform over the block; thread h stores head h's pair
+#pragma unroll
+        for (int h = 0; h < kGrpHeads; ++h)
+            if (h == tid) {
+                part[h] = m[h];
+                part[kGrpHeads + h] = l[h];
+            }
+    }
+    for (int o = tid; o < nhb * hd; o += 256) {
+        const int h = o / hd, d = o % hd;
+        float v = 0.0f;
+        for (int w = 0; w < 4; ++w)
+            for (int q = 0; q < ppi; ++q) v += red_o[(w * 64 + q * lpr + d / 4) * kRedPad + 4 * h + d % 4];
+        float mh = 0.0f, lh = 0.0f;
+#pragma unroll
+        for (int hh = 0; hh < kGrpHeads; ++hh)
+            if (hh == h) {
+                mh = m[hh];
+                lh = l[hh];
+            }
+        if (part) {
+            part[2 * kGrpHeads + h * hd + d] = v;
+        } else {
+            float *orow = a.out + bq * a.nh * hd + (int64_t)(head0 + h) * hd;
+            orow[d] = (mh == -INFINITY && a.kv_len > 0) ? NAN : v / (lh + kAttnEps);
+        }
+    }
+}
+
+// LDS-only block barrier: orders LDS accesses without waiting for the
+// global loads still in flight (a full __syncthreads waits for them).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// attention_group for head_dim = 4 * HD4 in {16, 32, 64}: every global load
+// of a pass (the group's queries, the pass's key rows and value rows) is
+// issued before any of them is used, from clamped addresses (positions past
+// the split read its last position and get p = 0), so a pass costs one
+// memory round trip.  Value rows are spread over all four waves: thread
+// (pg, d4) reads 16 bytes of rows pg, pg + 256 / HD4, ...
+template <int HD4>
+__global__ __launch_bounds__(256) void attention_small(const GrpArgs g) {
+    constexpr int HD = 4 * HD4, PPB = 256 / HD4, NQ = (kGrpHeads * HD + 255) / 256;
+    const AttnArgs &a = g.a;
+    __shared__ __attribute__((aligned(16))) float qs[kGrpHeads][HD];
+    __shared__ float ps[kGrpHeads][kPass];
+    __shared__ float redm[4][kGrpHeads], reds[4][kGrpHeads];
+    __shared__ float red_o[256 * kRedPad];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int64_t unit = blockIdx.x / g.splits;
+    const int split = (int)(blockIdx.x % g.splits);
+    const int hc = (int)(unit % g.hchunks);
+    const int64_t grp = unit / g.hchunks;
+    const int kvh = (int)(grp % a.nkv);
+    const int64_t bq = grp / a.nkv;
+    const int64_t b = bq / a.seq_len;
+    const int nhb = min(kGrpHeads, g.rep - hc * kGrpHeads);
+    const int head0 = kvh * g.rep + hc * kGrpHeads;
+    const int64_t kvd = (int64_t)a.nkv * HD;
+    const float *kb = a.k + b * a.kv_len * kvd + (int64_t)kvh * HD;
+    const float *vb = a.v + b * a.kv_len * kvd + (int64_t)kvh * HD;
+    const float *qb = a.q + bq * a.nh * HD + (int64_t)head0 * HD;
+    const int64_t c0 = split * g.chunk, c1 = min(a.kv_len, c0 + g.chunk);
+    const int pg = tid / HD4, d4 = tid % HD4;
+
+    float qv[NQ];
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+        const int o = tid + 256 * i;
+        const int h = min(o / HD, nhb - 1);    // heads past the group read a valid row
+        qv[i] = qb[h * HD + o % HD];
+    }
+    float m[kGrpHeads], l[kGrpHeads];
+    float4 acc[kGrpHeads];
+#pragma unroll
+    for (int h = 0; h < kGrpHeads; ++h) {
+        m[h] = -INFINITY;
+        l[h] = 0.0f;
+        acc[h] = float4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int64_t p0 = c0; p0 < c1; p0 += kPass) {
+        const int64_t t = p0 + tid;
+        const bool valid = t < c1;
+        const float4 *kr = (const float4 *)(kb + min(t, c1 - 1) * kvd);
+        float4 kreg[HD4], vreg[HD4];
+#pragma unroll
+        for (int i = 0; i < HD4; ++i) kreg[i] = kr[i];
+#pragma unroll
+        for (int j = 0; j < HD4; ++j)
+            vreg[j] = *(const float4 *)(vb + min(p0 + pg + j * PPB, c1 - 1) * kvd + 4 * d4);
+        const float mk = a.mask ? a.mask[min(t, c1 - 1)] : 0.0f;
+        if (p0 == c0) {
+#pragma unroll
+            for (int i = 0; i < NQ; ++i) {
+                const int o = tid + 256 * i;
+                if (o < kGrpHeads * HD) qs[o / HD][o % HD] = qv[i];
+            }
+            lds_barrier();
+        }
+        float sc[kGrpHeads];
+#pragma unroll
+        for (int h = 0; h < kGrpHeads; ++h) {
+            float d = 0.0f;
+#pragma unroll
+            for (int i = 0; i < HD4; ++i) {
+                const float4 q4 = *(const float4 *)&qs[h][4 * i];
+                d += q4.x * kreg[i].x + q4.y * kreg[i].y + q4.z * kreg[i].z + q4.w * kreg[i].w;
+            }
+            sc[h] = valid ? d * a.scale + mk : -INFINITY;
+            const float wm = wave_max(sc[h]);
+            if (lane == 0) redm[wave][h] = wm;
+        }
+        lds_barrier();
+        float corr[kGrpHeads];
+#pragma unroll
+        for (int h = 0; h < kGrpHeads; ++h) {
+            const float pm = fmaxf(fmaxf(redm[0][h], redm[1][h]), fmaxf(redm[2][h], redm[3][h]));
+            const float nm = fmaxf(m[h], pm);
+            corr[h] = nm == -INFINITY ? 1.0f : expf(m[h] - nm);
+            const float pv = nm == -INFINITY ? 0.0f : expf(sc[h] - nm);
+            ps[h][tid] = pv;
+            const float ws = wave_sum(pv);
+            if (lane == 0) reds[wave][h] = ws;
+            m[h] = nm;
+        }
+        lds_barrier();
+#pragma unroll
+        for (int h = 0; h < kGrpHeads; ++h) {
+            l[h] = l[h] * corr[h] + ((reds[0][h] + reds[1][h]) + (reds[2][h] + reds[3][h]));
+            float4 a4 = acc[h];
+            a4.x *= corr[h];
+            a4.y *= corr[h];
+            a4.z *= corr[h];
+            a4.w *= corr[h];
+#pragma unroll
+            for (int j = 0; j < HD4; ++j) {
+                const float pr = ps[h][pg + j * PPB];   // 0 past the split
+                a4.x += pr * vreg[j].x;
+                a4.y += pr * vreg[j].y;
+                a4.z += pr * vreg[j].z;
+                a4.w += pr * vreg[j].w;
+            }
+            acc[h] = a4;
+        }
+        lds_barrier();   // ps and redm are rewritten by the next pass
+    }
+
+#pragma unroll
+    for (int h = 0; h < kGrpHeads; ++h) {
+        red_o[tid * kRedPad + 4 * h + 0] = acc[h].x;
+        red_o[tid * kRedPad + 4 * h + 1] = acc[h].y;
+        red_o[tid * kRedPad + 4 * h + 2] = acc[h].z;
+        red_o[tid * kRedPad + 4 * h + 3] = acc[h].w;
+    }
+    __syncthreads();
+    float *part = g.splits > 1 ? g.part + (unit * g.splits + split) * (2 * kGrpHeads + kGrpHeads * HD) : nullptr;
+    if (part && tid < kGrpHeads) {
+#pragma unroll
+        for (int h = 0; h < kGrpHeads; ++h)
+            if (h == tid) {
+                part[h] = m[h];
+                part[kGrpHeads + h] = l[h];
+            }
+    }
+    for (int o = tid; o < nhb * HD; o += 256) {
+        const int h = o / HD, d = o % HD;
+        float v = 0.0f;
+#pragma unroll 4
+        for (int q = 0; q < PPB; ++q) v += red_o[(q * HD4 + d / 4) * kRedPad + 4 * h + d % 4];
+        float mh = 0.0f, lh = 0.0f;
+#pragma unroll
+        for (int hh = 0; hh < kGrpHeads; ++hh)
+            if (hh == h) {
+                mh = m[hh];
+                lh = l[hh];
+            }
+        if (part) {
+            part[2 * kGrpHeads + h * HD + d] = v;
+        } else {
+            float *orow = a.out + bq * a.nh * HD + (int64_t)(head0 + h) * HD;
+            orow[d] = (mh == -INFINITY && a.kv_len > 0) ? NAN : v / (lh + kAttnEps);
+        }
+    }
+}
+
+// Merges the split partials of attention_group / attention_small: per head,
+// M = max m_s, out = sum(o_s e^(m_s - M)) / (sum(l_s e^(m_s - M)) + eps).
+// One block per (group, head): the split weights e^(m_s - M) go through LDS,
+// then thread (sg, d4) sums 16-byte pieces of the splits sg, sg + 256/hd4, ...
+__global__ __launch_bounds__(256) void attention_combine(const GrpArgs g) {
+    const AttnArgs &a = g.a;
+    __shared__ float wsp[1024];            // split weights (splits <= 1024)
+    __shared__ float4 red[256];
+    __shared__ float lsum[4];
+    const int tid = threadIdx.x, hd = a.hd, hd4 = hd / 4;
+    const int64_t unit = blockIdx.x / kGrpHeads;
+    const int h = (int)(blockIdx.x % kGrpHeads);
+    const int hc = (int)(unit % g.hchunks);
+    if (h >= g.rep - hc * kGrpHeads) return;   // uniform over the block
+    const int64_t grp = unit / g.hchunks;
+    const int kvh = (int)(grp % a.nkv);
+    const int64_t bq = grp / a.nkv;
+    const int64_t stride = 2 * kGrpHeads + (int64_t)kGrpHeads * hd;
+    const float *pb = g.part + unit * g.splits * stride;
+    float mloc = -INFINITY;
+    for (int sp = tid; sp < g.splits; sp += 256) {
+        const float mv = pb[sp * stride + h];
+        wsp[sp] = mv;
+        mloc = fmaxf(mloc, mv);
+    }
+    mloc = wave_max(mloc);
+    if ((tid & 63) == 0) lsum[tid >> 6] = mloc;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(lsum[0], lsum[1]), fmaxf(lsum[2], lsum[3]));
+    __syncthreads();
+    float lpart = 0.0f;
+    for (int sp = tid; sp < g.splits; sp += 256) {
+        const float w = M == -INFINITY ? 0.0f : expf(wsp[sp] - M);
+        wsp[sp] = w;
+        lpart += w * pb[sp * stride + kGrpHeads + h];
+    }
+    lpart = wave_sum(lpart);
+    if ((tid & 63) == 0) lsum[tid >> 6] = lpart;
+    __syncthreads();
+    const float L = (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
+    const int sg = tid / hd4, d4 = tid % hd4, nsg = 256 / hd4;
+    float4 o = float4{0.f, 0.f, 0.f, 0.f};
+    if (sg < nsg) {
+#pragma unroll 8
+        for (int sp = sg; sp < g.splits; sp += nsg) {
+            const float w = wsp[sp];
+            const float4 v = *(const float4 *)(pb + sp * stride + 2 * kGrpHeads + h * hd + 4 * d4);
+            o.x += w * v.x;
+            o.y += w * v.y;
+            o.z += w * v.z;
+            o.w += w * v.w;
+        }
+    }
+    red[tid] = o;
+    __syncthreads();
+    if (tid < hd4) {
+        float4 r = float4{0.f, 0.f, 0.f, 0.f};
+        for (int q = 0; q < nsg; ++q) {
+            const float4 v = red[q * hd4 + tid];
+            r.x += v.x;
+            r.y += v.y;
+            r.z += v.z;
+            r.w += v.w;
+        }
+        const int head = kvh * g.rep + hc * kGrpHeads + h;
+        float *orow = a.out + bq * a.nh * hd + (int64_t)head * hd + 4 * tid;
+        const float den = L + kAttnEps;
+        const bool dead = M == -INFINITY;
+        orow[0] = dead ? NAN : r.x / den;
+        orow[1] = dead ? NAN : r.y / den;
+        orow[2] = dead ? NAN : r.z / den;
+        orow[3] = dead ? NAN : r.w / den;
+    }
+}
+
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 unsigned grid_for(int64_t blocks, const tbh_device *dev) {
@@ -325,7 +729,46 @@ hipError_t launch_act(const tbh_device *dev, const float *x, int64_t n, float *y
     return hipGetLastError();
 }
 
-hipError_t launch_attention(const AttnArgs &a, hipStream_t s) {
+hipError_t launch_attention_rows(const AttnArgs &a, hipStream_t s);
+
+hipError_t launch_attention(tbh_device *dev, const AttnArgs &a, hipStream_t s) {
+    if (a.hd % 4 != 0 || !aligned16(a.k) || !aligned16(a.v)) return launch_attention_rows(a, s);
+    GrpArgs g{};
+    g.a = a;
+    g.rep = a.nh / a.nkv;
+    g.hchunks = (g.rep + kGrpHeads - 1) / kGrpHeads;
+    g.units = (a.rows / a.nh) * a.nkv * g.hchunks;
+    g.splits = 1;
+    g.chunk = std::max<int64_t>(a.kv_len, 1);
+    const int64_t target = 2 * (int64_t)std::max(1, dev->cu_count);
+    if (g.units < target && a.kv_len > 64) {
+        const int64_t want = std::min<int64_t>(std::min((target + g.units - 1) / g.units, (a.kv_len + 63) / 64), 1024);
+        g.chunk = ((a.kv_len + want - 1) / want + 63) / 64 * 64;
+        g.splits = (int32_t)((a.kv_len + g.chunk - 1) / g.chunk);
+    }
+    if (g.splits > 1) {
+        const size_t bytes = (size_t)(g.units * g.splits * (2 * kGrpHeads + kGrpHeads * a.hd)) * sizeof(float);
+        g.part = (float *)stream_workspace(dev, s, bytes);
+        if (!g.part) {   // no workspace (graph capture before any eager call): one split
+            g.splits = 1;
+            g.chunk = std::max<int64_t>(a.kv_len, 1);
+        }
+    }
+    if (g.units * g.splits > INT32_MAX) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)(g.units * g.splits));
+    switch (a.hd) {
+    case 16: hipLaunchKernelGGL(attention_small<4>, grid, dim3(256), 0, s, g); break;
+    case 32: hipLaunchKernelGGL(attention_small<8>, grid, dim3(256), 0, s, g); break;
+    case 64: hipLaunchKernelGGL(attention_small<16>, grid, dim3(256), 0, s, g); break;
+    default: hipLaunchKernelGGL(attention_group, grid, dim3(256), 0, s, g); break;
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || g.splits == 1) return e;
+    hipLaunchKernelGGL(attention_combine, dim3((unsigned)(g.units * kGrpHeads)), dim3(256), 0, s, g);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention_rows(const AttnArgs &a, hipStream_t s) {
     const bool vec = a.hd % 4 == 0 && aligned16(a.q) && aligned16(a.k);
     const dim3 grid((unsigned)((a.rows + 3) / 4));
     const int nd = (a.hd + 63) / 64;
@@ -502,7 +945,7 @@ tbh_status tbh_attention_device(tbh_device *dev, const tbh_attention_shape *shap
     a.v = v;
     a.mask = mask;
     a.out = out;
-    hipError_t e = launch_attention(a, (hipStream_t)stream);
+    hipError_t e = launch_attention(dev, a, (hipStream_t)stream);
     return e == hipSuccess ? TBH_OK : hip_error(e, "attention launch");
 }
 
@@ -521,7 +964,7 @@ tbh_status tbh_attention(tbh_device *dev, const tbh_attention_shape *shape, cons
                          a.v = (const float *)d[2];
                          a.mask = (const float *)d[3];
                          a.out = (float *)o;
-                         return launch_attention(a, s);
+                         return launch_attention(dev, a, s);
                      });
 }
 
