@@ -14,10 +14,12 @@
 //     h += W_down . (silu(gate) * up)                          (:449-457)
 //   logits = W_lm . rmsnorm(h) * g_final                       (:186-199)
 //
-// Five launches per layer: Q|K|V and gate|up are each one weight
+// Six launches per layer: Q|K|V and gate|up are each one weight
 // (concatenated along N at set-up), RMSNorm and SiLU*up run in the GEMV's x
-// staging, the residual adds in its epilogue, and one attention kernel does
-// RoPE, the cache append, softmax and the context.  The token position lives
+// staging, the residual adds in its epilogue, and attention is two kernels:
+// one block per (KV head, 64 cache positions) does RoPE, the cache append
+// and that range's softmax partials for the KV head's query heads, and a
+// merge kernel assembles the context.  The token position lives
 // in device memory and the step ends with a one-thread kernel that advances
 // it, so a captured step replays as the next one.
 #include <cmath>
@@ -26,6 +28,7 @@
 #include <vector>
 
 #include "tbh_internal.h"
+#include "tbh_wave.h"
 
 struct tbh_decoder {
     tbh_device *dev = nullptr;
@@ -42,6 +45,9 @@ struct tbh_decoder {
     float *kcache = nullptr;     // [layers][max_seq][kv_dim]
     float *vcache = nullptr;
     float *h = nullptr, *qkv = nullptr, *ctx = nullptr, *gu = nullptr, *logits = nullptr;
+    float *attn_part = nullptr;  // attention split partials (one layer at a time)
+    float *rope_theta = nullptr; // [head_dim / 2] RoPE frequencies
+    int32_t attn_hchunks = 1, attn_splits = 1;
     int32_t *pos = nullptr;      // [0] position, [1] overflow flag
     std::vector<void *> allocs;
 };
@@ -53,21 +59,17 @@ struct AttnParams {
     const float *qkv;
     float *kcache, *vcache;  // this layer
     float *ctx;
+    float *part;             // [units][splits][2 * kGroup + kGroup * hd] split partials
+    const float *theta;      // [hd / 2]: base^(-2i / hd), fp32
     int32_t *pos;            // [0] position, [1] overflow flag
     int32_t nh, nkv, hd, kvd, hidden, max_seq;
+    int32_t rep, hchunks, splits;  // units = nkv * hchunks blocks per split
     float rope_base, scale;
 };
 
-constexpr int kAttnThreads = 512;
-constexpr int kAttnUnits = 20;  // K and V float4 loads per thread per batch
 constexpr int kMaxHd = 128;
-
-// Positions one batch covers: every thread loads kAttnUnits float4 of K and
-// of V, so a batch is kAttnUnits * kAttnThreads / (hd / 4) positions.
-__host__ __device__ inline int attn_batch(int hd) { return kAttnUnits * kAttnThreads / (hd / 4); }
-// LDS floats: q, new k, new v [hd] each; wave partials [8]; per-thread
-// context partials [kAttnThreads][4].
-__host__ __device__ inline int attn_lds_floats(int hd) { return 3 * hd + 8 + 4 * kAttnThreads; }
+constexpr int kSplit = 64;   // cache positions one attention block covers
+constexpr int kGroup = 8;    // query heads (of one KV head) one block serves
 
 __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
@@ -75,145 +77,273 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// One block per query head h, KV group h / (num_heads / num_kv_heads)
-// (ModelRunner.swift:524-536).  RoPE (interleaved pairs, theta =
-// base^(-i/hd), fp32; :470-494) on q and the new k; the first head of each
-// group appends the new k and v to the cache at pos (:503-516) and every
-// block uses its own copy for position pos.  Positions go in batches: each
-// thread issues all its K and V loads of a batch together (thread <-> one
-// float4 column of hd/4 and positions tid/(hd/4) + i * 512/(hd/4)), scores
-// them against q with the hd/4 lanes of a row summed by shuffles, and the
-// block keeps a running max / sum / context (the softmax of :545-551) over
-// the batches.  One launch produces the context; HBM latency is paid about
-// once per batch.
-__global__ __launch_bounds__(kAttnThreads) void attention_head(const AttnParams a) {
-    extern __shared__ float lds[];
-    const int h = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int rep = a.nh / a.nkv, kvh = h / rep, hd = a.hd, H4 = hd / 4;
-    float *qs = lds;              // [hd]
-    float *kn = qs + hd;          // [hd]
-    float *vn = kn + hd;          // [hd]
-    float *red = vn + hd;         // [8]
-    float4 *cs = (float4 *)(red + 8);  // [kAttnThreads]
+// sin and cos of a RoPE angle formed in fp32 as the reference forms it
+// (Float(pos) * theta, ModelRunner.swift:480-486).  The angle is reduced by
+// 2 pi in double precision first, so sincosf only sees |r| <= pi and never
+// takes its large-argument path (a table walk in memory on the critical
+// path of the kernel).
+__device__ __forceinline__ void rope_sincos(float ang, float *sn, float *cs) {
+    const double a = (double)ang;
+    const double k = rint(a * 0.15915494309189535);  // 1 / (2 pi)
+    sincosf((float)fma(-k, 6.283185307179586, a), sn, cs);
+}
 
-    // Everything that does not depend on the position is loaded before it:
-    // this thread's RoPE pair and v element, and the first batch's K / V rows
-    // 0..NB-1 (in bounds whatever the position; rows past it are masked).
-    const int NB = attn_batch(hd);
-    const int d4 = tid % H4, j0 = tid / H4, jstep = kAttnThreads / H4;
-    const int64_t col = (int64_t)kvh * hd + 4 * d4;
-    float4 kv[kAttnUnits], vv[kAttnUnits];
-    auto load_batch = [&](int b0, int nb) {
-#pragma unroll
-        for (int i = 0; i < kAttnUnits; ++i) {
-            const int64_t row = (int64_t)(b0 + min(j0 + i * jstep, nb - 1)) * a.kvd + col;
-            kv[i] = *(const float4 *)&a.kcache[row];
-            vv[i] = *(const float4 *)&a.vcache[row];
-        }
-    };
-    load_batch(0, min(NB, a.max_seq));
-    const float *qin = a.qkv + (int64_t)h * hd;
-    const float *kin = a.qkv + a.hidden + kvh * hd;
-    const float *vin = a.qkv + a.hidden + a.kvd + kvh * hd;
-    const int jr = tid < hd ? tid : 0, ir = 2 * (jr % (hd / 2));
-    const float *src = jr < hd / 2 ? qin : kin;
-    const float x0 = src[ir], x1 = src[ir + 1];
-    const float vx = vin[jr];
+__device__ __forceinline__ float wave_max(float v) { return wave::max(v); }
+__device__ __forceinline__ float wave_sum(float v) { return wave::sum(v); }
+
+// Orders a wave's LDS writes before its later LDS reads by other lanes of
+// the same wave (no block barrier: the waves of a block are independent).
+__device__ __forceinline__ void wave_lds_fence() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+}
+
+// Attention of one decode step, split over the cache.  One wave per (query
+// head, range of kSplit positions <= pos): it writes the range's softmax
+// partial -- max m, sum l of exp(score - m), and sum of exp(score - m) * v --
+// and attention_merge combines the ranges.  A block's four waves are four
+// query heads of one KV head (ModelRunner.swift:524-536, kvHead = head /
+// repeats), so they share the range's key and value rows through L1; the
+// grid covers max_seq and waves past pos return at once.
+//
+// Every global load is issued before the position is read: the position,
+// this step's q, k, v and RoPE frequencies, and the range's cache rows (the
+// cache is zero-filled at creation and only ever holds finite values, so
+// rows past pos are harmless -- they get p = 0 -- and row pos is replaced by
+// the new k and v).  The wave applies RoPE (interleaved pairs, fp32;
+// :470-494) to its query head and the new k, scores one position per lane,
+// reduces max and sum with DPP, and sums p * v with 16-byte value pieces
+// (lane (pg, d4) covers rows pg, pg + 64 / (hd / 4), ...).  The wave of the
+// group's first head appends the new k and v to the cache (:503-516).
+template <int HD>
+__global__ __launch_bounds__(256) void attention_split(const AttnParams a) {
+    constexpr int HD4 = HD / 4, PPI = 64 / HD4, NV = (kSplit + PPI - 1) / PPI, NP = HD / 2;
+    constexpr int NPL = (NP + 63) / 64;  // RoPE pairs per lane
+    __shared__ __attribute__((aligned(16))) float qs[4][HD];
+    __shared__ __attribute__((aligned(16))) float kn[4][HD];
+    __shared__ __attribute__((aligned(16))) float vn[4][HD];
+    __shared__ float ps[4][kSplit];
+    __shared__ float4 red[4][64];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nquad = (a.rep + 3) / 4;
+    const int split = blockIdx.x % a.splits;
+    const int quad = (blockIdx.x / a.splits) % nquad;
+    const int kvh = blockIdx.x / (a.splits * nquad);
+    const int hg = quad * 4 + w;                // head within the KV group
+    if (hg >= a.rep) return;
+    const int head = kvh * a.rep + hg;
+    const int c0 = split * kSplit;
+    const int64_t kvo = (int64_t)kvh * HD;
+    const int last = a.max_seq - 1;
 
     const int pos = a.pos[0];
+    float qx0[NPL], qx1[NPL], kx0[NPL], kx1[NPL], th[NPL];
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+        const int pr = min(lane + 64 * i, NP - 1);
+        qx0[i] = a.qkv[head * HD + 2 * pr];
+        qx1[i] = a.qkv[head * HD + 2 * pr + 1];
+        kx0[i] = a.qkv[a.hidden + kvo + 2 * pr];
+        kx1[i] = a.qkv[a.hidden + kvo + 2 * pr + 1];
+        th[i] = a.theta[pr];
+    }
+    float vx[NPL * 2];
+#pragma unroll
+    for (int i = 0; i < 2 * NPL; ++i) vx[i] = a.qkv[a.hidden + a.kvd + kvo + min(lane + 64 * i, HD - 1)];
+    float4 kreg[HD4];
+    {
+        const float *kr = a.kcache + (int64_t)min(c0 + lane, last) * a.kvd + kvo;
+#pragma unroll
+        for (int i = 0; i < HD4; ++i) kreg[i] = *(const float4 *)(kr + 4 * i);
+    }
+    const int pg = lane / HD4, d4 = lane % HD4;
+    float4 vreg[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int r = min(pg + j * PPI, kSplit - 1);
+        vreg[j] = *(const float4 *)(a.vcache + (int64_t)min(c0 + r, last) * a.kvd + kvo + 4 * d4);
+    }
     if (pos < 0 || pos >= a.max_seq) {  // cache full: flag it, write nothing
-        if (h == 0 && tid == 0) a.pos[1] = 1;
+        if (blockIdx.x == 0 && threadIdx.x == 0) a.pos[1] = 1;
         return;
     }
-    const int n = pos + 1;
-    if (tid < hd) {
-        const float theta = powf(a.rope_base, -((float)ir / (float)hd));
-        const float ang = (float)pos * theta;
-        const float c = cosf(ang), sn = sinf(ang);
-        float *dst = jr < hd / 2 ? qs : kn;
-        dst[ir] = x0 * c - x1 * sn;
-        dst[ir + 1] = x0 * sn + x1 * c;
-        vn[tid] = vx;
-    }
-    lds_barrier();
-    if (h % rep == 0)
-        for (int d = tid; d < hd; d += kAttnThreads) {
-            a.kcache[(int64_t)pos * a.kvd + kvh * hd + d] = kn[d];
-            a.vcache[(int64_t)pos * a.kvd + kvh * hd + d] = vn[d];
-        }
-    const float4 q4 = *(const float4 *)&qs[4 * d4];
-    const float4 kn4 = *(const float4 *)&kn[4 * d4], vn4 = *(const float4 *)&vn[4 * d4];
+    if (c0 > pos) return;
 
-    float M = -INFINITY, L = 0.0f;
-    float4 C = float4{0.f, 0.f, 0.f, 0.f};
-    for (int b0 = 0; b0 < n; b0 += NB) {
-        const int nb = min(NB, n - b0);
-        if (b0 > 0) load_batch(b0, nb);
-        // scores of this thread's positions (the hd/4 lanes of a row summed)
-        float sc[kAttnUnits];
-        float mx = -INFINITY;
+    // RoPE at pos for this head's q and the new k; the new v
 #pragma unroll
-        for (int i = 0; i < kAttnUnits; ++i) {
-            const int j = j0 + i * jstep;
-            const float4 k4 = b0 + j == pos ? kn4 : kv[i];
-            float dot = q4.x * k4.x;
-            dot = __builtin_fmaf(q4.y, k4.y, dot);
-            dot = __builtin_fmaf(q4.z, k4.z, dot);
-            dot = __builtin_fmaf(q4.w, k4.w, dot);
-            for (int o = 1; o < H4; o <<= 1) dot += __shfl_xor(dot, o);
-            sc[i] = j < nb ? dot * a.scale : -INFINITY;
-            mx = fmaxf(mx, sc[i]);
+    for (int i = 0; i < NPL; ++i) {
+        const int pr = lane + 64 * i;
+        if (pr < NP) {
+            float c, sn;
+            rope_sincos((float)pos * th[i], &sn, &c);
+            qs[w][2 * pr] = qx0[i] * c - qx1[i] * sn;
+            qs[w][2 * pr + 1] = qx0[i] * sn + qx1[i] * c;
+            kn[w][2 * pr] = kx0[i] * c - kx1[i] * sn;
+            kn[w][2 * pr + 1] = kx0[i] * sn + kx1[i] * c;
         }
-        // block max of the batch
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-        if (lane == 0) red[wave] = mx;
-        lds_barrier();
-        mx = red[0];
-        for (int w = 1; w < kAttnThreads / 64; ++w) mx = fmaxf(mx, red[w]);
-        const float mnew = fmaxf(M, mx);
-        const float f = expf(M - mnew);
-        float ps = 0.0f;
-        float4 cb = float4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int i = 0; i < kAttnUnits; ++i) {
-            const int j = j0 + i * jstep;
-            const float p = j < nb ? expf(sc[i] - mnew) : 0.0f;
-            const float4 v4 = b0 + j == pos ? vn4 : vv[i];
-            ps += d4 == 0 ? p : 0.0f;  // one copy per position
-            cb.x = __builtin_fmaf(p, v4.x, cb.x);
-            cb.y = __builtin_fmaf(p, v4.y, cb.y);
-            cb.z = __builtin_fmaf(p, v4.z, cb.z);
-            cb.w = __builtin_fmaf(p, v4.w, cb.w);
-        }
-        // block sum of the batch
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) ps += __shfl_xor(ps, o);
-        lds_barrier();  // every wave has read red[] (the max)
-        if (lane == 0) red[wave] = ps;
-        lds_barrier();
-        ps = 0.0f;
-        for (int w = 0; w < kAttnThreads / 64; ++w) ps += red[w];
-        L = L * f + ps;
-        M = mnew;
-        C = float4{__builtin_fmaf(C.x, f, cb.x), __builtin_fmaf(C.y, f, cb.y),
-                   __builtin_fmaf(C.z, f, cb.z), __builtin_fmaf(C.w, f, cb.w)};
-        lds_barrier();  // red[] free for the next batch
     }
-    // context: sum the partials of the threads that share a float4 column
-    cs[tid] = C;
-    lds_barrier();
-    if (tid < H4) {
-        float4 r = float4{0.f, 0.f, 0.f, 0.f};
-        for (int k = 0; k < jstep; ++k) {
-            const float4 c = cs[tid + k * H4];
-            r.x += c.x;
-            r.y += c.y;
-            r.z += c.z;
-            r.w += c.w;
+#pragma unroll
+    for (int i = 0; i < 2 * NPL; ++i)
+        if (lane + 64 * i < HD) vn[w][lane + 64 * i] = vx[i];
+    wave_lds_fence();
+
+    // one position per lane
+    const int t = c0 + lane;
+    const bool tvalid = t <= pos, tnew = t == pos;
+    float d = 0.0f;
+#pragma unroll
+    for (int i = 0; i < HD4; ++i) {
+        const float4 k4 = tnew ? *(const float4 *)&kn[w][4 * i] : kreg[i];
+        const float4 q4 = *(const float4 *)&qs[w][4 * i];
+        d += q4.x * k4.x + q4.y * k4.y + q4.z * k4.z + q4.w * k4.w;
+    }
+    const float sc = tvalid ? d * a.scale : -INFINITY;
+    const float m = wave::max(sc);                    // finite: position c0 <= pos
+    const float p = tvalid ? expf(sc - m) : 0.0f;
+    const float l = wave::sum(p);
+    ps[w][lane] = p;
+    wave_lds_fence();
+
+    float4 acc = float4{0.f, 0.f, 0.f, 0.f};
+    if (pg < PPI) {
+        const float4 vn4 = *(const float4 *)&vn[w][4 * d4];
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int r = pg + j * PPI;
+            if (r < kSplit) {
+                const float4 v4 = c0 + r == pos ? vn4 : vreg[j];
+                const float pr = ps[w][r];
+                acc.x += pr * v4.x;
+                acc.y += pr * v4.y;
+                acc.z += pr * v4.z;
+                acc.w += pr * v4.w;
+            }
         }
-        const float inv = 1.0f / L;
-        *(float4 *)&a.ctx[h * hd + 4 * tid] = float4{r.x * inv, r.y * inv, r.z * inv, r.w * inv};
+    }
+    red[w][lane] = acc;
+    wave_lds_fence();
+
+    const int unit = kvh * a.hchunks + hg / kGroup, hs = hg % kGroup;
+    float *part = a.part + ((int64_t)unit * a.splits + split) * (2 * kGroup + kGroup * HD);
+    if (lane == 0) {
+        part[hs] = m;
+        part[kGroup + hs] = l;
+    }
+    if (lane < HD4) {
+        float4 o = red[w][lane];
+#pragma unroll
+        for (int q = 1; q < PPI; ++q) {
+            const float4 v = red[w][q * HD4 + lane];
+            o.x += v.x;
+            o.y += v.y;
+            o.z += v.z;
+            o.w += v.w;
+        }
+        *(float4 *)&part[2 * kGroup + hs * HD + 4 * lane] = o;
+        // append the new k and v (the group's first head, range holding pos);
+        // the row-pos values this launch loaded are never used
+        if (hg == 0 && pos < c0 + kSplit) {
+            *(float4 *)&a.kcache[(int64_t)pos * a.kvd + kvo + 4 * lane] = *(const float4 *)&kn[w][4 * lane];
+            *(float4 *)&a.vcache[(int64_t)pos * a.kvd + kvo + 4 * lane] = *(const float4 *)&vn[w][4 * lane];
+        }
+    }
+}
+
+// ctx of head h = sum over splits of e^(m_s - M) o_s / sum of e^(m_s - M) l_s
+// with M = max m_s (the softmax of :545-551 assembled from the ranges).  One
+// block per (unit, head).  Thread (sg, d4) loads the partials of splits
+// sg, sg + 256 / (hd / 4), ... (up to kMergeLoads of them) together with the
+// position, so the usual case costs one memory round trip; splits past pos
+// are masked out afterwards.
+constexpr int kMergeLoads = 4;
+
+template <int HD>
+__global__ __launch_bounds__(256) void attention_merge(const AttnParams a) {
+    constexpr int HD4 = HD / 4, NSG = 256 / HD4;
+    constexpr int64_t kStride = 2 * kGroup + kGroup * HD;
+    __shared__ float4 red[256];
+    __shared__ float rs[8];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int unit = blockIdx.x / kGroup, h = blockIdx.x % kGroup;
+    const int hc = unit % a.hchunks, kvh = unit / a.hchunks;
+    if (h >= a.rep - hc * kGroup) return;
+    const float *pb = a.part + (int64_t)unit * a.splits * kStride;
+    const int sg = tid / HD4, d4 = tid % HD4;
+    const bool slane = sg < NSG;
+    const int pos = a.pos[0];
+    float mv[kMergeLoads], lv[kMergeLoads];
+    float4 ov[kMergeLoads];
+#pragma unroll
+    for (int j = 0; j < kMergeLoads; ++j) {
+        const int sp = min(sg + NSG * j, a.splits - 1);
+        mv[j] = pb[sp * kStride + h];
+        lv[j] = pb[sp * kStride + kGroup + h];
+        ov[j] = *(const float4 *)(pb + sp * kStride + 2 * kGroup + h * HD + 4 * d4);
+    }
+    if (pos < 0 || pos >= a.max_seq) return;
+    const int ns = pos / kSplit + 1;
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kMergeLoads; ++j)
+        if (slane && sg + NSG * j < ns) mloc = fmaxf(mloc, mv[j]);
+    for (int sp = sg + NSG * kMergeLoads; slane && sp < ns; sp += NSG) mloc = fmaxf(mloc, pb[sp * kStride + h]);
+    mloc = wave::max(mloc);
+    if (lane == 0) rs[wv] = mloc;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(rs[0], rs[1]), fmaxf(rs[2], rs[3]));
+    float L = 0.0f;
+    float4 o = float4{0.f, 0.f, 0.f, 0.f};
+    auto add = [&](float m, float l, float4 v) {
+        const float e = expf(m - M);
+        if (d4 == 0) L += e * l;   // one thread per split counts its sum
+        o.x += e * v.x;
+        o.y += e * v.y;
+        o.z += e * v.z;
+        o.w += e * v.w;
+    };
+#pragma unroll
+    for (int j = 0; j < kMergeLoads; ++j)
+        if (slane && sg + NSG * j < ns) add(mv[j], lv[j], ov[j]);
+    for (int sp = sg + NSG * kMergeLoads; slane && sp < ns; sp += NSG)
+        add(pb[sp * kStride + h], pb[sp * kStride + kGroup + h],
+            *(const float4 *)(pb + sp * kStride + 2 * kGroup + h * HD + 4 * d4));
+    L = wave::sum(L);
+    if (lane == 0) rs[4 + wv] = L;
+    red[tid] = o;
+    __syncthreads();
+    if (tid < HD4) {
+        float4 r = float4{0.f, 0.f, 0.f, 0.f};
+        for (int q = 0; q < NSG; ++q) {
+            const float4 v = red[q * HD4 + tid];
+            r.x += v.x;
+            r.y += v.y;
+            r.z += v.z;
+            r.w += v.w;
+        }
+        const float inv = 1.0f / ((rs[4] + rs[5]) + (rs[6] + rs[7]));
+        const int head = kvh * a.rep + hc * kGroup + h;
+        *(float4 *)&a.ctx[(int64_t)head * HD + 4 * tid] = float4{r.x * inv, r.y * inv, r.z * inv, r.w * inv};
+    }
+}
+
+template <int HD>
+void launch_attention_hd(const AttnParams &ap, hipStream_t s) {
+    const int units = ap.nkv * ap.hchunks, nquad = (ap.rep + 3) / 4;
+    hipLaunchKernelGGL(attention_split<HD>, dim3((unsigned)(ap.nkv * nquad * ap.splits)), dim3(256), 0, s, ap);
+    hipLaunchKernelGGL(attention_merge<HD>, dim3((unsigned)(units * kGroup)), dim3(256), 0, s, ap);
+}
+
+void launch_attention(const AttnParams &ap, hipStream_t s) {
+    switch (ap.hd) {
+    case 16: launch_attention_hd<16>(ap, s); break;
+    case 32: launch_attention_hd<32>(ap, s); break;
+    case 48: launch_attention_hd<48>(ap, s); break;
+    case 64: launch_attention_hd<64>(ap, s); break;
+    case 80: launch_attention_hd<80>(ap, s); break;
+    case 96: launch_attention_hd<96>(ap, s); break;
+    case 112: launch_attention_hd<112>(ap, s); break;
+    default: launch_attention_hd<128>(ap, s); break;
     }
 }
 
@@ -404,6 +534,17 @@ tbh_status tbh_decoder_create(tbh_device *dev, const tbh_decoder_config *cfg, co
     if ((st = dmalloc(d.get(), &d->gu, 2 * (size_t)c.intermediate)) != TBH_OK) return st;
     if ((st = dmalloc(d.get(), &d->logits, (size_t)c.vocab)) != TBH_OK) return st;
     if ((st = dmalloc(d.get(), &d->pos, 2)) != TBH_OK) return st;
+    const int32_t rep = c.num_heads / c.num_kv_heads;
+    d->attn_hchunks = (rep + kGroup - 1) / kGroup;
+    d->attn_splits = (c.max_seq + kSplit - 1) / kSplit;
+    const size_t part = (size_t)c.num_kv_heads * d->attn_hchunks * d->attn_splits * (2 * kGroup + kGroup * hd);
+    if ((st = dmalloc(d.get(), &d->attn_part, part)) != TBH_OK) return st;
+    // RoPE frequencies theta_i = base^(-2i / hd) in fp32 (ModelRunner.swift:476-479)
+    std::vector<float> theta((size_t)hd / 2);
+    for (int32_t i = 0; i < hd / 2; ++i) theta[(size_t)i] = std::pow(c.rope_base, -((float)(2 * i) / (float)hd));
+    if ((st = dmalloc(d.get(), &d->rope_theta, theta.size())) != TBH_OK) return st;
+    if (hipMemcpy(d->rope_theta, theta.data(), theta.size() * sizeof(float), hipMemcpyHostToDevice) != hipSuccess)
+        return set_error(TBH_E_HIP, "tbh_decoder_create: upload RoPE frequencies");
     if (hipMemcpy(d->emb, embeddings, (size_t)c.vocab * H * sizeof(float), hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(d->norms + 2 * L * H, final_norm, H * sizeof(float), hipMemcpyHostToDevice) != hipSuccess ||
         hipMemset(d->pos, 0, 2 * sizeof(int32_t)) != hipSuccess ||
@@ -509,8 +650,12 @@ tbh_status tbh_decoder_step_device(tbh_decoder *d, int32_t token, float *logits,
     ap.hidden = c.hidden;
     ap.max_seq = c.max_seq;
     ap.rope_base = c.rope_base;
+    ap.part = d->attn_part;
+    ap.theta = d->rope_theta;
+    ap.rep = c.num_heads / c.num_kv_heads;
+    ap.hchunks = d->attn_hchunks;
+    ap.splits = d->attn_splits;
     ap.scale = 1.0f / std::sqrt((float)d->head_dim);
-    const size_t attn_lds = (size_t)attn_lds_floats(d->head_dim) * sizeof(float);
     hipError_t e = hipSuccess;
     for (int32_t l = 0; l < c.num_layers && e == hipSuccess; ++l) {
         const auto &L = d->layers[(size_t)l];
@@ -519,7 +664,7 @@ tbh_status tbh_decoder_step_device(tbh_decoder *d, int32_t token, float *logits,
         if (e != hipSuccess) break;
         ap.kcache = d->kcache + (size_t)l * c.max_seq * d->kv_dim;
         ap.vcache = d->vcache + (size_t)l * c.max_seq * d->kv_dim;
-        hipLaunchKernelGGL(attention_head, dim3((unsigned)c.num_heads), dim3(kAttnThreads), attn_lds, s, ap);
+        launch_attention(ap, s);
         e = launch_gemv_fused(*L.o, FusedGemvArgs{d->ctx, nullptr, nullptr, 0.0f, d->h, 0, 1}, s);
         if (e != hipSuccess) break;
         e = launch_gemv_fused(*L.gu, FusedGemvArgs{d->h, nullptr, g_post, c.rms_eps, d->gu, 1, 0}, s);

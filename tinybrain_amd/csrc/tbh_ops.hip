@@ -26,6 +26,7 @@
 #include <cstring>
 
 #include "tbh_internal.h"
+#include "tbh_wave.h"
 
 namespace tbh {
 namespace {
@@ -35,17 +36,8 @@ constexpr float kAttnEps = 1e-7f;      // FlashAttention.metal final division
 constexpr int64_t kWaveRowMax = 1024;  // longest row one wave handles
 constexpr int kAttnMaxHeadDim = 256;
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
-}
+__device__ __forceinline__ float wave_sum(float v) { return wave::sum(v); }
+__device__ __forceinline__ float wave_max(float v) { return wave::max(v); }
 
 // (max, sum of exp(x - max)) pairs: merge b into a.  An empty pair is
 // (-inf, 0).
@@ -81,10 +73,22 @@ __device__ __forceinline__ float row_sum(float v, float *red) {
 
 template <int W>
 __device__ __forceinline__ void row_ms(float &m, float &s, float *red) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float m2 = __shfl_xor(m, o), s2 = __shfl_xor(s, o);
+    // pairs of partner lanes merged with DPP inside each 16-lane row, then
+    // the four rows through readlane
+    {
+        float m2 = wave::dpp<wave::kXor1>(m), s2 = wave::dpp<wave::kXor1>(s);
         ms_merge(m, s, m2, s2);
+        m2 = wave::dpp<wave::kXor2>(m), s2 = wave::dpp<wave::kXor2>(s);
+        ms_merge(m, s, m2, s2);
+        m2 = wave::dpp<wave::kHalfMirror>(m), s2 = wave::dpp<wave::kHalfMirror>(s);
+        ms_merge(m, s, m2, s2);
+        m2 = wave::dpp<wave::kRowMirror>(m), s2 = wave::dpp<wave::kRowMirror>(s);
+        ms_merge(m, s, m2, s2);
+        float mm = wave::lane_value(m, 0), ss = wave::lane_value(s, 0);
+#pragma unroll
+        for (int r = 16; r < 64; r += 16) ms_merge(mm, ss, wave::lane_value(m, r), wave::lane_value(s, r));
+        m = mm;
+        s = ss;
     }
     if (W == 1) return;
     const int wave = threadIdx.x >> 6;
@@ -262,7 +266,7 @@ __global__ __launch_bounds__(256) void attention_rows(const AttnArgs a) {
         for (int i = 0; i < ND; ++i) o[i] *= corr;
         const int nt = (int)std::min<int64_t>(64, a.kv_len - t0);
         for (int j = 0; j < nt; ++j) {
-            const float pj = __shfl(p, j);
+            const float pj = wave::lane_value(p, j);
             const float *vr = vb + (t0 + j) * kvd;
 #pragma unroll
             for (int i = 0; i < ND; ++i) {
