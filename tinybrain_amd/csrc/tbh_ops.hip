@@ -48,6 +48,17 @@ __device__ __forceinline__ void ms_merge(float &m, float &s, float m2, float s2)
     m = mm;
 }
 
+// Four values at once: one rescale per float4 instead of one per element.
+__device__ __forceinline__ void ms_add4(float &m, float &s, float4 v) {
+    const float mx = fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w));
+    if (mx == -INFINITY) return;
+    if (mx > m) {
+        s *= expf(m - mx);
+        m = mx;
+    }
+    s += (expf(v.x - m) + expf(v.y - m)) + (expf(v.z - m) + expf(v.w - m));
+}
+
 __device__ __forceinline__ void ms_add(float &m, float &s, float x) {
     if (x == -INFINITY) return;  // contributes exp(-inf) = 0
     if (x > m) {
@@ -68,7 +79,10 @@ __device__ __forceinline__ float row_sum(float v, float *red) {
     __syncthreads();
     if ((threadIdx.x & 63) == 0) red[wave] = v;
     __syncthreads();
-    return red[0] + red[1] + red[2] + red[3];
+    float t = 0.0f;
+#pragma unroll
+    for (int i = 0; i < W; ++i) t += red[i];
+    return t;
 }
 
 template <int W>
@@ -101,17 +115,19 @@ __device__ __forceinline__ void row_ms(float &m, float &s, float *red) {
     m = red[0];
     s = red[1];
 #pragma unroll
-    for (int i = 1; i < 4; ++i) ms_merge(m, s, red[2 * i], red[2 * i + 1]);
+    for (int i = 1; i < W; ++i) ms_merge(m, s, red[2 * i], red[2 * i + 1]);
 }
 
-// Softmax over rows.  W = waves per row (1: four rows per block; 4: one row
-// per block).  VEC: 16-byte loads and stores (cols % 4 == 0, aligned rows).
+// Softmax over rows.  W = waves per row (1: four rows per 256-thread block;
+// 16: one row per 1024-thread block).  VEC: 16-byte loads and stores
+// (cols % 4 == 0, aligned rows).
 template <int W, bool VEC>
-__global__ __launch_bounds__(256) void softmax_rows(const float *__restrict__ x, float *__restrict__ y,
-                                                    int64_t rows, int64_t cols) {
-    __shared__ float red[8];
+__global__ __launch_bounds__(W == 1 ? 256 : 64 * W) void softmax_rows(const float *__restrict__ x,
+                                                                     float *__restrict__ y, int64_t rows,
+                                                                     int64_t cols) {
+    __shared__ float red[2 * W];
     constexpr int T = 64 * W;
-    const int64_t row = (int64_t)blockIdx.x * (4 / W) + (threadIdx.x / T);
+    const int64_t row = W == 1 ? (int64_t)blockIdx.x * 4 + (threadIdx.x / T) : (int64_t)blockIdx.x;
     const int t = threadIdx.x % T;
     // Rows past the end compute on the last row and store nothing, so every
     // thread reaches the block barriers.
@@ -119,13 +135,7 @@ __global__ __launch_bounds__(256) void softmax_rows(const float *__restrict__ x,
     const float *xr = x + r * cols;
     float m = -INFINITY, s = 0.0f;
     if (VEC) {
-        for (int64_t i = t; i < cols / 4; i += T) {
-            const float4 v = ((const float4 *)xr)[i];
-            ms_add(m, s, v.x);
-            ms_add(m, s, v.y);
-            ms_add(m, s, v.z);
-            ms_add(m, s, v.w);
-        }
+        for (int64_t i = t; i < cols / 4; i += T) ms_add4(m, s, ((const float4 *)xr)[i]);
     } else {
         for (int64_t i = t; i < cols; i += T) ms_add(m, s, xr[i]);
     }
@@ -700,8 +710,8 @@ hipError_t launch_softmax(const float *x, int64_t rows, int64_t cols, float *y, 
         else hipLaunchKernelGGL((softmax_rows<1, false>), grid, dim3(256), 0, s, x, y, rows, cols);
     } else {
         const dim3 grid((unsigned)rows);
-        if (vec) hipLaunchKernelGGL((softmax_rows<4, true>), grid, dim3(256), 0, s, x, y, rows, cols);
-        else hipLaunchKernelGGL((softmax_rows<4, false>), grid, dim3(256), 0, s, x, y, rows, cols);
+        if (vec) hipLaunchKernelGGL((softmax_rows<16, true>), grid, dim3(1024), 0, s, x, y, rows, cols);
+        else hipLaunchKernelGGL((softmax_rows<16, false>), grid, dim3(1024), 0, s, x, y, rows, cols);
     }
     return hipGetLastError();
 }
