@@ -10,13 +10,16 @@
 //     q, k <- RoPE(pos); append k, v to the cache; ctx = softmax(q K^T / sqrt(d)) V
 //                                                              (:470-592)
 //     h += W_o . ctx                                           (:434)
-//     gu  = W_gate|up . rmsnorm(h) * g_post                    (:436-451)
-//     h += W_down . (silu(gate) * up)                          (:449-457)
+//     act = silu(W_gate . x) * (W_up . x), x = rmsnorm(h) * g_post
+//                                                              (:436-451)
+//     h += W_down . act                                        (:452-457)
 //   logits = W_lm . rmsnorm(h) * g_final                       (:186-199)
 //
 // Six launches per layer: Q|K|V and gate|up are each one weight
-// (concatenated along N at set-up), RMSNorm and SiLU*up run in the GEMV's x
-// staging, the residual adds in its epilogue, and attention is two kernels:
+// (concatenated along N at set-up; gate and up rows interleaved so one wave
+// holds both rows of a pair and its epilogue writes silu(gate) * up),
+// RMSNorm runs in the GEMV's x staging, the residual adds in its epilogue,
+// and attention is two kernels:
 // one block per (KV head, 64 cache positions) does RoPE, the cache append
 // and that range's softmax partials for the KV head's query heads, and a
 // merge kernel assembles the context.  The token position lives
@@ -441,11 +444,63 @@ tbh_status concat_n(const tbh_qtensor_desc *const *parts, int n, OwnedDesc &out)
     return TBH_OK;
 }
 
+// Reorders a two-part concatenation [A | B] (N = 2 * half outputs) so that
+// output 2j is A's j and output 2j + 1 is B's j.
+void interleave_halves(OwnedDesc &od) {
+    const int64_t K = od.d.K, N = od.d.N, half = N / 2;
+    const bool has_zp = !od.zp.empty();
+    if (od.d.precision == TBH_PREC_INT8) {   // [K][N] bytes, one scale per column
+        std::vector<int8_t> data(od.data.size());
+        for (int64_t k = 0; k < K; ++k)
+            for (int64_t j = 0; j < half; ++j) {
+                data[(size_t)(k * N + 2 * j)] = od.data[(size_t)(k * N + j)];
+                data[(size_t)(k * N + 2 * j + 1)] = od.data[(size_t)(k * N + half + j)];
+            }
+        od.data.swap(data);
+        std::vector<float> sc(od.scales.size());
+        std::vector<int8_t> zp(od.zp.size());
+        for (int64_t j = 0; j < half; ++j) {
+            sc[(size_t)(2 * j)] = od.scales[(size_t)j];
+            sc[(size_t)(2 * j + 1)] = od.scales[(size_t)(half + j)];
+            if (has_zp) {
+                zp[(size_t)(2 * j)] = od.zp[(size_t)j];
+                zp[(size_t)(2 * j + 1)] = od.zp[(size_t)(half + j)];
+            }
+        }
+        od.scales.swap(sc);
+        od.zp.swap(zp);
+    } else {   // converter layout: N rows of K / 2 bytes, G = K / gs scales per row
+        const int64_t rb = K / 2, G = K / od.d.group_size;
+        std::vector<int8_t> data(od.data.size());
+        std::vector<float> sc(od.scales.size());
+        std::vector<int8_t> zp(od.zp.size());
+        for (int64_t j = 0; j < half; ++j)
+            for (int p = 0; p < 2; ++p) {
+                const int64_t src = p * half + j, dst = 2 * j + p;
+                std::memcpy(&data[(size_t)(dst * rb)], &od.data[(size_t)(src * rb)], (size_t)rb);
+                std::memcpy(&sc[(size_t)(dst * G)], &od.scales[(size_t)(src * G)], (size_t)G * sizeof(float));
+                if (has_zp) std::memcpy(&zp[(size_t)(dst * G)], &od.zp[(size_t)(src * G)], (size_t)G);
+            }
+        od.data.swap(data);
+        od.scales.swap(sc);
+        od.zp.swap(zp);
+    }
+    od.d.data = od.data.data();
+    od.d.scales = od.scales.data();
+    od.d.zero_points = has_zp ? od.zp.data() : nullptr;
+}
+
+// interleave: two parts of equal N whose outputs alternate (gate|up rows).
 tbh_status make_weight(tbh_decoder *dec, const tbh_qtensor_desc *const *parts, int n, int64_t K,
-                       int64_t N, tbh_weight **out) {
+                       int64_t N, tbh_weight **out, bool interleave = false) {
     OwnedDesc od;
     tbh_status st = n == 1 ? TBH_OK : concat_n(parts, n, od);
     if (st != TBH_OK) return st;
+    if (interleave) {
+        if (n != 2 || parts[0]->N != parts[1]->N)
+            return set_error(TBH_E_INVALID, "decoder: gate and up projections differ in shape");
+        interleave_halves(od);
+    }
     const tbh_qtensor_desc *d = n == 1 ? parts[0] : &od.d;
     if (!d) return set_error(TBH_E_INVALID, "decoder: NULL weight");
     if (d->K != K || d->N != N) return set_error(TBH_E_INVALID, "decoder: projection shape mismatch");
@@ -579,7 +634,7 @@ tbh_status tbh_decoder_set_layer(tbh_decoder *d, int32_t layer, const float *inp
     const tbh_qtensor_desc *dd[1] = {down};
     tbh_status st = make_weight(d, qkv, 3, c.hidden, d->qkv_dim, &nw[0]);
     if (st == TBH_OK) st = make_weight(d, od, 1, c.hidden, c.hidden, &nw[1]);
-    if (st == TBH_OK) st = make_weight(d, gu, 2, c.hidden, 2 * (int64_t)c.intermediate, &nw[2]);
+    if (st == TBH_OK) st = make_weight(d, gu, 2, c.hidden, 2 * (int64_t)c.intermediate, &nw[2], true);
     if (st == TBH_OK) st = make_weight(d, dd, 1, c.intermediate, c.hidden, &nw[3]);
     const size_t H = (size_t)c.hidden;
     if (st == TBH_OK &&
@@ -667,10 +722,10 @@ tbh_status tbh_decoder_step_device(tbh_decoder *d, int32_t token, float *logits,
         launch_attention(ap, s);
         e = launch_gemv_fused(*L.o, FusedGemvArgs{d->ctx, nullptr, nullptr, 0.0f, d->h, 0, 1}, s);
         if (e != hipSuccess) break;
-        e = launch_gemv_fused(*L.gu, FusedGemvArgs{d->h, nullptr, g_post, c.rms_eps, d->gu, 1, 0}, s);
+        // gate and up rows interleaved: the epilogue writes silu(gate) * up
+        e = launch_gemv_fused(*L.gu, FusedGemvArgs{d->h, nullptr, g_post, c.rms_eps, d->gu, 1, 2}, s);
         if (e != hipSuccess) break;
-        e = launch_gemv_fused(*L.down, FusedGemvArgs{d->gu, d->gu + c.intermediate, nullptr, 0.0f, d->h, 2, 1},
-                              s);
+        e = launch_gemv_fused(*L.down, FusedGemvArgs{d->gu, nullptr, nullptr, 0.0f, d->h, 0, 1}, s);
     }
     if (e == hipSuccess)
         e = launch_gemv_fused(*d->lm_head,

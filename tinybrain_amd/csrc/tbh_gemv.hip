@@ -64,7 +64,9 @@ struct KParams {
 };
 
 enum { PRO_NONE = 0, PRO_RMSNORM = 1, PRO_SILU_MUL = 2 };
-enum { EPI_STORE = 0, EPI_ACCUMULATE = 1 };
+// EPI_SILU_PAIR: rows 2j and 2j + 1 are a gate and an up row; the output is
+// y[j] = silu(r[2j]) * r[2j + 1] (ModelRunner.swift:449-451).
+enum { EPI_STORE = 0, EPI_ACCUMULATE = 1, EPI_SILU_PAIR = 2 };
 
 // expf at full precision (not the hardware exp2 approximation).
 __device__ __forceinline__ float __expf_exact(float v) { return expf(v); }
@@ -613,7 +615,16 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
 #pragma unroll
     for (int j = 0; j < V; ++j) v[j] = acc[j / U][j % U];
     const float tot = reduce_multi<V>(v, lane);
-    if ((lane & (64 / V - 1)) == 0) {
+    if constexpr (EPI == EPI_SILU_PAIR) {
+        // value ridx ^ 1 (the pair's other row) sits at lane ^ (64 / V)
+        static_assert(M == 1 && U >= 2, "pairs of rows within one wave");
+        const float r = PREC == 8 ? tot * rs : tot;
+        const float other = __shfl_xor(r, 64 / V);
+        if ((lane & (64 / V - 1)) == 0 && (ridx & 1) == 0) {
+            const int n = r0 + ridx;
+            if (n < p.N) p.y[n / 2] = (r / (1.0f + expf(-r))) * other;
+        }
+    } else if ((lane & (64 / V - 1)) == 0) {
         const int m = ridx / U, n = r0 + ridx % U;
         const float v = PREC == 8 ? tot * rs : tot;
         if (n < p.N) p.y[(int64_t)m * p.ldy + n] = EPI == EPI_ACCUMULATE ? yin + v : v;
@@ -666,7 +677,7 @@ constexpr int kBurstMaxI = 6;
 
 template <int PREC, int M, int U, int I, int PRO, int EPI>
 hipError_t launch_burst_one(const KParams &p, size_t lds, hipStream_t s) {
-    if constexpr (U * I > 16) {
+    if constexpr (U * I > 16 || (EPI == EPI_SILU_PAIR && (U < 2 || M != 1))) {
         return hipErrorInvalidValue;
     } else {
         const int64_t waves = (p.Np + U - 1) / U;
@@ -718,6 +729,8 @@ hipError_t burst_fused(int pro, int epi, int I, int U, const KParams &p, size_t 
     if (pro == PRO_NONE && epi == EPI_ACCUMULATE) return burst_i<PREC, 1, PRO_NONE, EPI_ACCUMULATE>(I, U, p, lds, s);
     if (pro == PRO_SILU_MUL && epi == EPI_ACCUMULATE)
         return burst_i<PREC, 1, PRO_SILU_MUL, EPI_ACCUMULATE>(I, U, p, lds, s);
+    if (pro == PRO_RMSNORM && epi == EPI_SILU_PAIR)
+        return burst_i<PREC, 1, PRO_RMSNORM, EPI_SILU_PAIR>(I, U, p, lds, s);
     return hipErrorInvalidValue;
 }
 
@@ -806,6 +819,10 @@ hipError_t launch_gemv_fused(const tbh_weight &w, const FusedGemvArgs &f, hipStr
     int I, U;
     int64_t lds;
     if (!burst_shape(w, p, 1, &I, &U, &lds)) return hipErrorInvalidValue;
+    if (f.epilogue == EPI_SILU_PAIR) {
+        if (w.N % 2 != 0 || 2 * I > 16) return hipErrorInvalidValue;
+        U = std::max(U, 2);   // both rows of a pair in one wave
+    }
     return w.precision == TBH_PREC_INT8 ? burst_fused<8>(f.prologue, f.epilogue, I, U, p, (size_t)lds, s)
                                         : burst_fused<4>(f.prologue, f.epilogue, I, U, p, (size_t)lds, s);
 }

@@ -119,7 +119,8 @@ int64_t gemv_max_rows(const tbh_weight &w);
 //   prologue 0: x as given; 1: rmsnorm(x) * g with epsilon eps
 //   (Tensor.swift:1543-1556); 2: silu(x) * x2 (Tensor.swift:1135-1141,
 //   ModelRunner.swift:449-451).  epilogue 0: store; 1: y += result
-//   (the residual adds, ModelRunner.swift:434, :457).
+//   (the residual adds, ModelRunner.swift:434, :457); 2: rows 2j, 2j + 1
+//   are a gate and an up row, y[j] = silu(r[2j]) * r[2j + 1] (:449-451).
 struct FusedGemvArgs {
     const float *x;
     const float *x2;
