@@ -309,25 +309,27 @@ hipError_t launch_tile(const PParams &p, int splits, hipStream_t s) {
     return hipGetLastError();
 }
 
-// Blocks a split-K launch aims for, per CU (TBH_PREFILL_BLOCKS_PER_CU
-// overrides the default of 2; 0 disables split-K).
-int blocks_per_cu() {
+// Blocks a split-K launch aims for, per CU: `dflt` unless
+// TBH_PREFILL_BLOCKS_PER_CU is set (0 disables split-K).
+int blocks_per_cu(int dflt) {
     static const int v = [] {
         const char *e = std::getenv("TBH_PREFILL_BLOCKS_PER_CU");
-        return e ? std::max(0, std::atoi(e)) : 2;
+        return e ? std::max(0, std::atoi(e)) : -1;
     }();
-    return v;
+    return v >= 0 ? v : dflt;
 }
 
 constexpr int kMinSplitSteps = 4;  // K steps of 64 a split keeps at least
 
+// K is split over blocks when there are fewer than bpc blocks per CU.
 template <int PREC, int BM, int BN>
-hipError_t launch_split(const tbh_weight &w, PParams p, int64_t tiles, hipStream_t s) {
+hipError_t launch_split(const tbh_weight &w, PParams p, int64_t tiles, int bpc, hipStream_t s) {
     const int nsteps = (int)((p.chunks * (PREC == 8 ? kInt8ChunkElems : kInt4ChunkElems) + kBK - 1) / kBK);
     const int64_t cus = std::max(1, w.dev->cu_count);
     int splits = 1, sps = nsteps;
-    if (tiles < cus && p.ldy == p.N && blocks_per_cu() > 0) {
-        const int64_t want = (blocks_per_cu() * cus + tiles - 1) / tiles;
+    bpc = blocks_per_cu(bpc);
+    if (tiles < bpc * cus && p.ldy == p.N) {
+        const int64_t want = (bpc * cus + tiles - 1) / tiles;
         sps = (int)std::max<int64_t>(kMinSplitSteps, (nsteps + want - 1) / want);
         sps = (sps + kDepth - 1) / kDepth * kDepth;
         splits = (nsteps + sps - 1) / sps;
@@ -364,14 +366,15 @@ hipError_t launch_split(const tbh_weight &w, PParams p, int64_t tiles, hipStream
 template <int PREC>
 hipError_t launch_prec(const tbh_weight &w, const PParams &p, hipStream_t s) {
     // Largest tile that still gives every CU a block; below that, 64 x 64
-    // tiles split along K.
+    // tiles split along K until there are two blocks per CU (a 64 x 64 block
+    // does little work per K step, so one per CU leaves its latency exposed).
     const int64_t cus = std::max(1, w.dev->cu_count);
     const int64_t t128 = ((p.Np + 127) / 128) * ((p.M + 127) / 128);
     const int64_t t64x128 = ((p.Np + 127) / 128) * ((p.M + 63) / 64);
     const int64_t t64 = ((p.Np + 63) / 64) * ((p.M + 63) / 64);
-    if (t128 >= cus) return launch_split<PREC, 128, 128>(w, p, t128, s);
-    if (t64x128 >= cus) return launch_split<PREC, 64, 128>(w, p, t64x128, s);
-    return launch_split<PREC, 64, 64>(w, p, t64, s);
+    if (t128 >= cus) return launch_split<PREC, 128, 128>(w, p, t128, 1, s);
+    if (t64x128 >= cus) return launch_split<PREC, 64, 128>(w, p, t64x128, 1, s);
+    return launch_split<PREC, 64, 64>(w, p, t64, 2, s);
 }
 
 }  // namespace
