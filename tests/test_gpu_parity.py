@@ -143,7 +143,8 @@ def test_int4_baseline_config1(backend, K, N):
     _check(backend, _product(qt, (K, N), T.Layout.NK_FLAT), qt, Ms=(1, 4, 8))
 
 
-# Burst GEMV (M <= 2, no zero points, 16-byte aligned x, K % 4 == 0): one case
+# Burst GEMV (M in {1, 2, 4}; M = 8 runs as two M = 4 launches; no zero
+# points, 16-byte aligned x, K % 4 == 0): one case
 # per chunk-iteration count I = ceil(chunks / 64) = 1..6 and per rows-per-wave
 # U = 1..16, which the launch picks from N and the CU count (256 on MI355X).
 @pytest.mark.parametrize("prec,K,N", [
@@ -166,7 +167,7 @@ def test_burst_shapes(backend, prec, K, N):
     else:
         oq = _int4_nk(43 + K, K, N, 32)
         pq = _product(oq, (K, N), T.Layout.NK_FLAT)
-    _check(backend, pq, oq, Ms=(1, 2), cpu_path=False)
+    _check(backend, pq, oq, Ms=(1, 2, 4, 8), cpu_path=False)
 
 
 @pytest.mark.parametrize("K,N,gs,path", [(256, 512, 32, "int4_ngroup"), (2048, 2048, 32, "int4_ngroup"),

@@ -677,7 +677,7 @@ constexpr int kBurstMaxI = 6;
 
 template <int PREC, int M, int U, int I, int PRO, int EPI>
 hipError_t launch_burst_one(const KParams &p, size_t lds, hipStream_t s) {
-    if constexpr (U * I > 16 || (EPI == EPI_SILU_PAIR && (U < 2 || M != 1))) {
+    if constexpr (U * I > 16 || M * U > 32 || (EPI == EPI_SILU_PAIR && (U < 2 || M != 1))) {
         return hipErrorInvalidValue;
     } else {
         const int64_t waves = (p.Np + U - 1) / U;
@@ -717,6 +717,7 @@ hipError_t burst_m(int M, int I, int U, const KParams &p, size_t lds, hipStream_
     switch (M) {
     case 1: return burst_i<PREC, 1, PRO_NONE, EPI_STORE>(I, U, p, lds, s);
     case 2: return burst_i<PREC, 2, PRO_NONE, EPI_STORE>(I, U, p, lds, s);
+    case 4: return burst_i<PREC, 4, PRO_NONE, EPI_STORE>(I, U, p, lds, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -784,14 +785,15 @@ bool burst_shape(const tbh_weight &w, const KParams &p, int M, int *I_out, int *
     const int I = (p.chunks + 63) / 64;
     const int ce = w.precision == TBH_PREC_INT8 ? kInt8ChunkElems : kInt4ChunkElems;
     const int64_t blds = (int64_t)M * 64 * I * (ce + 4) * (int64_t)sizeof(float);
-    if (kernel_sel || M > 2 || w.zp != nullptr || I > kBurstMaxI || !p.x_vec4 ||
+    if (kernel_sel || !(M == 1 || M == 2 || M == 4) || w.zp != nullptr || I > kBurstMaxI || !p.x_vec4 ||
         blds > kMaxLdsBytes || !(w.path == Path::Int8Row || w.path == Path::Int4KGroup) ||
         w.mfma_tiles)
         return false;
     const int64_t cus = std::max(1, w.dev->cu_count);
+    // U * I <= 16 weight chunks per lane; M * U <= 32 values in the reduce
     int U = 1;
-    while (2 * U * I <= 16 && w.Np / (2 * U) >= burst_wpc * cus) U *= 2;
-    if (u_force > 0 && u_force * I <= 16 && (u_force & (u_force - 1)) == 0) U = u_force;
+    while (2 * U * I <= 16 && 2 * U * M <= 32 && w.Np / (2 * U) >= burst_wpc * cus) U *= 2;
+    if (u_force > 0 && u_force * I <= 16 && u_force * M <= 32 && (u_force & (u_force - 1)) == 0) U = u_force;
     *I_out = I;
     *U_out = U;
     *lds_out = blds;
