@@ -194,6 +194,140 @@ __global__ __launch_bounds__(256) void rmsnorm_rows(const float *__restrict__ x,
     }
 }
 
+// Register-resident rows (16-byte aligned rows, cols % 4 == 0, at most
+// 8 * 64 * W float4 per row): thread t of a row's 64 * W threads holds float4
+// elements t, t + 64 W, ... in registers, so x is read from memory once and y
+// written once.  W = 1: four rows per 256-thread block; W = 4 or 16: one row
+// per block.
+template <int W>
+__device__ __forceinline__ float block_max(float v, float *red) {
+    v = wave_max(v);
+    if (W == 1) return v;
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[wave] = v;
+    __syncthreads();
+    float r = red[0];
+#pragma unroll
+    for (int i = 1; i < W; ++i) r = fmaxf(r, red[i]);
+    __syncthreads();
+    return r;
+}
+
+template <int W>
+__device__ __forceinline__ float block_sum(float v, float *red) {
+    v = wave_sum(v);
+    if (W == 1) return v;
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[wave] = v;
+    __syncthreads();
+    float r = 0.0f;
+#pragma unroll
+    for (int i = 0; i < W; ++i) r += red[i];
+    __syncthreads();
+    return r;
+}
+
+template <int W, int R>
+__global__ __launch_bounds__(W == 1 ? 256 : 64 * W) void softmax_reg(const float *__restrict__ x,
+                                                                    float *__restrict__ y, int64_t rows,
+                                                                    int64_t cols) {
+    __shared__ float red[W];
+    constexpr int T = 64 * W;
+    const int64_t row = W == 1 ? (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6) : (int64_t)blockIdx.x;
+    const int t = threadIdx.x % T;
+    const int64_t r = row < rows ? row : rows - 1;   // every thread reaches the barriers
+    const float4 *xr = (const float4 *)(x + r * cols);
+    const int n4 = (int)(cols / 4);
+    float4 v[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        const int j = t + T * i;
+        v[i] = j < n4 ? xr[min(j, n4 - 1)] : float4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < R; ++i) m = fmaxf(m, fmaxf(fmaxf(v[i].x, v[i].y), fmaxf(v[i].z, v[i].w)));
+    m = block_max<W>(m, red);
+    // Tensor.softmaxCPU: exp(x - max) / (sum + epsilon); an all -inf row
+    // gives NaN there (x - max = NaN) and here
+    float sm = 0.0f;
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        v[i] = float4{expf(v[i].x - m), expf(v[i].y - m), expf(v[i].z - m), expf(v[i].w - m)};
+        const int j = t + T * i;
+        if (j < n4) sm += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+    }
+    sm = block_sum<W>(sm, red);
+    if (row >= rows) return;
+    const float den = sm + kSoftmaxEps;
+    float4 *yr = (float4 *)(y + r * cols);
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        const int j = t + T * i;
+        if (j < n4) yr[j] = float4{v[i].x / den, v[i].y / den, v[i].z / den, v[i].w / den};
+    }
+}
+
+template <int W, int R>
+__global__ __launch_bounds__(W == 1 ? 256 : 64 * W) void rmsnorm_reg(const float *__restrict__ x,
+                                                                    const float *__restrict__ g, float eps,
+                                                                    float *__restrict__ y, int64_t rows,
+                                                                    int64_t hidden) {
+    __shared__ float red[W];
+    constexpr int T = 64 * W;
+    const int64_t row = W == 1 ? (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6) : (int64_t)blockIdx.x;
+    const int t = threadIdx.x % T;
+    const int64_t r = row < rows ? row : rows - 1;
+    const float4 *xr = (const float4 *)(x + r * hidden);
+    const float4 *g4 = (const float4 *)g;
+    const int n4 = (int)(hidden / 4);
+    float4 v[R], w[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        const int j = min(t + T * i, n4 - 1);
+        v[i] = xr[j];
+        w[i] = g4[j];
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+        if (t + T * i < n4) ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
+    ss = block_sum<W>(ss, red);
+    if (row >= rows) return;
+    // Tensor.rmsNormCPU: invRMS = 1 / sqrt(ss / hidden + eps); x * invRMS * w
+    const float inv = 1.0f / sqrtf(ss / (float)hidden + eps);
+    float4 *yr = (float4 *)(y + r * hidden);
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        const int j = t + T * i;
+        if (j < n4)
+            yr[j] = float4{v[i].x * inv * w[i].x, v[i].y * inv * w[i].y, v[i].z * inv * w[i].z, v[i].w * inv * w[i].w};
+    }
+}
+
+// Launches the register-resident form when the row fits (returns false
+// otherwise): W from {1, 4, 16} threads-per-row waves, R float4 per thread.
+template <class K1, class K4, class K16>
+bool launch_reg_rows(int64_t rows, int64_t cols, hipStream_t s, K1 k1, K4 k4, K16 k16) {
+    const int64_t n4 = cols / 4;
+    auto rpt = [](int64_t n, int t) { const int64_t r = (n + t - 1) / t; return r <= 1 ? 1 : r <= 2 ? 2 : r <= 4 ? 4 : 8; };
+    if (n4 <= 64 * 4) k1(rpt(n4, 64), dim3((unsigned)((rows + 3) / 4)), dim3(256), s);
+    else if (n4 <= 256 * 8) k4(rpt(n4, 256), dim3((unsigned)rows), dim3(256), s);
+    else if (n4 <= 1024 * 8) k16(rpt(n4, 1024), dim3((unsigned)rows), dim3(1024), s);
+    else return false;
+    return true;
+}
+
+#define TBH_REG_LAUNCHER(NAME, KERNEL, W, ...)                                                     \
+    auto NAME = [&](int R, dim3 grid, dim3 block, hipStream_t st) {                                \
+        switch (R) {                                                                               \
+        case 1: hipLaunchKernelGGL((KERNEL<W, 1>), grid, block, 0, st, __VA_ARGS__); break;        \
+        case 2: hipLaunchKernelGGL((KERNEL<W, 2>), grid, block, 0, st, __VA_ARGS__); break;        \
+        case 4: hipLaunchKernelGGL((KERNEL<W, 4>), grid, block, 0, st, __VA_ARGS__); break;        \
+        default: hipLaunchKernelGGL((KERNEL<W, 8>), grid, block, 0, st, __VA_ARGS__); break;       \
+        }                                                                                          \
+    }
+
 enum Act { ACT_SILU = 0, ACT_GELU = 1 };
 
 template <int A>
@@ -704,6 +838,12 @@ unsigned grid_for(int64_t blocks, const tbh_device *dev) {
 
 hipError_t launch_softmax(const float *x, int64_t rows, int64_t cols, float *y, hipStream_t s) {
     const bool vec = cols % 4 == 0 && aligned16(x) && aligned16(y);
+    if (vec) {
+        TBH_REG_LAUNCHER(k1, softmax_reg, 1, x, y, rows, cols);
+        TBH_REG_LAUNCHER(k4, softmax_reg, 4, x, y, rows, cols);
+        TBH_REG_LAUNCHER(k16, softmax_reg, 16, x, y, rows, cols);
+        if (launch_reg_rows(rows, cols, s, k1, k4, k16)) return hipGetLastError();
+    }
     if (cols <= kWaveRowMax) {
         const dim3 grid((unsigned)((rows + 3) / 4));
         if (vec) hipLaunchKernelGGL((softmax_rows<1, true>), grid, dim3(256), 0, s, x, y, rows, cols);
@@ -719,6 +859,12 @@ hipError_t launch_softmax(const float *x, int64_t rows, int64_t cols, float *y, 
 hipError_t launch_rmsnorm(const float *x, int64_t rows, int64_t hidden, const float *g, float eps, float *y,
                           hipStream_t s) {
     const bool vec = hidden % 4 == 0 && aligned16(x) && aligned16(y) && aligned16(g);
+    if (vec) {
+        TBH_REG_LAUNCHER(k1, rmsnorm_reg, 1, x, g, eps, y, rows, hidden);
+        TBH_REG_LAUNCHER(k4, rmsnorm_reg, 4, x, g, eps, y, rows, hidden);
+        TBH_REG_LAUNCHER(k16, rmsnorm_reg, 16, x, g, eps, y, rows, hidden);
+        if (launch_reg_rows(rows, hidden, s, k1, k4, k16)) return hipGetLastError();
+    }
     if (hidden <= kWaveRowMax) {
         const dim3 grid((unsigned)((rows + 3) / 4));
         if (vec) hipLaunchKernelGGL((rmsnorm_rows<1, true>), grid, dim3(256), 0, s, x, g, eps, y, rows, hidden);
