@@ -11,16 +11,15 @@
 // pair, once for the output) instead of the reference kernel's three reads
 // and two writes.
 //
-// Attention (head_dim % 4 == 0): a block serves the query heads (up to 8)
-// that share one key/value head, so each key and value row is read once per
-// group rather than once per query head.  When there are too few (query,
-// key/value head) groups to fill the chip, the key positions are split over
-// several blocks, each writing a partial (max, sum, output) per head to a
-// workspace, and a second kernel merges them (split-KV decoding).  Inside a
-// block, a pass scores 256 positions (one per thread, 16-byte key loads,
-// queries broadcast from LDS), keeps an online softmax per head across
-// passes, and accumulates p * v with 16-byte value loads.  Other head
-// dimensions take a one-wave-per-row kernel.
+// Attention: when there are too few (query, key/value head) pairs to fill
+// the chip, the key positions are split over several blocks, each writing a
+// partial (max, sum, output) per head to a workspace, and a second kernel
+// merges them (split-KV decoding).  Head dimensions 16/32/64/128 take one
+// wave per (query, query head, range): the four waves of a block are query
+// heads of one key/value head and share its rows through L1.  Other head
+// dimensions that are multiples of 4 take a block per (query, key/value
+// head) serving up to 8 query heads (256 positions per pass, one per
+// thread); the rest a one-wave-per-row kernel.
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -603,167 +602,137 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// attention_group for head_dim = 4 * HD4 in {16, 32, 64}: every global load
-// of a pass (the group's queries, the pass's key rows and value rows) is
-// issued before any of them is used, from clamped addresses (positions past
-// the split read its last position and get p = 0), so a pass costs one
-// memory round trip.  Value rows are spread over all four waves: thread
-// (pg, d4) reads 16 bytes of rows pg, pg + 256 / HD4, ...
-template <int HD4>
-__global__ __launch_bounds__(256) void attention_small(const GrpArgs g) {
-    constexpr int HD = 4 * HD4, PPB = 256 / HD4, NQ = (kGrpHeads * HD + 255) / 256;
+// Orders a wave's LDS writes before later LDS reads by other lanes of the
+// same wave (the waves of attention_wave never wait for each other).
+__device__ __forceinline__ void wave_lds_fence() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+}
+
+// Attention for head_dim HD in {16, 32, 64, 128}: one wave per (query row,
+// query head, range of key positions); a block's four waves are four query
+// heads of one key/value head, so they share the range's key and value rows
+// through L1, and no wave waits for another.  A pass covers 64 positions,
+// one per lane for the scores (16-byte key loads), with max and sum by DPP;
+// p * v takes 16-byte value pieces (lane (pg, d4) covers rows pg,
+// pg + 64 / (HD / 4), ...).  The wave keeps an online softmax across
+// passes; with one split it writes the output, else its range's (max, sum,
+// p.v) partial for attention_combine.
+template <int HD>
+__global__ __launch_bounds__(256) void attention_wave(const GrpArgs g) {
+    constexpr int HD4 = HD / 4, PPI = 64 / HD4, NV = HD4;
     const AttnArgs &a = g.a;
-    __shared__ __attribute__((aligned(16))) float qs[kGrpHeads][HD];
-    __shared__ float ps[kGrpHeads][kPass];
-    __shared__ float redm[4][kGrpHeads], reds[4][kGrpHeads];
-    __shared__ float red_o[256 * kRedPad];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int64_t unit = blockIdx.x / g.splits;
-    const int split = (int)(blockIdx.x % g.splits);
-    const int hc = (int)(unit % g.hchunks);
-    const int64_t grp = unit / g.hchunks;
-    const int kvh = (int)(grp % a.nkv);
-    const int64_t bq = grp / a.nkv;
-    const int64_t b = bq / a.seq_len;
-    const int nhb = min(kGrpHeads, g.rep - hc * kGrpHeads);
-    const int head0 = kvh * g.rep + hc * kGrpHeads;
+    __shared__ __attribute__((aligned(16))) float qs[4][HD];
+    __shared__ float ps[4][64];
+    __shared__ float4 red[4][64];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nquad = (g.rep + 3) / 4;
+    int64_t bi = blockIdx.x;
+    const int split = (int)(bi % g.splits);
+    bi /= g.splits;
+    const int quad = (int)(bi % nquad);
+    bi /= nquad;
+    const int kvh = (int)(bi % a.nkv);
+    const int64_t bq = bi / a.nkv;                // batch * seq_len + query
+    const int hg = quad * 4 + w;
+    if (hg >= g.rep) return;
+    const int head = kvh * g.rep + hg;
+    const int64_t batch = bq / a.seq_len;
     const int64_t kvd = (int64_t)a.nkv * HD;
-    const float *kb = a.k + b * a.kv_len * kvd + (int64_t)kvh * HD;
-    const float *vb = a.v + b * a.kv_len * kvd + (int64_t)kvh * HD;
-    const float *qb = a.q + bq * a.nh * HD + (int64_t)head0 * HD;
+    const float *qrow = a.q + (bq * a.nh + head) * HD;
+    const float *kb = a.k + batch * a.kv_len * kvd + (int64_t)kvh * HD;
+    const float *vb = a.v + batch * a.kv_len * kvd + (int64_t)kvh * HD;
+    for (int d = lane; d < HD; d += 64) qs[w][d] = qrow[d];
     const int64_t c0 = split * g.chunk, c1 = min(a.kv_len, c0 + g.chunk);
-    const int pg = tid / HD4, d4 = tid % HD4;
+    const int pg = lane / HD4, d4 = lane % HD4;
+    wave_lds_fence();
 
-    float qv[NQ];
+    float m = -INFINITY, l = 0.0f;
+    float4 acc = float4{0.f, 0.f, 0.f, 0.f};
+    for (int64_t p0 = c0; p0 < c1; p0 += 64) {
+        const int64_t t = p0 + lane, last = c1 - 1;
+        const bool tv = t < c1;
+        float4 kreg[HD4], vreg[NV];
+        const float *kr = kb + min(t, last) * kvd;
 #pragma unroll
-    for (int i = 0; i < NQ; ++i) {
-        const int o = tid + 256 * i;
-        const int h = min(o / HD, nhb - 1);    // heads past the group read a valid row
-        qv[i] = qb[h * HD + o % HD];
-    }
-    float m[kGrpHeads], l[kGrpHeads];
-    float4 acc[kGrpHeads];
+        for (int i = 0; i < HD4; ++i) kreg[i] = *(const float4 *)(kr + 4 * i);
 #pragma unroll
-    for (int h = 0; h < kGrpHeads; ++h) {
-        m[h] = -INFINITY;
-        l[h] = 0.0f;
-        acc[h] = float4{0.f, 0.f, 0.f, 0.f};
-    }
-    for (int64_t p0 = c0; p0 < c1; p0 += kPass) {
-        const int64_t t = p0 + tid;
-        const bool valid = t < c1;
-        const float4 *kr = (const float4 *)(kb + min(t, c1 - 1) * kvd);
-        float4 kreg[HD4], vreg[HD4];
+        for (int j = 0; j < NV; ++j)
+            vreg[j] = *(const float4 *)(vb + min(p0 + pg + j * PPI, last) * kvd + 4 * d4);
+        const float mk = a.mask ? a.mask[min(t, last)] : 0.0f;
+        float d = 0.0f;
 #pragma unroll
-        for (int i = 0; i < HD4; ++i) kreg[i] = kr[i];
-#pragma unroll
-        for (int j = 0; j < HD4; ++j)
-            vreg[j] = *(const float4 *)(vb + min(p0 + pg + j * PPB, c1 - 1) * kvd + 4 * d4);
-        const float mk = a.mask ? a.mask[min(t, c1 - 1)] : 0.0f;
-        if (p0 == c0) {
-#pragma unroll
-            for (int i = 0; i < NQ; ++i) {
-                const int o = tid + 256 * i;
-                if (o < kGrpHeads * HD) qs[o / HD][o % HD] = qv[i];
-            }
-            lds_barrier();
+        for (int i = 0; i < HD4; ++i) {
+            const float4 q4 = *(const float4 *)&qs[w][4 * i];
+            d += q4.x * kreg[i].x + q4.y * kreg[i].y + q4.z * kreg[i].z + q4.w * kreg[i].w;
         }
-        float sc[kGrpHeads];
+        const float sc = tv ? d * a.scale + mk : -INFINITY;
+        const float nm = fmaxf(m, wave_max(sc));
+        if (nm == -INFINITY) continue;            // every position so far masked (uniform)
+        const float corr = expf(m - nm);
+        const float p = expf(sc - nm);
+        l = l * corr + wave_sum(p);
+        ps[w][lane] = p;
+        wave_lds_fence();
+        acc.x *= corr;
+        acc.y *= corr;
+        acc.z *= corr;
+        acc.w *= corr;
 #pragma unroll
-        for (int h = 0; h < kGrpHeads; ++h) {
-            float d = 0.0f;
-#pragma unroll
-            for (int i = 0; i < HD4; ++i) {
-                const float4 q4 = *(const float4 *)&qs[h][4 * i];
-                d += q4.x * kreg[i].x + q4.y * kreg[i].y + q4.z * kreg[i].z + q4.w * kreg[i].w;
-            }
-            sc[h] = valid ? d * a.scale + mk : -INFINITY;
-            const float wm = wave_max(sc[h]);
-            if (lane == 0) redm[wave][h] = wm;
+        for (int j = 0; j < NV; ++j) {
+            const float pr = ps[w][pg + j * PPI];   // 0 past the range
+            acc.x += pr * vreg[j].x;
+            acc.y += pr * vreg[j].y;
+            acc.z += pr * vreg[j].z;
+            acc.w += pr * vreg[j].w;
         }
-        lds_barrier();
-        float corr[kGrpHeads];
+        m = nm;
+        wave_lds_fence();                         // ps is rewritten by the next pass
+    }
+    red[w][lane] = acc;
+    wave_lds_fence();
+    if (lane < HD4) {
+        float4 o = red[w][lane];
 #pragma unroll
-        for (int h = 0; h < kGrpHeads; ++h) {
-            const float pm = fmaxf(fmaxf(redm[0][h], redm[1][h]), fmaxf(redm[2][h], redm[3][h]));
-            const float nm = fmaxf(m[h], pm);
-            corr[h] = nm == -INFINITY ? 1.0f : expf(m[h] - nm);
-            const float pv = nm == -INFINITY ? 0.0f : expf(sc[h] - nm);
-            ps[h][tid] = pv;
-            const float ws = wave_sum(pv);
-            if (lane == 0) reds[wave][h] = ws;
-            m[h] = nm;
+        for (int q = 1; q < PPI; ++q) {
+            const float4 v = red[w][q * HD4 + lane];
+            o.x += v.x;
+            o.y += v.y;
+            o.z += v.z;
+            o.w += v.w;
         }
-        lds_barrier();
-#pragma unroll
-        for (int h = 0; h < kGrpHeads; ++h) {
-            l[h] = l[h] * corr[h] + ((reds[0][h] + reds[1][h]) + (reds[2][h] + reds[3][h]));
-            float4 a4 = acc[h];
-            a4.x *= corr[h];
-            a4.y *= corr[h];
-            a4.z *= corr[h];
-            a4.w *= corr[h];
-#pragma unroll
-            for (int j = 0; j < HD4; ++j) {
-                const float pr = ps[h][pg + j * PPB];   // 0 past the split
-                a4.x += pr * vreg[j].x;
-                a4.y += pr * vreg[j].y;
-                a4.z += pr * vreg[j].z;
-                a4.w += pr * vreg[j].w;
-            }
-            acc[h] = a4;
-        }
-        lds_barrier();   // ps and redm are rewritten by the next pass
-    }
-
-#pragma unroll
-    for (int h = 0; h < kGrpHeads; ++h) {
-        red_o[tid * kRedPad + 4 * h + 0] = acc[h].x;
-        red_o[tid * kRedPad + 4 * h + 1] = acc[h].y;
-        red_o[tid * kRedPad + 4 * h + 2] = acc[h].z;
-        red_o[tid * kRedPad + 4 * h + 3] = acc[h].w;
-    }
-    __syncthreads();
-    float *part = g.splits > 1 ? g.part + (unit * g.splits + split) * (2 * kGrpHeads + kGrpHeads * HD) : nullptr;
-    if (part && tid < kGrpHeads) {
-#pragma unroll
-        for (int h = 0; h < kGrpHeads; ++h)
-            if (h == tid) {
-                part[h] = m[h];
-                part[kGrpHeads + h] = l[h];
-            }
-    }
-    for (int o = tid; o < nhb * HD; o += 256) {
-        const int h = o / HD, d = o % HD;
-        float v = 0.0f;
-#pragma unroll 4
-        for (int q = 0; q < PPB; ++q) v += red_o[(q * HD4 + d / 4) * kRedPad + 4 * h + d % 4];
-        float mh = 0.0f, lh = 0.0f;
-#pragma unroll
-        for (int hh = 0; hh < kGrpHeads; ++hh)
-            if (hh == h) {
-                mh = m[hh];
-                lh = l[hh];
-            }
-        if (part) {
-            part[2 * kGrpHeads + h * HD + d] = v;
+        if (g.splits == 1) {
+            // no positions (kv_len 0) leaves zeros; all masked gives NaN
+            const bool dead = m == -INFINITY && a.kv_len > 0;
+            const float den = l + kAttnEps;
+            float *orow = a.out + (bq * a.nh + head) * HD + 4 * lane;
+            *(float4 *)orow = dead ? float4{NAN, NAN, NAN, NAN} : float4{o.x / den, o.y / den, o.z / den, o.w / den};
         } else {
-            float *orow = a.out + bq * a.nh * HD + (int64_t)(head0 + h) * HD;
-            orow[d] = (mh == -INFINITY && a.kv_len > 0) ? NAN : v / (lh + kAttnEps);
+            const int64_t unit = (bq * a.nkv + kvh) * g.hchunks + hg / kGrpHeads;
+            const int hs = hg % kGrpHeads;
+            float *part = g.part + (unit * g.splits + split) * (2 * kGrpHeads + kGrpHeads * HD);
+            if (lane == 0) {
+                part[hs] = m;
+                part[kGrpHeads + hs] = l;
+            }
+            *(float4 *)&part[2 * kGrpHeads + hs * HD + 4 * lane] = o;
         }
     }
 }
 
-// Merges the split partials of attention_group / attention_small: per head,
+// Merges the split partials of attention_group / attention_wave: per head,
 // M = max m_s, out = sum(o_s e^(m_s - M)) / (sum(l_s e^(m_s - M)) + eps).
-// One block per (group, head): the split weights e^(m_s - M) go through LDS,
-// then thread (sg, d4) sums 16-byte pieces of the splits sg, sg + 256/hd4, ...
+// One block per (unit, head); thread (sg, d4) loads the partials of splits
+// sg, sg + 256 / (hd / 4), ... (kCombineLoads of them) in one memory trip
+// (more splits than that take further trips).
+constexpr int kCombineLoads = 4;
+
 __global__ __launch_bounds__(256) void attention_combine(const GrpArgs g) {
     const AttnArgs &a = g.a;
-    __shared__ float wsp[1024];            // split weights (splits <= 1024)
     __shared__ float4 red[256];
-    __shared__ float lsum[4];
-    const int tid = threadIdx.x, hd = a.hd, hd4 = hd / 4;
+    __shared__ float rs[8];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, hd = a.hd, hd4 = hd / 4;
     const int64_t unit = blockIdx.x / kGrpHeads;
     const int h = (int)(blockIdx.x % kGrpHeads);
     const int hc = (int)(unit % g.hchunks);
@@ -773,40 +742,46 @@ __global__ __launch_bounds__(256) void attention_combine(const GrpArgs g) {
     const int64_t bq = grp / a.nkv;
     const int64_t stride = 2 * kGrpHeads + (int64_t)kGrpHeads * hd;
     const float *pb = g.part + unit * g.splits * stride;
-    float mloc = -INFINITY;
-    for (int sp = tid; sp < g.splits; sp += 256) {
-        const float mv = pb[sp * stride + h];
-        wsp[sp] = mv;
-        mloc = fmaxf(mloc, mv);
-    }
-    mloc = wave_max(mloc);
-    if ((tid & 63) == 0) lsum[tid >> 6] = mloc;
-    __syncthreads();
-    const float M = fmaxf(fmaxf(lsum[0], lsum[1]), fmaxf(lsum[2], lsum[3]));
-    __syncthreads();
-    float lpart = 0.0f;
-    for (int sp = tid; sp < g.splits; sp += 256) {
-        const float w = M == -INFINITY ? 0.0f : expf(wsp[sp] - M);
-        wsp[sp] = w;
-        lpart += w * pb[sp * stride + kGrpHeads + h];
-    }
-    lpart = wave_sum(lpart);
-    if ((tid & 63) == 0) lsum[tid >> 6] = lpart;
-    __syncthreads();
-    const float L = (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
     const int sg = tid / hd4, d4 = tid % hd4, nsg = 256 / hd4;
-    float4 o = float4{0.f, 0.f, 0.f, 0.f};
-    if (sg < nsg) {
-#pragma unroll 8
-        for (int sp = sg; sp < g.splits; sp += nsg) {
-            const float w = wsp[sp];
-            const float4 v = *(const float4 *)(pb + sp * stride + 2 * kGrpHeads + h * hd + 4 * d4);
-            o.x += w * v.x;
-            o.y += w * v.y;
-            o.z += w * v.z;
-            o.w += w * v.w;
-        }
+    const bool slane = sg < nsg;
+    float mv[kCombineLoads], lv[kCombineLoads];
+    float4 ov[kCombineLoads];
+#pragma unroll
+    for (int j = 0; j < kCombineLoads; ++j) {
+        const int sp = min(sg + nsg * j, g.splits - 1);
+        mv[j] = pb[sp * stride + h];
+        lv[j] = pb[sp * stride + kGrpHeads + h];
+        ov[j] = *(const float4 *)(pb + sp * stride + 2 * kGrpHeads + h * hd + 4 * d4);
     }
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kCombineLoads; ++j)
+        if (slane && sg + nsg * j < g.splits) mloc = fmaxf(mloc, mv[j]);
+    for (int sp = sg + nsg * kCombineLoads; slane && sp < g.splits; sp += nsg) mloc = fmaxf(mloc, pb[sp * stride + h]);
+    mloc = wave_max(mloc);
+    if (lane == 0) rs[wv] = mloc;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(rs[0], rs[1]), fmaxf(rs[2], rs[3]));
+    float L = 0.0f;
+    float4 o = float4{0.f, 0.f, 0.f, 0.f};
+    if (M != -INFINITY) {
+        auto add = [&](float m, float l, float4 v) {
+            const float e = expf(m - M);
+            if (d4 == 0) L += e * l;   // one thread per split counts its sum
+            o.x += e * v.x;
+            o.y += e * v.y;
+            o.z += e * v.z;
+            o.w += e * v.w;
+        };
+#pragma unroll
+        for (int j = 0; j < kCombineLoads; ++j)
+            if (slane && sg + nsg * j < g.splits) add(mv[j], lv[j], ov[j]);
+        for (int sp = sg + nsg * kCombineLoads; slane && sp < g.splits; sp += nsg)
+            add(pb[sp * stride + h], pb[sp * stride + kGrpHeads + h],
+                *(const float4 *)(pb + sp * stride + 2 * kGrpHeads + h * hd + 4 * d4));
+    }
+    L = wave_sum(L);
+    if (lane == 0) rs[4 + wv] = L;
     red[tid] = o;
     __syncthreads();
     if (tid < hd4) {
@@ -818,14 +793,10 @@ __global__ __launch_bounds__(256) void attention_combine(const GrpArgs g) {
             r.z += v.z;
             r.w += v.w;
         }
+        const float den = ((rs[4] + rs[5]) + (rs[6] + rs[7])) + kAttnEps;
         const int head = kvh * g.rep + hc * kGrpHeads + h;
-        float *orow = a.out + bq * a.nh * hd + (int64_t)head * hd + 4 * tid;
-        const float den = L + kAttnEps;
-        const bool dead = M == -INFINITY;
-        orow[0] = dead ? NAN : r.x / den;
-        orow[1] = dead ? NAN : r.y / den;
-        orow[2] = dead ? NAN : r.z / den;
-        orow[3] = dead ? NAN : r.w / den;
+        float4 *orow = (float4 *)(a.out + (bq * a.nh + head) * hd) + tid;
+        *orow = M == -INFINITY ? float4{NAN, NAN, NAN, NAN} : float4{r.x / den, r.y / den, r.z / den, r.w / den};
     }
 }
 
@@ -892,7 +863,7 @@ hipError_t launch_act(const tbh_device *dev, const float *x, int64_t n, float *y
 hipError_t launch_attention_rows(const AttnArgs &a, hipStream_t s);
 
 hipError_t launch_attention(tbh_device *dev, const AttnArgs &a, hipStream_t s) {
-    if (a.hd % 4 != 0 || !aligned16(a.k) || !aligned16(a.v)) return launch_attention_rows(a, s);
+    if (a.hd % 4 != 0 || !aligned16(a.k) || !aligned16(a.v) || !aligned16(a.out)) return launch_attention_rows(a, s);
     GrpArgs g{};
     g.a = a;
     g.rep = a.nh / a.nkv;
@@ -900,9 +871,14 @@ hipError_t launch_attention(tbh_device *dev, const AttnArgs &a, hipStream_t s) {
     g.units = (a.rows / a.nh) * a.nkv * g.hchunks;
     g.splits = 1;
     g.chunk = std::max<int64_t>(a.kv_len, 1);
+    const bool wave = a.hd == 16 || a.hd == 32 || a.hd == 64 || a.hd == 128;
+    // blocks per split: (query row, KV head, 4 query heads) for attention_wave,
+    // (query row, KV head, 8 query heads) for attention_group
+    const int64_t per_split = wave ? (a.rows / a.nh) * a.nkv * ((g.rep + 3) / 4) : g.units;
     const int64_t target = 2 * (int64_t)std::max(1, dev->cu_count);
-    if (g.units < target && a.kv_len > 64) {
-        const int64_t want = std::min<int64_t>(std::min((target + g.units - 1) / g.units, (a.kv_len + 63) / 64), 1024);
+    if (per_split < target && a.kv_len > 64) {
+        const int64_t want =
+            std::min<int64_t>(std::min((target + per_split - 1) / per_split, (a.kv_len + 63) / 64), 1024);
         g.chunk = ((a.kv_len + want - 1) / want + 63) / 64 * 64;
         g.splits = (int32_t)((a.kv_len + g.chunk - 1) / g.chunk);
     }
@@ -914,12 +890,13 @@ hipError_t launch_attention(tbh_device *dev, const AttnArgs &a, hipStream_t s) {
             g.chunk = std::max<int64_t>(a.kv_len, 1);
         }
     }
-    if (g.units * g.splits > INT32_MAX) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)(g.units * g.splits));
+    if (per_split * g.splits > INT32_MAX) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)(per_split * g.splits));
     switch (a.hd) {
-    case 16: hipLaunchKernelGGL(attention_small<4>, grid, dim3(256), 0, s, g); break;
-    case 32: hipLaunchKernelGGL(attention_small<8>, grid, dim3(256), 0, s, g); break;
-    case 64: hipLaunchKernelGGL(attention_small<16>, grid, dim3(256), 0, s, g); break;
+    case 16: hipLaunchKernelGGL(attention_wave<16>, grid, dim3(256), 0, s, g); break;
+    case 32: hipLaunchKernelGGL(attention_wave<32>, grid, dim3(256), 0, s, g); break;
+    case 64: hipLaunchKernelGGL(attention_wave<64>, grid, dim3(256), 0, s, g); break;
+    case 128: hipLaunchKernelGGL(attention_wave<128>, grid, dim3(256), 0, s, g); break;
     default: hipLaunchKernelGGL(attention_group, grid, dim3(256), 0, s, g); break;
     }
     hipError_t e = hipGetLastError();
