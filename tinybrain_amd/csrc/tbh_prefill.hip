@@ -85,9 +85,10 @@ __global__ __launch_bounds__(256) void gemm_bf16(const PParams p) {
     constexpr int TM = WM / 16, TN = WN / 16;
     static_assert(XSEG % 256 == 0, "BM must be a multiple of 32");
 
-    __shared__ __attribute__((aligned(16))) uint16_t xs[BM * kLdsRow];
-    __shared__ __attribute__((aligned(16))) uint16_t ws[BN * kLdsRow];
-    __shared__ float ssc[PREC == 4 ? BN * CPR : 1];   // INT4: scale of each (row, K-slice)
+    // two LDS buffers: step t + 1 is staged while step t's MFMAs read
+    __shared__ __attribute__((aligned(16))) uint16_t xs[2][BM * kLdsRow];
+    __shared__ __attribute__((aligned(16))) uint16_t ws[2][BN * kLdsRow];
+    __shared__ float ssc[2][PREC == 4 ? BN * CPR : 1];   // INT4: scale of each (row, K-slice)
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int wm = wave >> 1, wn = wave & 1;
@@ -147,19 +148,19 @@ __global__ __launch_bounds__(256) void gemm_bf16(const PParams p) {
     };
 
     // ---- registers -> LDS (x as is; weights dequantized to bf16 pieces)
-    auto store_step = [&](int d) {
+    auto store_step = [&](int d, int bb) {
 #pragma unroll
         for (int j = 0; j < XPT; ++j) {
             const int s = tid + 256 * j;
             const int row = s / (kBK / 8), kq = s % (kBK / 8);
-            *(u32x4 *)&xs[row * kLdsRow + 8 * kq] = xin[d][j] ? xr[d][j] : u32x4{0, 0, 0, 0};
+            *(u32x4 *)&xs[bb][row * kLdsRow + 8 * kq] = xin[d][j] ? xr[d][j] : u32x4{0, 0, 0, 0};
         }
 #pragma unroll
         for (int j = 0; j < WPT; ++j) {
             const int s = tid + 256 * j;
             if (s < WCH) {
                 const int row = s / CPR, cl = s % CPR;
-                uint16_t *dst = &ws[row * kLdsRow + cl * CE];
+                uint16_t *dst = &ws[bb][row * kLdsRow + cl * CE];
                 if (PREC == 8) {
                     // bytes {0,2,1,3} of each word are k+{0,1,2,3}; value u - 128 - zp
                     const float off = 128.0f + (ZP ? (float)zq[d][j] : 0.0f);
@@ -190,7 +191,7 @@ __global__ __launch_bounds__(256) void gemm_bf16(const PParams p) {
                         }
                         *(u32x4 *)(dst + 8 * q) = u32x4{o[0], o[1], o[2], o[3]};
                     }
-                    ssc[s] = sr[d][j];
+                    ssc[bb][s] = sr[d][j];
                 }
             }
         }
@@ -202,48 +203,60 @@ __global__ __launch_bounds__(256) void gemm_bf16(const PParams p) {
 #pragma unroll
         for (int b = 0; b < TN; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+    auto compute = [&](int bb) {
+#pragma unroll
+        for (int ks = 0; ks < kBK / 32; ++ks) {
+            const int kofs = ks * 32 + 8 * (lane >> 4);
+            bf16x8 af[TM];
+#pragma unroll
+            for (int a = 0; a < TM; ++a)
+                af[a] = *(const bf16x8 *)&xs[bb][(wm * WM + a * 16 + (lane & 15)) * kLdsRow + kofs];
+#pragma unroll
+            for (int b = 0; b < TN; ++b) {
+                const int wrow = wn * WN + b * 16 + (lane & 15);
+                const bf16x8 bfr = *(const bf16x8 *)&ws[bb][wrow * kLdsRow + kofs];
+                if (PREC == 8) {
+#pragma unroll
+                    for (int a = 0; a < TM; ++a)
+                        acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[a], bfr, acc[a][b], 0, 0, 0);
+                } else {
+                    const float sc = ssc[bb][wrow * CPR + ks];
+#pragma unroll
+                    for (int a = 0; a < TM; ++a) {
+                        const f32x4 part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            af[a], bfr, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) acc[a][b][e] = __builtin_fmaf(part[e], sc, acc[a][b][e]);
+                    }
+                }
+            }
+        }
+    };
+
+    // Register ring slot s holds a step's global loads; LDS buffer t % 2 holds
+    // step t.  Each iteration stages step t + 1 from its slot into the other
+    // buffer, refills that slot with step t + 3, computes step t, and ends with
+    // the one barrier of the step (step t + 1 visible, step t's reads done).
     // Steps are padded to a multiple of kDepth and every iteration loads and
     // computes unconditionally: steps past K read clamped addresses and meet
     // x = 0, so they add nothing, and the loop body has no branches at which
     // the compiler would have to wait for every load in flight.
+    static_assert(kDepth == 2, "two register slots, two LDS buffers");
     const int t_stop = t_begin + ((t_end - t_begin + kDepth - 1) / kDepth) * kDepth;
-#pragma unroll
-    for (int d = 0; d < kDepth; ++d) load_step(t_begin + d, d);
-    for (int t0 = t_begin; t0 < t_stop; t0 += kDepth) {
-#pragma unroll
-        for (int d = 0; d < kDepth; ++d) {
-            store_step(d);
-            lds_barrier();
-            load_step(t0 + d + kDepth, d);
-#pragma unroll
-            for (int ks = 0; ks < kBK / 32; ++ks) {
-                const int kofs = ks * 32 + 8 * (lane >> 4);
-                bf16x8 af[TM];
-#pragma unroll
-                for (int a = 0; a < TM; ++a)
-                    af[a] = *(const bf16x8 *)&xs[(wm * WM + a * 16 + (lane & 15)) * kLdsRow + kofs];
-#pragma unroll
-                for (int b = 0; b < TN; ++b) {
-                    const int wrow = wn * WN + b * 16 + (lane & 15);
-                    const bf16x8 bfr = *(const bf16x8 *)&ws[wrow * kLdsRow + kofs];
-                    if (PREC == 8) {
-#pragma unroll
-                        for (int a = 0; a < TM; ++a)
-                            acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[a], bfr, acc[a][b], 0, 0, 0);
-                    } else {
-                        const float sc = ssc[wrow * CPR + ks];
-#pragma unroll
-                        for (int a = 0; a < TM; ++a) {
-                            const f32x4 part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                                af[a], bfr, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) acc[a][b][e] = __builtin_fmaf(part[e], sc, acc[a][b][e]);
-                        }
-                    }
-                }
-            }
-            lds_barrier();
-        }
+    load_step(t_begin, 0);
+    load_step(t_begin + 1, 1);
+    store_step(0, 0);
+    lds_barrier();
+    load_step(t_begin + 2, 0);
+    for (int t0 = t_begin; t0 < t_stop; t0 += 2) {
+        store_step(1, 1);        // step t0 + 1
+        load_step(t0 + 3, 1);
+        compute(0);              // step t0
+        lds_barrier();
+        store_step(0, 0);        // step t0 + 2
+        load_step(t0 + 4, 0);
+        compute(1);              // step t0 + 1
+        lds_barrier();
     }
 
     // ---- epilogue: lane holds C[4 (lane / 16) + e][lane % 16] of each tile
