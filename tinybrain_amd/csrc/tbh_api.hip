@@ -494,9 +494,9 @@ tbh_status tbh_weight_create(tbh_device *dev, const tbh_qtensor_desc *desc, tbh_
                 std::vector<int8_t> z((size_t)(w->Np * G), 0);
                 for (int64_t n = 0; n < N; ++n)
                     for (int64_t g = 0; g < G; ++g) {
-                        int64_t gi = group_of(seg ? g * seg : 0, n);
-                        s[n * G + g] = d.scales[gi];
-                        if (d.zero_points) z[n * G + g] = d.zero_points[gi];
+                        const int64_t gi = group_of(seg ? g * seg : 0, n);
+                        s[kgroup_index(n, g, G)] = d.scales[gi];
+                        if (d.zero_points) z[kgroup_index(n, g, G)] = d.zero_points[gi];
                     }
                 if (e == hipSuccess) e = upload(&w->scales, s.data(), s.size(), w->device_bytes, w->n_scales_dev);
                 if (e == hipSuccess && has_zp) e = upload(&w->zp, z.data(), z.size(), w->device_bytes, w->n_zp_dev);

@@ -18,6 +18,14 @@ constexpr int kChunkBytes = 16;
 constexpr int kInt8ChunkElems = 16;
 constexpr int kInt4ChunkElems = 32;
 
+// INT4 K-group scales and zero points of the row layout, [Np / 4][G][4]:
+// the four rows of a row quad sit side by side for each group, so a wave
+// that owns four rows reads the scales of one chunk with one 16-byte load.
+// Np is a multiple of 8.
+__host__ __device__ __forceinline__ int64_t kgroup_index(int64_t n, int64_t g, int64_t G) {
+    return ((n >> 2) * G + g) * 4 + (n & 3);
+}
+
 // Largest x tile (M * Kp fp32) the VALU GEMV keeps in LDS.
 constexpr int64_t kMaxLdsBytes = 64 * 1024;
 

@@ -138,7 +138,7 @@ __global__ __launch_bounds__(256) void gemm_bf16(const PParams p) {
             const int64_t nn = in ? n : 0, cc = in ? c : 0;
             wr[d][j] = __builtin_nontemporal_load((const u32x4 *)(p.data + nn * p.row_bytes + cc * 16));
             if (PREC == 4) {
-                const int64_t gi = nn * p.G + cc / p.cpg;
+                const int64_t gi = kgroup_index(nn, cc / p.cpg, p.G);
                 sr[d][j] = p.scales[gi];
                 if (ZP) zq[d][j] = p.zp[gi];
             } else if (ZP) {

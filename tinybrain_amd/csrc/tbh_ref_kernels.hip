@@ -101,7 +101,7 @@ __global__ void dequant_int4_kgroup(const DequantParams p) {
          idx += (int64_t)gridDim.x * blockDim.x) {
         const int64_t k = idx / p.N, n = idx - k * p.N;
         const int q = int4_repacked(p.data + n * p.row_bytes, k);
-        const int64_t gi = n * p.G + (k / kInt4ChunkElems) / p.cpg;
+        const int64_t gi = kgroup_index(n, (k / kInt4ChunkElems) / p.cpg, p.G);
         const int z = p.zp ? (int)p.zp[gi] : 0;
         p.out[idx] = __fmul_rn((float)q - (float)z, p.scales[gi]);
     }
