@@ -402,6 +402,14 @@ __global__ __launch_bounds__(256) void gemv_valu(const KParams p) {
     }
 }
 
+// A wave-uniform element offset pinned in scalar registers: loads then take
+// the form base (SGPR pair) + 32-bit lane offset, instead of the compiler
+// folding the row offset into per-lane 64-bit multiply-adds.
+__device__ __forceinline__ int64_t uniform_offset(int64_t v) {
+    asm volatile("" : "+s"(v));
+    return v;
+}
+
 // Workgroup barrier that orders LDS only: it does not wait for the global
 // loads still in flight, which a full __syncthreads() fence would.
 __device__ __forceinline__ void lds_barrier() {
@@ -433,7 +441,8 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
     __shared__ float red[4];
 
     constexpr int lds_row = 64 * I * CS;  // LDS floats per x row: every slot the loads cover
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps r0 scalar
     const int r0 = (blockIdx.x * 4 + wave) * U;
 
     // ---- 1. x loads (16-byte aligned rows, K % 4 == 0; clamped addresses,
@@ -463,7 +472,9 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
         }
     }
 
-    // ---- 2. all weight (and scale) loads of the wave, in consumption order
+    // ---- 2. all weight (and scale) loads of the wave, in consumption order.
+    // Row and quad base addresses are wave-uniform (scalar registers); a lane
+    // adds only its chunk offset, so no 64-bit address math lands on the VALU.
     u32x4 w[I][U];
     float s[I][U];
 #pragma unroll
@@ -472,24 +483,29 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
         // a shift, not a division: a per-lane integer division here delays
         // every wave's first loads (measured 9.7 -> 9.0 us on 32000x2048)
         const int g = c >> p.cpg_shift;
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int64_t row = min(r0 + u, p.Np - 1);
-            w[i][u] = __builtin_nontemporal_load(
-                (const u32x4 *)(p.data + row * p.row_bytes + (int64_t)c * 16));
-            if (PREC == 4 && U < 4) s[i][u] = p.scales[kgroup_index(row, g, p.G)];
-        }
         if constexpr (PREC == 4 && U >= 4) {
-            // one 16-byte load per row quad: the quad's four scales of group g
+            // a row quad's four scales of group g in one 16-byte load, issued
+            // ahead of the quad's weights so the first row need not wait for
+            // the last load of the wave
 #pragma unroll
             for (int q = 0; q < U / 4; ++q) {
-                const int64_t quad = min(r0 + 4 * q, p.Np - 4);  // r0 is a multiple of 4
-                const f32x4 sv = __builtin_nontemporal_load((const f32x4 *)(p.scales + kgroup_index(quad, g, p.G)));
+                const int quad = min(r0 + 4 * q, p.Np - 4);  // r0 is a multiple of 4
+                const float *sq = p.scales + uniform_offset((int64_t)(quad >> 2) * p.G * 4);
+                const f32x4 sv = __builtin_nontemporal_load((const f32x4 *)(sq + (uint32_t)(4 * g)));
                 s[i][4 * q] = sv.x;
                 s[i][4 * q + 1] = sv.y;
                 s[i][4 * q + 2] = sv.z;
                 s[i][4 * q + 3] = sv.w;
             }
+            __builtin_amdgcn_sched_barrier(0);  // keep the scale loads first
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int row = min(r0 + u, p.Np - 1);
+            const uint8_t *rp = p.data + uniform_offset((int64_t)row * p.row_bytes);
+            w[i][u] = __builtin_nontemporal_load((const u32x4 *)(rp + (uint32_t)(16 * c)));
+            if (PREC == 4 && U < 4)
+                s[i][u] = p.scales[(int64_t)(row >> 2) * p.G * 4 + (row & 3) + 4 * g];  // kgroup_index
         }
     }
     const int ridx = reduce_index<V>(lane);  // value this lane holds after the reduce
