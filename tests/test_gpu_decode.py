@@ -87,6 +87,21 @@ def test_decode_tinyllama_width(backend):
     dec.close()
 
 
+@pytest.mark.parametrize("heads", [(4, 2), (16, 2), (8, 8)])
+def test_decode_long_context(backend, heads):
+    # more than two 64-position attention ranges, so the step's attention
+    # combines several range partials (and, for 4/2, a quad with idle waves)
+    nh, nkv = heads
+    cfg = T.DecoderConfig(**dict(SMALL, num_heads=nh, num_kv_heads=nkv, max_seq=160))
+    dec, ref = _model(backend, cfg, "int8", seed=61 + nh)
+    rng = np.random.default_rng(nh * 7 + nkv)
+    for i, tok in enumerate(rng.integers(0, cfg.vocab, size=150)):
+        y = dec.step(int(tok))
+        r = ref.step(int(tok))
+        assert _gated(y, r) <= GATE, (i, _gated(y, r))
+    dec.close()
+
+
 def test_decode_reset_is_deterministic(backend):
     cfg = T.DecoderConfig(**SMALL)
     dec, _ = _model(backend, cfg, "int8", seed=31)

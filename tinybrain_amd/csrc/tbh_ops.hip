@@ -243,27 +243,34 @@ __global__ __launch_bounds__(W == 1 ? 256 : 64 * W) void softmax_reg(const float
         const int j = t + T * i;
         v[i] = j < n4 ? xr[min(j, n4 - 1)] : float4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
     }
-    float m = -INFINITY;
+    // Each thread exponentiates its own elements against its own maximum as
+    // soon as its loads land (overlapping the exponentials with the rest of
+    // the block's loads); the block maximum M then rescales by e^(m_t - M):
+    // e^(x - m_t) e^(m_t - M) = e^(x - M).  Tensor.softmaxCPU computes
+    // exp(x - max) / (sum + epsilon); an all -inf row gives NaN there
+    // (x - max = NaN) and here (m_t - M = NaN).
+    float mt = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < R; ++i) m = fmaxf(m, fmaxf(fmaxf(v[i].x, v[i].y), fmaxf(v[i].z, v[i].w)));
-    m = block_max<W>(m, red);
-    // Tensor.softmaxCPU: exp(x - max) / (sum + epsilon); an all -inf row
-    // gives NaN there (x - max = NaN) and here
-    float sm = 0.0f;
+    for (int i = 0; i < R; ++i) mt = fmaxf(mt, fmaxf(fmaxf(v[i].x, v[i].y), fmaxf(v[i].z, v[i].w)));
+    const bool none = mt == -INFINITY;  // this thread's elements are all -inf (or padding)
+    float st = 0.0f;
 #pragma unroll
     for (int i = 0; i < R; ++i) {
-        v[i] = float4{expf(v[i].x - m), expf(v[i].y - m), expf(v[i].z - m), expf(v[i].w - m)};
+        v[i] = none ? float4{0.f, 0.f, 0.f, 0.f}
+                    : float4{expf(v[i].x - mt), expf(v[i].y - mt), expf(v[i].z - mt), expf(v[i].w - mt)};
         const int j = t + T * i;
-        if (j < n4) sm += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+        if (j < n4) st += (v[i].x + v[i].y) + (v[i].z + v[i].w);
     }
-    sm = block_sum<W>(sm, red);
+    const float m = block_max<W>(mt, red);
+    const float f = expf(mt - m);
+    const float sm = block_sum<W>(none ? 0.0f : st * f, red);
     if (row >= rows) return;
-    const float den = sm + kSoftmaxEps;
+    const float k = f / (sm + kSoftmaxEps);
     float4 *yr = (float4 *)(y + r * cols);
 #pragma unroll
     for (int i = 0; i < R; ++i) {
         const int j = t + T * i;
-        if (j < n4) yr[j] = float4{v[i].x / den, v[i].y / den, v[i].z / den, v[i].w / den};
+        if (j < n4) yr[j] = float4{v[i].x * k, v[i].y * k, v[i].z * k, v[i].w * k};
     }
 }
 
