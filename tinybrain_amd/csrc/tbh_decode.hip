@@ -154,13 +154,22 @@ __global__ __launch_bounds__(256) void attention_split(const AttnParams a) {
     float vx[NPL * 2];
 #pragma unroll
     for (int i = 0; i < 2 * NPL; ++i) vx[i] = a.qkv[a.hidden + a.kvd + kvo + min(lane + 64 * i, HD - 1)];
-    float4 kreg[HD4];
-    {
+    // key rows: with HD / 4 a power of two, lane (pg, d4) reads piece d4 of
+    // rows pg, pg + PPI, ... (whole row segments per load instruction) and a
+    // DPP transpose-sum assembles the scores; otherwise one row per lane
+    constexpr bool kCoop = (HD4 & (HD4 - 1)) == 0;
+    constexpr int NK = kCoop ? kSplit / PPI : HD4;
+    const int pg = lane / HD4, d4 = lane % HD4;
+    float4 kreg[NK];
+    if constexpr (kCoop) {
+#pragma unroll
+        for (int j = 0; j < NK; ++j)
+            kreg[j] = *(const float4 *)(a.kcache + (int64_t)min(c0 + pg + j * PPI, last) * a.kvd + kvo + 4 * d4);
+    } else {
         const float *kr = a.kcache + (int64_t)min(c0 + lane, last) * a.kvd + kvo;
 #pragma unroll
         for (int i = 0; i < HD4; ++i) kreg[i] = *(const float4 *)(kr + 4 * i);
     }
-    const int pg = lane / HD4, d4 = lane % HD4;
     float4 vreg[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
@@ -191,21 +200,37 @@ __global__ __launch_bounds__(256) void attention_split(const AttnParams a) {
         if (lane + 64 * i < HD) vn[w][lane + 64 * i] = vx[i];
     wave_lds_fence();
 
-    // one position per lane
-    const int t = c0 + lane;
-    const bool tvalid = t <= pos, tnew = t == pos;
+    // one position per lane: lane (pg, d4) scores position pg + PPI * d4
+    // (cooperative form) or position lane
+    const int tl = kCoop ? pg + PPI * d4 : lane;
+    const int t = c0 + tl;
+    const bool tvalid = t <= pos;
     float d = 0.0f;
+    if constexpr (kCoop) {
+        const float4 q4 = *(const float4 *)&qs[w][4 * d4];
+        const float4 n4 = *(const float4 *)&kn[w][4 * d4];
+        const float dn = q4.x * n4.x + q4.y * n4.y + q4.z * n4.z + q4.w * n4.w;
+        float part[NK];
 #pragma unroll
-    for (int i = 0; i < HD4; ++i) {
-        const float4 k4 = tnew ? *(const float4 *)&kn[w][4 * i] : kreg[i];
-        const float4 q4 = *(const float4 *)&qs[w][4 * i];
-        d += q4.x * k4.x + q4.y * k4.y + q4.z * k4.z + q4.w * k4.w;
+        for (int j = 0; j < NK; ++j) {
+            const float dj = q4.x * kreg[j].x + q4.y * kreg[j].y + q4.z * kreg[j].z + q4.w * kreg[j].w;
+            part[j] = c0 + pg + j * PPI == pos ? dn : dj;   // row pos: the new k
+        }
+        d = wave::transpose_sum<NK>(part, lane);
+    } else {
+        const bool tnew = t == pos;
+#pragma unroll
+        for (int i = 0; i < HD4; ++i) {
+            const float4 k4 = tnew ? *(const float4 *)&kn[w][4 * i] : kreg[i];
+            const float4 q4 = *(const float4 *)&qs[w][4 * i];
+            d += q4.x * k4.x + q4.y * k4.y + q4.z * k4.z + q4.w * k4.w;
+        }
     }
     const float sc = tvalid ? d * a.scale : -INFINITY;
     const float m = wave::max(sc);                    // finite: position c0 <= pos
     const float p = tvalid ? expf(sc - m) : 0.0f;
     const float l = wave::sum(p);
-    ps[w][lane] = p;
+    ps[w][tl] = p;
     wave_lds_fence();
 
     float4 acc = float4{0.f, 0.f, 0.f, 0.f};

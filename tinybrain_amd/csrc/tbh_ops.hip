@@ -620,17 +620,19 @@ __device__ __forceinline__ void wave_lds_fence() {
 // Attention for head_dim HD in {16, 32, 64, 128}: one wave per (query row,
 // query head, range of key positions); a block's four waves are four query
 // heads of one key/value head, so they share the range's key and value rows
-// through L1, and no wave waits for another.  A pass covers 64 positions,
-// one per lane for the scores (16-byte key loads), with max and sum by DPP;
-// p * v takes 16-byte value pieces (lane (pg, d4) covers rows pg,
-// pg + 64 / (HD / 4), ...).  The wave keeps an online softmax across
-// passes; with one split it writes the output, else its range's (max, sum,
-// p.v) partial for attention_combine.
+// through L1, and no wave waits for another.  A pass covers 64 positions.
+// Lane (pg, d4) loads 16-byte piece d4 of key and value rows pg, pg + PPI,
+// ... (PPI = 64 / (HD / 4) rows per load instruction, so every load reads
+// whole row segments); its partial dot products with q piece d4 are summed
+// over the row's HD / 4 lanes by a DPP transpose-sum, after which the lane
+// holds the score of position pg + PPI * d4.  Max and sum by DPP, p * v
+// over the value pieces.  The wave keeps an online softmax across passes;
+// with one split it writes the output, else its range's (max, sum, p.v)
+// partial for attention_combine.
 template <int HD>
 __global__ __launch_bounds__(256) void attention_wave(const GrpArgs g) {
     constexpr int HD4 = HD / 4, PPI = 64 / HD4, NV = HD4;
     const AttnArgs &a = g.a;
-    __shared__ __attribute__((aligned(16))) float qs[4][HD];
     __shared__ float ps[4][64];
     __shared__ float4 red[4][64];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -647,40 +649,39 @@ __global__ __launch_bounds__(256) void attention_wave(const GrpArgs g) {
     const int head = kvh * g.rep + hg;
     const int64_t batch = bq / a.seq_len;
     const int64_t kvd = (int64_t)a.nkv * HD;
-    const float *qrow = a.q + (bq * a.nh + head) * HD;
     const float *kb = a.k + batch * a.kv_len * kvd + (int64_t)kvh * HD;
     const float *vb = a.v + batch * a.kv_len * kvd + (int64_t)kvh * HD;
-    for (int d = lane; d < HD; d += 64) qs[w][d] = qrow[d];
     const int64_t c0 = split * g.chunk, c1 = min(a.kv_len, c0 + g.chunk);
     const int pg = lane / HD4, d4 = lane % HD4;
-    wave_lds_fence();
+    const float *qrow = a.q + (bq * a.nh + head) * HD + 4 * d4;
+    const float4 q4 = float4{qrow[0], qrow[1], qrow[2], qrow[3]};   // q rows need not be 16-byte aligned
 
     float m = -INFINITY, l = 0.0f;
     float4 acc = float4{0.f, 0.f, 0.f, 0.f};
     for (int64_t p0 = c0; p0 < c1; p0 += 64) {
-        const int64_t t = p0 + lane, last = c1 - 1;
-        const bool tv = t < c1;
+        const int64_t last = c1 - 1;
         float4 kreg[HD4], vreg[NV];
-        const float *kr = kb + min(t, last) * kvd;
 #pragma unroll
-        for (int i = 0; i < HD4; ++i) kreg[i] = *(const float4 *)(kr + 4 * i);
+        for (int j = 0; j < HD4; ++j)
+            kreg[j] = *(const float4 *)(kb + min(p0 + pg + j * PPI, last) * kvd + 4 * d4);
 #pragma unroll
         for (int j = 0; j < NV; ++j)
             vreg[j] = *(const float4 *)(vb + min(p0 + pg + j * PPI, last) * kvd + 4 * d4);
+        const int64_t t = p0 + pg + PPI * d4;     // this lane's position after the transpose-sum
+        const bool tv = t < c1;
         const float mk = a.mask ? a.mask[min(t, last)] : 0.0f;
-        float d = 0.0f;
+        float part[HD4];
 #pragma unroll
-        for (int i = 0; i < HD4; ++i) {
-            const float4 q4 = *(const float4 *)&qs[w][4 * i];
-            d += q4.x * kreg[i].x + q4.y * kreg[i].y + q4.z * kreg[i].z + q4.w * kreg[i].w;
-        }
+        for (int j = 0; j < HD4; ++j)
+            part[j] = q4.x * kreg[j].x + q4.y * kreg[j].y + q4.z * kreg[j].z + q4.w * kreg[j].w;
+        const float d = wave::transpose_sum<HD4>(part, lane);
         const float sc = tv ? d * a.scale + mk : -INFINITY;
         const float nm = fmaxf(m, wave_max(sc));
         if (nm == -INFINITY) continue;            // every position so far masked (uniform)
         const float corr = expf(m - nm);
         const float p = expf(sc - nm);
         l = l * corr + wave_sum(p);
-        ps[w][lane] = p;
+        ps[w][pg + PPI * d4] = p;
         wave_lds_fence();
         acc.x *= corr;
         acc.y *= corr;

@@ -60,5 +60,35 @@ __device__ __forceinline__ float max(float v) {
     return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
 }
 
+// Transpose-sum inside aligned groups of G lanes (G = 4, 8, 16 or 32), each
+// lane holding G values: afterwards lane l holds the group's total of value
+// index l % G.  Each stage halves the values a lane carries -- a lane keeps
+// the upper half when its stage bit is set and adds the partner's copy of
+// the half it keeps -- so the cost is G - 1 exchanges instead of G full
+// reductions.  Partners: lane ^ 16 (through LDS), then row mirror, half-row
+// mirror, quad swaps (DPP); a mirror partner differs in the stage bit and
+// shares every higher bit, which is all the pairing needs.
+template <int CTRL, int N>
+__device__ __forceinline__ void transpose_stage(float *v, bool upper) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const float send = upper ? v[i] : v[i + N];
+        const float keep = upper ? v[i + N] : v[i];
+        if constexpr (CTRL < 0) v[i] = keep + __shfl_xor(send, 16);
+        else v[i] = keep + dpp<CTRL>(send);
+    }
+}
+
+template <int G>
+__device__ __forceinline__ float transpose_sum(float (&v)[G], int lane) {
+    static_assert(G == 4 || G == 8 || G == 16 || G == 32, "group of 4, 8, 16 or 32 lanes");
+    if constexpr (G >= 32) transpose_stage<-1, 16>(v, lane & 16);
+    if constexpr (G >= 16) transpose_stage<kRowMirror, 8>(v, lane & 8);
+    if constexpr (G >= 8) transpose_stage<kHalfMirror, 4>(v, lane & 4);
+    transpose_stage<kXor2, 2>(v, lane & 2);
+    transpose_stage<kXor1, 1>(v, lane & 1);
+    return v[0];
+}
+
 }  // namespace wave
 }  // namespace tbh
