@@ -597,20 +597,23 @@ def main():
         backend.close()
         return
 
+    # Launches are captured into HIP graphs (one graph = one sweep over the
+    # pool), so the timed region measures the GPU, not Python/ctypes launch
+    # overhead.  Replays are checked against an eager run on the capture
+    # stream (which also sizes that stream's split-K workspace, so the
+    # captured launches split K exactly as the eager ones do).
+    cap = torch.cuda.Stream(dev)
+    cap.wait_stream(stream)
+
     def step(i):
         ws = pool[i % n_sets]
         for j, (N, K) in enumerate(shapes):
-            backend.matmul_device(xs[K], ws[j], out=ys[j], stream=stream)
+            backend.matmul_device(xs[K], ws[j], out=ys[j], stream=cap)
 
-    # Launches are captured into HIP graphs (one graph = one sweep over the
-    # pool), so the timed region measures the GPU, not Python/ctypes launch
-    # overhead.  Replays are checked against an eager run before timing.
     for i in range(n_sets):
         step(i)
     torch.cuda.synchronize()
     eager = [y.clone() for y in ys]
-    cap = torch.cuda.Stream(dev)
-    cap.wait_stream(stream)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=cap):
         for i in range(n_sets):

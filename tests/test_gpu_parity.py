@@ -277,6 +277,91 @@ def test_device_resident_entry_point(backend):
 
 
 # ---------------------------------------------------------------------------
+# 2..8 rows of x on the matrix cores (tbh_sgemv.hip): row-layout INT4 K-group
+# weights without zero points; small N splits K over blocks
+# ---------------------------------------------------------------------------
+@pytest.fixture
+def sgemv_from_two_rows(monkeypatch):
+    monkeypatch.setenv("TBH_SGEMV_MIN_ROWS", "2")   # the MFMA path for every M >= 2
+    yield
+
+
+@pytest.mark.parametrize("M", [2, 3, 4, 5, 6, 7, 9, 16])
+@pytest.mark.parametrize("K,N,gs", [(1024, 96, 32), (2048, 1000, 64), (4096, 300, 128), (160, 24, 32),
+                                    (5632, 2048, 32)])
+def test_sgemv_every_m(backend, sgemv_from_two_rows, M, K, N, gs):
+    qt = _int4_nk(600 + M + K + gs, K, N, gs)
+    _check(backend, _product(qt, (K, N), T.Layout.NK_FLAT), qt, Ms=(M,), cpu_path=False)
+
+
+def test_sgemv_x_range_extremes(backend, sgemv_from_two_rows):
+    # per-row power-of-two rescaling: huge, tiny and zero rows, and rows with
+    # one huge or one tiny 32-element chunk
+    K, N = 1024, 200
+    qt = _int4_nk(701, K, N, 32)
+    pq = _product(qt, (K, N), T.Layout.NK_FLAT)
+    W = _oracle_weight(qt, T.Layout.NK_FLAT)
+    x = O.fill_normal(702, 6 * K).reshape(6, K)
+    x[0] *= 1e6
+    x[1] *= 1e-7
+    x[2, ::3] = 0.0
+    x[3, :] = 0.0
+    x[4, :32] *= 1e20               # one huge chunk, the rest ordinary
+    x[5, 32:64] *= 1e-20            # one tiny chunk
+    y = backend.matmulQuantized(x, pq)
+    y64 = O.gemm_f64(x, W)
+    for m in (0, 1, 2, 4, 5):
+        assert O.parity_errors(y[m:m + 1], y64[m:m + 1])["gated"] <= GATE, m
+    assert np.all(y[3] == 0.0)
+
+
+def test_sgemv_split_k_determinism_and_graphs(backend, sgemv_from_two_rows):
+    # N = 2048 gives 16 blocks of 128 rows, so K is split over blocks and the
+    # splits are summed in a fixed order by a second kernel.  Captured on a
+    # stream with no workspace yet, the launch runs unsplit or falls back to
+    # the VALU kernel; captured after an eager call, the split launch.
+    import torch
+
+    K, N, M = 2048, 2048, 8
+    oq = _int4_nk(801, K, N, 32)
+    w = backend.weight(_product(oq, (K, N), T.Layout.NK_FLAT))
+    xh = O.fill_normal(802, M * K).reshape(M, K)
+    ref = O.gemm_f64(xh, _oracle_weight(oq, T.Layout.NK_FLAT))
+    x = torch.from_numpy(xh).cuda()
+    a = backend.matmul_device(x, w)
+    b = backend.matmul_device(x, w)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(a.cpu().numpy(), b.cpu().numpy())
+    assert O.parity_errors(a.cpu().numpy(), ref)["gated"] <= GATE
+    s = torch.cuda.Stream()
+    y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    for phase in range(2):
+        if phase == 1:
+            with torch.cuda.stream(s):
+                backend.matmul_device(x, w, out=y, stream=s)
+            torch.cuda.synchronize()
+            eager = y.cpu().numpy().copy()
+            np.testing.assert_array_equal(eager, a.cpu().numpy())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            backend.matmul_device(x, w, out=y, stream=s)
+        first = None
+        for _ in range(3):
+            y.zero_()
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            got = y.cpu().numpy()
+            assert O.parity_errors(got, ref)["gated"] <= GATE, phase
+            if first is None:
+                first = got.copy()
+            np.testing.assert_array_equal(got, first)
+        if phase == 1:
+            np.testing.assert_array_equal(first, eager)
+        del g
+
+
+# ---------------------------------------------------------------------------
 # both HBM layouts: K-contiguous rows (VALU GEMV, default) and 1 KiB MFMA
 # tiles (MFMA GEMV, TBH_LAYOUT=tiles)
 # ---------------------------------------------------------------------------

@@ -631,14 +631,27 @@ static tbh_status matmul_enqueue(const tbh_weight *w, const float *x, int64_t M,
                                  hipStream_t s) {
     if (!weight_arrays_ok(*w))
         return set_error(TBH_E_INVALID, "weight device arrays are inconsistent with its layout");
-    const int64_t rows = w->mfma_tiles ? 8 : gemv_max_rows(*w);
+    // 5..8 rows of x per launch on the matrix cores when the weight allows
+    // it (measured: at M = 8 half the time of two 4-row VALU launches; at
+    // M <= 4 the VALU kernels are as fast or faster).  TBH_SGEMV_MIN_ROWS
+    // moves the threshold (2..9; 9 turns the MFMA path off).
+    const char *min_env = std::getenv("TBH_SGEMV_MIN_ROWS");
+    const int64_t sg_min = min_env && *min_env ? std::max(2, std::atoi(min_env)) : 5;
+    const bool sg = M >= sg_min && sgemv_supported(*w);
+    const int64_t rows = w->mfma_tiles || sg ? 8 : gemv_max_rows(*w);
     for (int64_t m0 = 0; m0 < M;) {
-        const int64_t mc = rows > 0 ? std::min(rows, M - m0) : M - m0;
+        int64_t mc = rows > 0 ? std::min(rows, M - m0) : M - m0;
         GemvArgs a{x + m0 * w->K, w->K, y + m0 * w->N, w->N, mc};
-        hipError_t e;
+        hipError_t e = hipErrorInvalidValue;
         if (w->mfma_tiles) e = launch_mgemv(*w, a, s);
-        else if (rows > 0) e = launch_gemv(*w, a, s);
-        else e = launch_generic(*w, a, s);
+        else if (sg && mc >= sg_min) e = launch_sgemv(*w, a, s);
+        if (e == hipErrorInvalidValue && !w->mfma_tiles) {
+            // the VALU kernels (at most gemv_max_rows rows per launch)
+            const int64_t vr = gemv_max_rows(*w);
+            mc = vr > 0 ? std::min(vr, mc) : mc;
+            a.M = mc;
+            e = vr > 0 ? launch_gemv(*w, a, s) : launch_generic(*w, a, s);
+        }
         if (e != hipSuccess) return hip_error(e, "matmul kernel launch");
         m0 += mc;
     }

@@ -73,8 +73,8 @@ struct tbh_weight {
     // fast paths: data [Np][row_bytes], offset-binary values
     int64_t Kp = 0, Np = 0, row_bytes = 0;
     uint8_t *data = nullptr;
-    float *scales = nullptr;     // Int8Row [Np]; Int4KGroup [Np][G]; Int4NGroup [NB][Kp]
-    int8_t *zp = nullptr;        // Int8Row [Np]; Int4KGroup [Np][G]; null when all zero
+    float *scales = nullptr;     // Int8Row [Np]; Int4KGroup [Np/4][G][4] (row quads); Int4NGroup [NB][Kp]
+    int8_t *zp = nullptr;        // Int8Row [Np]; Int4KGroup as scales; null when all zero
     int64_t groups_per_row = 1;  // G (Int4KGroup)
     int32_t chunks_per_group = 1;
     int32_t rows_per_nblock = 1; // Int4NGroup
@@ -140,6 +140,13 @@ struct FusedGemvArgs {
 };
 bool gemv_fused_supported(const tbh_weight &w);
 hipError_t launch_gemv_fused(const tbh_weight &w, const FusedGemvArgs &f, hipStream_t s);
+
+// MFMA dequant-GEMV for 2 <= M <= 8 rows of x on row-layout INT4 K-group
+// weights without zero points (tbh_sgemv.hip).  launch_sgemv returns
+// hipErrorInvalidValue for shapes it does not take (odd alignment of x,
+// M out of range, no workspace while capturing a long row).
+bool sgemv_supported(const tbh_weight &w);
+hipError_t launch_sgemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s);
 
 // MFMA dequant-GEMV for M <= 8 rows of x on MFMA-tiled weights (tbh_mgemv.hip).
 hipError_t launch_mgemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s);
