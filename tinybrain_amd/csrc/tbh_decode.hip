@@ -280,24 +280,24 @@ __global__ __launch_bounds__(256) void attention_split(const AttnParams a) {
 
 // ctx of head h = sum over splits of e^(m_s - M) o_s / sum of e^(m_s - M) l_s
 // with M = max m_s (the softmax of :545-551 assembled from the ranges).  One
-// block per (unit, head).  Thread (sg, d4) loads the partials of splits
-// sg, sg + 256 / (hd / 4), ... (up to kMergeLoads of them) together with the
-// position, so the usual case costs one memory round trip; splits past pos
-// are masked out afterwards.
-constexpr int kMergeLoads = 4;
+// wave per (unit, head), no block barriers: lane (sg, d4) loads the partials
+// of splits sg, sg + 64 / (hd / 4), ... (up to kMergeLoads of them) together
+// with the position, so up to 32 ranges (2048 positions at head_dim 64)
+// cost one memory round trip; splits past pos are masked out afterwards.
+// Max and sum by DPP; the value pieces of the split groups meet in LDS.
+constexpr int kMergeLoads = 8;
 
 template <int HD>
-__global__ __launch_bounds__(256) void attention_merge(const AttnParams a) {
-    constexpr int HD4 = HD / 4, NSG = 256 / HD4;
+__global__ __launch_bounds__(64) void attention_merge(const AttnParams a) {
+    constexpr int HD4 = HD / 4, NSG = 64 / HD4;
     constexpr int64_t kStride = 2 * kGroup + kGroup * HD;
-    __shared__ float4 red[256];
-    __shared__ float rs[8];
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    __shared__ float4 red[64];
+    const int lane = threadIdx.x;
     const int unit = blockIdx.x / kGroup, h = blockIdx.x % kGroup;
     const int hc = unit % a.hchunks, kvh = unit / a.hchunks;
     if (h >= a.rep - hc * kGroup) return;
     const float *pb = a.part + (int64_t)unit * a.splits * kStride;
-    const int sg = tid / HD4, d4 = tid % HD4;
+    const int sg = lane / HD4, d4 = lane % HD4;
     const bool slane = sg < NSG;
     const int pos = a.pos[0];
     float mv[kMergeLoads], lv[kMergeLoads];
@@ -307,7 +307,7 @@ __global__ __launch_bounds__(256) void attention_merge(const AttnParams a) {
         const int sp = min(sg + NSG * j, a.splits - 1);
         mv[j] = pb[sp * kStride + h];
         lv[j] = pb[sp * kStride + kGroup + h];
-        ov[j] = *(const float4 *)(pb + sp * kStride + 2 * kGroup + h * HD + 4 * d4);
+        ov[j] = *(const float4 *)(pb + sp * kStride + 2 * kGroup + h * HD + 4 * min(d4, HD4 - 1));
     }
     if (pos < 0 || pos >= a.max_seq) return;
     const int ns = pos / kSplit + 1;
@@ -316,15 +316,12 @@ __global__ __launch_bounds__(256) void attention_merge(const AttnParams a) {
     for (int j = 0; j < kMergeLoads; ++j)
         if (slane && sg + NSG * j < ns) mloc = fmaxf(mloc, mv[j]);
     for (int sp = sg + NSG * kMergeLoads; slane && sp < ns; sp += NSG) mloc = fmaxf(mloc, pb[sp * kStride + h]);
-    mloc = wave::max(mloc);
-    if (lane == 0) rs[wv] = mloc;
-    __syncthreads();
-    const float M = fmaxf(fmaxf(rs[0], rs[1]), fmaxf(rs[2], rs[3]));
+    const float M = wave::max(mloc);
     float L = 0.0f;
     float4 o = float4{0.f, 0.f, 0.f, 0.f};
     auto add = [&](float m, float l, float4 v) {
         const float e = expf(m - M);
-        if (d4 == 0) L += e * l;   // one thread per split counts its sum
+        if (d4 == 0) L += e * l;   // one lane per split counts its sum
         o.x += e * v.x;
         o.y += e * v.y;
         o.z += e * v.z;
@@ -337,21 +334,21 @@ __global__ __launch_bounds__(256) void attention_merge(const AttnParams a) {
         add(pb[sp * kStride + h], pb[sp * kStride + kGroup + h],
             *(const float4 *)(pb + sp * kStride + 2 * kGroup + h * HD + 4 * d4));
     L = wave::sum(L);
-    if (lane == 0) rs[4 + wv] = L;
-    red[tid] = o;
-    __syncthreads();
-    if (tid < HD4) {
-        float4 r = float4{0.f, 0.f, 0.f, 0.f};
-        for (int q = 0; q < NSG; ++q) {
-            const float4 v = red[q * HD4 + tid];
+    red[lane] = o;
+    wave_lds_fence();
+    if (lane < HD4) {
+        float4 r = red[lane];
+#pragma unroll
+        for (int q = 1; q < NSG; ++q) {
+            const float4 v = red[q * HD4 + lane];
             r.x += v.x;
             r.y += v.y;
             r.z += v.z;
             r.w += v.w;
         }
-        const float inv = 1.0f / ((rs[4] + rs[5]) + (rs[6] + rs[7]));
+        const float inv = 1.0f / L;
         const int head = kvh * a.rep + hc * kGroup + h;
-        *(float4 *)&a.ctx[(int64_t)head * HD + 4 * tid] = float4{r.x * inv, r.y * inv, r.z * inv, r.w * inv};
+        *(float4 *)&a.ctx[(int64_t)head * HD + 4 * lane] = float4{r.x * inv, r.y * inv, r.z * inv, r.w * inv};
     }
 }
 
@@ -359,7 +356,7 @@ template <int HD>
 void launch_attention_hd(const AttnParams &ap, hipStream_t s) {
     const int units = ap.nkv * ap.hchunks, nquad = (ap.rep + 3) / 4;
     hipLaunchKernelGGL(attention_split<HD>, dim3((unsigned)(ap.nkv * nquad * ap.splits)), dim3(256), 0, s, ap);
-    hipLaunchKernelGGL(attention_merge<HD>, dim3((unsigned)(units * kGroup)), dim3(256), 0, s, ap);
+    hipLaunchKernelGGL(attention_merge<HD>, dim3((unsigned)(units * kGroup)), dim3(64), 0, s, ap);
 }
 
 void launch_attention(const AttnParams &ap, hipStream_t s) {
