@@ -34,6 +34,7 @@
 // by the block's eight waves.  Small N is split along K over blocks; a
 // second kernel adds the splits in split order (deterministic).
 #include <cmath>
+#include <cstdlib>
 
 #include "tbh_internal.h"
 #include "tbh_wave.h"
@@ -330,7 +331,11 @@ hipError_t launch_sgemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s) {
     static_assert(kMaxChunks * 8 * 8 <= 512 * kXUnits, "x units of M = 8 rows per thread");
     const int64_t nblk = (w.Np + kRows - 1) / kRows;
     const int64_t cus = std::max(1, w.dev->cu_count);
-    const int64_t want = std::max<int64_t>(1, (3 * cus / 4 + nblk - 1) / nblk);
+    static const int split_pct = [] {
+        const char *v = std::getenv("TBH_SGEMV_SPLIT_PCT");   // percent of the CUs to fill by K splits
+        return v && *v ? std::atoi(v) : 75;
+    }();
+    const int64_t want = std::max<int64_t>(1, (split_pct * cus / 100 + nblk - 1) / nblk);
     int64_t kchunks = ((p.chunks + want - 1) / want + kGrain - 1) / kGrain * kGrain;
     kchunks = std::min<int64_t>(kchunks, kMaxChunks);
     int64_t splits = (p.chunks + kchunks - 1) / kchunks;
