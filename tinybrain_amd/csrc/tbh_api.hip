@@ -631,12 +631,14 @@ static tbh_status matmul_enqueue(const tbh_weight *w, const float *x, int64_t M,
                                  hipStream_t s) {
     if (!weight_arrays_ok(*w))
         return set_error(TBH_E_INVALID, "weight device arrays are inconsistent with its layout");
-    // 5..8 rows of x per launch on the matrix cores when the weight allows
-    // it (measured: at M = 8 half the time of two 4-row VALU launches; at
-    // M <= 4 the VALU kernels are as fast or faster).  TBH_SGEMV_MIN_ROWS
-    // moves the threshold (2..9; 9 turns the MFMA path off).
+    // 2..8 rows of x per launch on the matrix cores when the weight allows
+    // it: from 5 rows on (at M = 8 under half the time of two 4-row VALU
+    // launches), and from 4 rows on for tall weights (N >= 16384: 12.9 against
+    // 16.7 us at 32000 x 2048); below that the VALU kernels are as fast or
+    // faster.  TBH_SGEMV_MIN_ROWS sets one threshold for every shape (2..9;
+    // 9 turns the MFMA path off).
     const char *min_env = std::getenv("TBH_SGEMV_MIN_ROWS");
-    const int64_t sg_min = min_env && *min_env ? std::max(2, std::atoi(min_env)) : 5;
+    const int64_t sg_min = min_env && *min_env ? std::max(2, std::atoi(min_env)) : (w->N >= 16384 ? 4 : 5);
     const bool sg = M >= sg_min && sgemv_supported(*w);
     const int64_t rows = w->mfma_tiles || sg ? 8 : gemv_max_rows(*w);
     for (int64_t m0 = 0; m0 < M;) {

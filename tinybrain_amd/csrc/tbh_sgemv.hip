@@ -117,7 +117,7 @@ __device__ __forceinline__ void transpose4(uint32_t (&v)[4]) {
     v[3] = d[1];
 }
 
-template <int M, int NS>
+template <int M, int NS, int D>
 __global__ __launch_bounds__(512) void sgemv_int4(const SParams p) {
     constexpr int R2 = 2 * M;                 // A rows in use
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -134,8 +134,7 @@ __global__ __launch_bounds__(512) void sgemv_int4(const SParams p) {
     const int row0 = nb * kRows + wave * 16;
     const int row = min(row0 + n, p.Np - 1);  // rows past Np re-read the last row (never stored)
 
-    // ---- 1. x loads (unit u = (m, chunk, float4 q), zero beyond K), issued
-    // before the weight loads so that waiting for x leaves those in flight
+    // ---- 1. x loads (unit u = (m, chunk, float4 q), zero beyond K)
     constexpr int KC = kStepChunks * NS;     // chunks of this block (= p.kchunks)
     constexpr int units = M * KC * 8;
     float4 xv[kXUnits];
@@ -149,23 +148,7 @@ __global__ __launch_bounds__(512) void sgemv_int4(const SParams p) {
         xv[i] = float4{in ? t.x : 0.f, in ? t.y : 0.f, in ? t.z : 0.f, in ? t.w : 0.f};
     }
 
-    // ---- 2. every weight and scale load of the wave: lane (n, r) takes
-    // chunk cb + 4 t + r of row n for step t.  Chunks past the row re-read
-    // its last chunk and meet x = 0.
-    const uint8_t *wrow = p.data + (int64_t)row * p.row_bytes;
-    const float *srow = p.scales + (int64_t)(row >> 2) * p.G * 4 + (row & 3);
-    __builtin_amdgcn_sched_barrier(0);     // x loads first
-    u32x4 wr[NS];
-    float sr[NS];
-#pragma unroll
-    for (int t = 0; t < NS; ++t) {
-        const int c = min(cb + kStepChunks * t + g, p.chunks - 1);
-        wr[t] = __builtin_nontemporal_load((const u32x4 *)(wrow + 16 * c));
-        sr[t] = srow[4 * (c >> p.cpg_shift)];
-    }
-    __builtin_amdgcn_sched_barrier(0);
-
-    // ---- 3. x fragments: per-row exponent from the block's max |x[m]|
+    // ---- 2. x fragments: per-row exponent from the block's max |x[m]|
     // (each thread's units, then its wave by DPP, then the eight waves)
     float mx[M];
 #pragma unroll
@@ -226,6 +209,23 @@ __global__ __launch_bounds__(512) void sgemv_int4(const SParams p) {
     }
     lds_barrier();
 
+    // ---- 3. weight and scale loads, D steps ahead of their use: lane (n, r)
+    // takes chunk cb + 4 t + r of row n for step t.  Chunks past the row
+    // re-read its last chunk and meet x = 0.  Issued after x is staged: a
+    // wave that issues every load of its range at once stalls at the issue
+    // (each load touches 16 rows' cache lines) and cannot compute meanwhile.
+    const uint8_t *wrow = p.data + (int64_t)row * p.row_bytes;
+    const float *srow = p.scales + (int64_t)(row >> 2) * p.G * 4 + (row & 3);
+    u32x4 wr[D];
+    float sr[D];
+    auto load_step = [&](int t) {
+        const int c = min(cb + kStepChunks * t + g, p.chunks - 1);
+        wr[t % D] = __builtin_nontemporal_load((const u32x4 *)(wrow + 16 * c));
+        sr[t % D] = srow[4 * (c >> p.cpg_shift)];
+    };
+#pragma unroll
+    for (int t = 0; t < D && t < NS; ++t) load_step(t);
+
     // ---- 4. per step: transpose, then per chunk j unpack, MFMA, scale
     const uint32_t kMagic = opaque(0x64006400u), kLo = opaque(0x000F000Fu), kHi = opaque(0x00F000F0u);
     const h2 c1 = splat(-1032.0f), c16 = splat(-1152.0f);
@@ -235,9 +235,10 @@ __global__ __launch_bounds__(512) void sgemv_int4(const SParams p) {
 #pragma unroll
     for (int t = 0; t < NS; ++t) {
         // lane (n, g) <- word g of chunks c .. c + 3, and their 4 scales
-        uint32_t bw[4] = {wr[t][0], wr[t][1], wr[t][2], wr[t][3]};
+        uint32_t bw[4] = {wr[t % D][0], wr[t % D][1], wr[t % D][2], wr[t % D][3]};
         transpose4(bw);
-        const uint32_t su = __builtin_bit_cast(uint32_t, sr[t]);
+        const uint32_t su = __builtin_bit_cast(uint32_t, sr[t % D]);
+        if (t + D < NS) load_step(t + D);   // refill the slot just read
         uint32_t sv[4] = {su, su, su, su};
         transpose4(sv);
         const int cl0 = kStepChunks * t;
@@ -282,7 +283,13 @@ __global__ __launch_bounds__(256) void sgemv_split_sum(const float *part, int32_
 
 template <int M, int NS>
 hipError_t launch_mn(const SParams &p, unsigned blocks, size_t lds, hipStream_t s) {
-    hipLaunchKernelGGL((sgemv_int4<M, NS>), dim3(blocks), dim3(512), lds, s, p);
+    static const int depth = [] {
+        const char *v = std::getenv("TBH_SGEMV_DEPTH");
+        return v && *v ? std::atoi(v) : 2;   // measured best of 2, 4, 8
+    }();
+    if (depth >= 8) hipLaunchKernelGGL((sgemv_int4<M, NS, 8>), dim3(blocks), dim3(512), lds, s, p);
+    else if (depth <= 2) hipLaunchKernelGGL((sgemv_int4<M, NS, 2>), dim3(blocks), dim3(512), lds, s, p);
+    else hipLaunchKernelGGL((sgemv_int4<M, NS, 4>), dim3(blocks), dim3(512), lds, s, p);
     return hipGetLastError();
 }
 
