@@ -28,10 +28,11 @@
 // rows) together with that chunk's scale; a 4 x 4 transpose of 32-bit words
 // across the wave's four 16-lane rows (v_permlane32_swap, v_permlane16_swap)
 // then gives lane (n, kb) word kb of chunks c .. c + 3 -- one B operand per
-// MFMA -- and all four scales.  Every weight load of a wave (at most 64
-// chunks of its 16 rows) is issued at kernel start, after the x loads; the
-// x fragments of the block's K range are built in LDS meanwhile and shared
-// by the block's eight waves.  Small N is split along K over blocks; a
+// MFMA -- and all four scales.  The x fragments of the block's K range are
+// built in LDS first and shared by the block's eight waves; the weight loads
+// then run two steps ahead of the MFMAs (a wave that issues all of its loads
+// at once sits at the issue until most of them are accepted, then computes
+// every step after the data has arrived).  Small N is split along K over blocks; a
 // second kernel adds the splits in split order (deterministic).
 #include <cmath>
 #include <cstdlib>
