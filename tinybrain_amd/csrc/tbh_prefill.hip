@@ -288,16 +288,28 @@ __global__ __launch_bounds__(256) void gemm_bf16(const PParams p) {
 }
 
 // y = sum over splits of the partial tiles, in split order (deterministic).
+// The partials of up to kSumBatch splits are loaded together before they are
+// added (clamped addresses, selected afterwards), so a sum costs one memory
+// round trip per kSumBatch splits instead of one per split.
+constexpr int kSumBatch = 8;
+
 __global__ __launch_bounds__(256) void split_sum4(const float4 *__restrict__ part, int64_t stride4, int splits,
                                                   float4 *__restrict__ y, int64_t n4) {
     for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256) {
         float4 v = part[i];
-        for (int z = 1; z < splits; ++z) {
-            const float4 u = part[z * stride4 + i];
-            v.x += u.x;
-            v.y += u.y;
-            v.z += u.z;
-            v.w += u.w;
+        for (int z0 = 1; z0 < splits; z0 += kSumBatch) {
+            float4 u[kSumBatch];
+#pragma unroll
+            for (int j = 0; j < kSumBatch; ++j) u[j] = part[min(z0 + j, splits - 1) * stride4 + i];
+#pragma unroll
+            for (int j = 0; j < kSumBatch; ++j) {
+                if (z0 + j < splits) {
+                    v.x += u[j].x;
+                    v.y += u[j].y;
+                    v.z += u[j].z;
+                    v.w += u[j].w;
+                }
+            }
         }
         y[i] = v;
     }
@@ -307,7 +319,14 @@ __global__ __launch_bounds__(256) void split_sum(const float *__restrict__ part,
                                                  float *__restrict__ y, int64_t n) {
     for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
         float v = part[i];
-        for (int z = 1; z < splits; ++z) v += part[z * stride + i];
+        for (int z0 = 1; z0 < splits; z0 += kSumBatch) {
+            float u[kSumBatch];
+#pragma unroll
+            for (int j = 0; j < kSumBatch; ++j) u[j] = part[min(z0 + j, splits - 1) * stride + i];
+#pragma unroll
+            for (int j = 0; j < kSumBatch; ++j)
+                if (z0 + j < splits) v += u[j];
+        }
         y[i] = v;
     }
 }

@@ -271,14 +271,25 @@ __global__ __launch_bounds__(512) void sgemv_int4(const SParams p) {
     }
 }
 
-// y[m][n] = sum over splits s = 0, 1, ... of part[s][m][n], in that order.
+// y[m][n] = sum over splits s = 0, 1, ... of part[s][m][n], in that order;
+// up to kSumBatch partials are loaded together before they are added, so a
+// sum costs one memory round trip per kSumBatch splits.
+constexpr int kSumBatch = 8;
+
 __global__ __launch_bounds__(256) void sgemv_split_sum(const float *part, int32_t splits, int32_t M, int32_t N,
                                                        float *y, int64_t ldy) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= (int64_t)M * N) return;
-    const int64_t m = i / N, n = i % N;
+    const int64_t m = i / N, n = i % N, mn = (int64_t)M * N;
     float s = 0.0f;
-    for (int k = 0; k < splits; ++k) s += part[(int64_t)k * M * N + i];
+    for (int k0 = 0; k0 < splits; k0 += kSumBatch) {
+        float u[kSumBatch];
+#pragma unroll
+        for (int j = 0; j < kSumBatch; ++j) u[j] = part[(int64_t)min(k0 + j, splits - 1) * mn + i];
+#pragma unroll
+        for (int j = 0; j < kSumBatch; ++j)
+            if (k0 + j < splits) s += u[j];
+    }
     y[m * ldy + n] = s;
 }
 
