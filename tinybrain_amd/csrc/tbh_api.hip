@@ -115,14 +115,15 @@ tbh_status tbh_device_open(int32_t ordinal, tbh_device **out) {
 
 tbh_status tbh_device_close(tbh_device *dev) {
     if (!dev) return TBH_OK;
-    use_device(dev->ordinal);
-    if (dev->stream) hipStreamSynchronize(dev->stream);
-    if (dev->stage) hipFree(dev->stage);
+    // teardown: statuses are not actionable here, the handle goes away regardless
+    (void)use_device(dev->ordinal);
+    if (dev->stream) (void)hipStreamSynchronize(dev->stream);
+    if (dev->stage) (void)hipFree(dev->stage);
     for (auto &ws : dev->workspaces) {
-        hipStreamSynchronize(ws.stream);
-        hipFree(ws.ptr);
+        (void)hipStreamSynchronize(ws.stream);
+        (void)hipFree(ws.ptr);
     }
-    if (dev->stream) hipStreamDestroy(dev->stream);
+    if (dev->stream) (void)hipStreamDestroy(dev->stream);
     delete dev;
     return TBH_OK;
 }
@@ -353,14 +354,12 @@ hipError_t upload(T **dst, const T *src, size_t count, int64_t &bytes, int64_t &
     return hipMemcpy(*dst, src, count * sizeof(T), hipMemcpyHostToDevice);
 }
 
+// Statuses of the frees are not actionable: the weight goes away regardless.
 void free_weight(tbh_weight *w) {
     if (!w) return;
-    hipFree(w->data);
-    hipFree(w->scales);
-    hipFree(w->zp);
-    hipFree(w->raw);
-    hipFree(w->raw_scales);
-    hipFree(w->raw_zp);
+    for (void *p : {(void *)w->data, (void *)w->scales, (void *)w->zp, (void *)w->raw, (void *)w->raw_scales,
+                    (void *)w->raw_zp})
+        (void)hipFree(p);
     delete w;
 }
 
@@ -686,7 +685,7 @@ tbh_status tbh_matmul(tbh_device *dev, const float *x, int64_t M, int64_t K, con
     const size_t xb = (size_t)(M * K) * sizeof(float), yb = (size_t)(M * w->N) * sizeof(float);
     const size_t need = ((xb + 255) & ~size_t(255)) + yb;
     if (dev->stage_bytes < need) {
-        hipFree(dev->stage);
+        (void)hipFree(dev->stage);   // replaced below; a failed free leaves nothing to undo
         dev->stage = nullptr;
         dev->stage_bytes = 0;
         TBH_HIP(hipMalloc(&dev->stage, need), "tbh_matmul: staging buffer");
@@ -753,7 +752,8 @@ tbh_status tbh_dequantize(tbh_device *dev, const tbh_weight *w, float *out) {
     hipError_t e = launch_dequant(*w, d, dev->stream);
     if (e == hipSuccess) e = hipMemcpyAsync(out, d, bytes, hipMemcpyDeviceToHost, dev->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(dev->stream);
-    hipFree(d);
+    const hipError_t ef = hipFree(d);
+    if (e == hipSuccess) e = ef;
     if (e != hipSuccess) return hip_error(e, "tbh_dequantize");
     return TBH_OK;
 }

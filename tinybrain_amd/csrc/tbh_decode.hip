@@ -74,12 +74,6 @@ constexpr int kMaxHd = 128;
 constexpr int kSplit = 64;   // cache positions one attention block covers
 constexpr int kGroup = 8;    // query heads (of one KV head) one block serves
 
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 // sin and cos of a RoPE angle formed in fp32 as the reference forms it
 // (Float(pos) * theta, ModelRunner.swift:480-486).  The angle is reduced by
 // 2 pi in double precision first, so sincosf only sees |r| <= pi and never
@@ -90,9 +84,6 @@ __device__ __forceinline__ void rope_sincos(float ang, float *sn, float *cs) {
     const double k = rint(a * 0.15915494309189535);  // 1 / (2 pi)
     sincosf((float)fma(-k, 6.283185307179586, a), sn, cs);
 }
-
-__device__ __forceinline__ float wave_max(float v) { return wave::max(v); }
-__device__ __forceinline__ float wave_sum(float v) { return wave::sum(v); }
 
 // Orders a wave's LDS writes before its later LDS reads by other lanes of
 // the same wave (no block barrier: the waves of a block are independent).

@@ -601,14 +601,6 @@ __global__ __launch_bounds__(256) void attention_group(const GrpArgs g) {
     }
 }
 
-// LDS-only block barrier: orders LDS accesses without waiting for the
-// global loads still in flight (a full __syncthreads waits for them).
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 // Orders a wave's LDS writes before later LDS reads by other lanes of the
 // same wave (the waves of attention_wave never wait for each other).
 __device__ __forceinline__ void wave_lds_fence() {
@@ -935,7 +927,7 @@ hipError_t launch_attention_rows(const AttnArgs &a, hipStream_t s) {
 // Grows the device's staging buffer (callers hold dev->mu).
 tbh_status ensure_stage(tbh_device *dev, size_t need) {
     if (dev->stage_bytes >= need) return TBH_OK;
-    hipFree(dev->stage);
+    (void)hipFree(dev->stage);   // replaced below; a failed free leaves nothing to undo
     dev->stage = nullptr;
     dev->stage_bytes = 0;
     hipError_t e = hipMalloc(&dev->stage, need);
