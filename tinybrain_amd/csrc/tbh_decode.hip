@@ -48,9 +48,10 @@ struct tbh_decoder {
     float *kcache = nullptr;     // [layers][max_seq][kv_dim]
     float *vcache = nullptr;
     float *h = nullptr, *qkv = nullptr, *ctx = nullptr, *gu = nullptr, *logits = nullptr;
-    float *attn_part = nullptr;  // attention split partials (one layer at a time)
+    float *attn_o = nullptr;     // attention range partials (one layer at a time):
+    float2 *attn_ml = nullptr;   //   context sums [splits][hidden], (m, l) [splits][heads]
     float *rope_theta = nullptr; // [head_dim / 2] RoPE frequencies
-    int32_t attn_hchunks = 1, attn_splits = 1;
+    int32_t attn_splits = 1;
     int32_t *pos = nullptr;      // [0] position, [1] overflow flag
     std::vector<void *> allocs;
 };
@@ -62,17 +63,17 @@ struct AttnParams {
     const float *qkv;
     float *kcache, *vcache;  // this layer
     float *ctx;
-    float *part;             // [units][splits][2 * kGroup + kGroup * hd] split partials
+    float *part_o;           // [splits][hidden]: range context sums, heads in ctx order
+    float2 *part_ml;         // [splits][nh]: range max score m and sum l of exp(score - m)
     const float *theta;      // [hd / 2]: base^(-2i / hd), fp32
     int32_t *pos;            // [0] position, [1] overflow flag
     int32_t nh, nkv, hd, kvd, hidden, max_seq;
-    int32_t rep, hchunks, splits;  // units = nkv * hchunks blocks per split
+    int32_t rep, splits;
     float rope_base, scale;
 };
 
 constexpr int kMaxHd = 128;
 constexpr int kSplit = 64;   // cache positions one attention block covers
-constexpr int kGroup = 8;    // query heads (of one KV head) one block serves
 
 // sin and cos of a RoPE angle formed in fp32 as the reference forms it
 // (Float(pos) * theta, ModelRunner.swift:480-486).  The angle is reduced by
@@ -243,12 +244,7 @@ __global__ __launch_bounds__(256) void attention_split(const AttnParams a) {
     red[w][lane] = acc;
     wave_lds_fence();
 
-    const int unit = kvh * a.hchunks + hg / kGroup, hs = hg % kGroup;
-    float *part = a.part + ((int64_t)unit * a.splits + split) * (2 * kGroup + kGroup * HD);
-    if (lane == 0) {
-        part[hs] = m;
-        part[kGroup + hs] = l;
-    }
+    if (lane == 0) a.part_ml[split * a.nh + head] = float2{m, l};
     if (lane < HD4) {
         float4 o = red[w][lane];
 #pragma unroll
@@ -259,7 +255,7 @@ __global__ __launch_bounds__(256) void attention_split(const AttnParams a) {
             o.z += v.z;
             o.w += v.w;
         }
-        *(float4 *)&part[2 * kGroup + hs * HD + 4 * lane] = o;
+        *(float4 *)&a.part_o[(int64_t)split * a.hidden + head * HD + 4 * lane] = o;
         // append the new k and v (the group's first head, range holding pos);
         // the row-pos values this launch loaded are never used
         if (hg == 0 && pos < c0 + kSplit) {
@@ -271,7 +267,7 @@ __global__ __launch_bounds__(256) void attention_split(const AttnParams a) {
 
 // ctx of head h = sum over splits of e^(m_s - M) o_s / sum of e^(m_s - M) l_s
 // with M = max m_s (the softmax of :545-551 assembled from the ranges).  One
-// wave per (unit, head), no block barriers: lane (sg, d4) loads the partials
+// wave per head, no block barriers: lane (sg, d4) loads the partials
 // of splits sg, sg + 64 / (hd / 4), ... (up to kMergeLoads of them) together
 // with the position, so up to 32 ranges (2048 positions at head_dim 64)
 // cost one memory round trip; splits past pos are masked out afterwards.
@@ -281,38 +277,35 @@ constexpr int kMergeLoads = 8;
 template <int HD>
 __global__ __launch_bounds__(64) void attention_merge(const AttnParams a) {
     constexpr int HD4 = HD / 4, NSG = 64 / HD4;
-    constexpr int64_t kStride = 2 * kGroup + kGroup * HD;
     __shared__ float4 red[64];
     const int lane = threadIdx.x;
-    const int unit = blockIdx.x / kGroup, h = blockIdx.x % kGroup;
-    const int hc = unit % a.hchunks, kvh = unit / a.hchunks;
-    if (h >= a.rep - hc * kGroup) return;
-    const float *pb = a.part + (int64_t)unit * a.splits * kStride;
+    const int head = blockIdx.x;
     const int sg = lane / HD4, d4 = lane % HD4;
     const bool slane = sg < NSG;
+    const float *po = a.part_o + head * HD + 4 * min(d4, HD4 - 1);
+    const float2 *pml = a.part_ml + head;
     const int pos = a.pos[0];
-    float mv[kMergeLoads], lv[kMergeLoads];
+    float2 mlv[kMergeLoads];
     float4 ov[kMergeLoads];
 #pragma unroll
     for (int j = 0; j < kMergeLoads; ++j) {
         const int sp = min(sg + NSG * j, a.splits - 1);
-        mv[j] = pb[sp * kStride + h];
-        lv[j] = pb[sp * kStride + kGroup + h];
-        ov[j] = *(const float4 *)(pb + sp * kStride + 2 * kGroup + h * HD + 4 * min(d4, HD4 - 1));
+        mlv[j] = pml[sp * a.nh];
+        ov[j] = *(const float4 *)(po + (int64_t)sp * a.hidden);
     }
     if (pos < 0 || pos >= a.max_seq) return;
     const int ns = pos / kSplit + 1;
     float mloc = -INFINITY;
 #pragma unroll
     for (int j = 0; j < kMergeLoads; ++j)
-        if (slane && sg + NSG * j < ns) mloc = fmaxf(mloc, mv[j]);
-    for (int sp = sg + NSG * kMergeLoads; slane && sp < ns; sp += NSG) mloc = fmaxf(mloc, pb[sp * kStride + h]);
+        if (slane && sg + NSG * j < ns) mloc = fmaxf(mloc, mlv[j].x);
+    for (int sp = sg + NSG * kMergeLoads; slane && sp < ns; sp += NSG) mloc = fmaxf(mloc, pml[sp * a.nh].x);
     const float M = wave::max(mloc);
     float L = 0.0f;
     float4 o = float4{0.f, 0.f, 0.f, 0.f};
-    auto add = [&](float m, float l, float4 v) {
-        const float e = expf(m - M);
-        if (d4 == 0) L += e * l;   // one lane per split counts its sum
+    auto add = [&](float2 ml, float4 v) {
+        const float e = expf(ml.x - M);
+        if (d4 == 0) L += e * ml.y;   // one lane per split counts its sum
         o.x += e * v.x;
         o.y += e * v.y;
         o.z += e * v.z;
@@ -320,10 +313,9 @@ __global__ __launch_bounds__(64) void attention_merge(const AttnParams a) {
     };
 #pragma unroll
     for (int j = 0; j < kMergeLoads; ++j)
-        if (slane && sg + NSG * j < ns) add(mv[j], lv[j], ov[j]);
+        if (slane && sg + NSG * j < ns) add(mlv[j], ov[j]);
     for (int sp = sg + NSG * kMergeLoads; slane && sp < ns; sp += NSG)
-        add(pb[sp * kStride + h], pb[sp * kStride + kGroup + h],
-            *(const float4 *)(pb + sp * kStride + 2 * kGroup + h * HD + 4 * d4));
+        add(pml[sp * a.nh], *(const float4 *)(po + (int64_t)sp * a.hidden));
     L = wave::sum(L);
     red[lane] = o;
     wave_lds_fence();
@@ -338,16 +330,15 @@ __global__ __launch_bounds__(64) void attention_merge(const AttnParams a) {
             r.w += v.w;
         }
         const float inv = 1.0f / L;
-        const int head = kvh * a.rep + hc * kGroup + h;
         *(float4 *)&a.ctx[(int64_t)head * HD + 4 * lane] = float4{r.x * inv, r.y * inv, r.z * inv, r.w * inv};
     }
 }
 
 template <int HD>
 void launch_attention_hd(const AttnParams &ap, hipStream_t s) {
-    const int units = ap.nkv * ap.hchunks, nquad = (ap.rep + 3) / 4;
+    const int nquad = (ap.rep + 3) / 4;
     hipLaunchKernelGGL(attention_split<HD>, dim3((unsigned)(ap.nkv * nquad * ap.splits)), dim3(256), 0, s, ap);
-    hipLaunchKernelGGL(attention_merge<HD>, dim3((unsigned)(units * kGroup)), dim3(64), 0, s, ap);
+    hipLaunchKernelGGL(attention_merge<HD>, dim3((unsigned)ap.nh), dim3(64), 0, s, ap);
 }
 
 void launch_attention(const AttnParams &ap, hipStream_t s) {
@@ -602,11 +593,9 @@ tbh_status tbh_decoder_create(tbh_device *dev, const tbh_decoder_config *cfg, co
     if ((st = dmalloc(d.get(), &d->gu, 2 * (size_t)c.intermediate)) != TBH_OK) return st;
     if ((st = dmalloc(d.get(), &d->logits, (size_t)c.vocab)) != TBH_OK) return st;
     if ((st = dmalloc(d.get(), &d->pos, 2)) != TBH_OK) return st;
-    const int32_t rep = c.num_heads / c.num_kv_heads;
-    d->attn_hchunks = (rep + kGroup - 1) / kGroup;
     d->attn_splits = (c.max_seq + kSplit - 1) / kSplit;
-    const size_t part = (size_t)c.num_kv_heads * d->attn_hchunks * d->attn_splits * (2 * kGroup + kGroup * hd);
-    if ((st = dmalloc(d.get(), &d->attn_part, part)) != TBH_OK) return st;
+    if ((st = dmalloc(d.get(), &d->attn_o, (size_t)d->attn_splits * H)) != TBH_OK) return st;
+    if ((st = dmalloc(d.get(), &d->attn_ml, (size_t)d->attn_splits * c.num_heads)) != TBH_OK) return st;
     // RoPE frequencies theta_i = base^(-2i / hd) in fp32 (ModelRunner.swift:476-479)
     std::vector<float> theta((size_t)hd / 2);
     for (int32_t i = 0; i < hd / 2; ++i) theta[(size_t)i] = std::pow(c.rope_base, -((float)(2 * i) / (float)hd));
@@ -718,32 +707,32 @@ tbh_status tbh_decoder_step_device(tbh_decoder *d, int32_t token, float *logits,
     ap.hidden = c.hidden;
     ap.max_seq = c.max_seq;
     ap.rope_base = c.rope_base;
-    ap.part = d->attn_part;
+    ap.part_o = d->attn_o;
+    ap.part_ml = d->attn_ml;
     ap.theta = d->rope_theta;
     ap.rep = c.num_heads / c.num_kv_heads;
-    ap.hchunks = d->attn_hchunks;
     ap.splits = d->attn_splits;
     ap.scale = 1.0f / std::sqrt((float)d->head_dim);
     hipError_t e = hipSuccess;
     for (int32_t l = 0; l < c.num_layers && e == hipSuccess; ++l) {
         const auto &L = d->layers[(size_t)l];
         const float *g_in = d->norms + (2 * (size_t)l) * H, *g_post = g_in + H;
-        e = launch_gemv_fused(*L.qkv, FusedGemvArgs{d->h, nullptr, g_in, c.rms_eps, d->qkv, 1, 0}, s);
+        e = launch_gemv_fused(*L.qkv, FusedGemvArgs{d->h, g_in, c.rms_eps, d->qkv, PRO_RMSNORM, EPI_STORE}, s);
         if (e != hipSuccess) break;
         ap.kcache = d->kcache + (size_t)l * c.max_seq * d->kv_dim;
         ap.vcache = d->vcache + (size_t)l * c.max_seq * d->kv_dim;
         launch_attention(ap, s);
-        e = launch_gemv_fused(*L.o, FusedGemvArgs{d->ctx, nullptr, nullptr, 0.0f, d->h, 0, 1}, s);
+        e = launch_gemv_fused(*L.o, FusedGemvArgs{d->ctx, nullptr, 0.0f, d->h, PRO_NONE, EPI_ACCUMULATE}, s);
         if (e != hipSuccess) break;
         // gate and up rows interleaved: the epilogue writes silu(gate) * up
-        e = launch_gemv_fused(*L.gu, FusedGemvArgs{d->h, nullptr, g_post, c.rms_eps, d->gu, 1, 2}, s);
+        e = launch_gemv_fused(*L.gu, FusedGemvArgs{d->h, g_post, c.rms_eps, d->gu, PRO_RMSNORM, EPI_SILU_PAIR}, s);
         if (e != hipSuccess) break;
-        e = launch_gemv_fused(*L.down, FusedGemvArgs{d->gu, nullptr, nullptr, 0.0f, d->h, 0, 1}, s);
+        e = launch_gemv_fused(*L.down, FusedGemvArgs{d->gu, nullptr, 0.0f, d->h, PRO_NONE, EPI_ACCUMULATE}, s);
     }
     if (e == hipSuccess)
         e = launch_gemv_fused(*d->lm_head,
-                              FusedGemvArgs{d->h, nullptr, d->norms + 2 * (size_t)c.num_layers * H, c.rms_eps,
-                                            out, 1, 0},
+                              FusedGemvArgs{d->h, d->norms + 2 * (size_t)c.num_layers * H, c.rms_eps, out,
+                                            PRO_RMSNORM, EPI_STORE},
                               s);
     if (e == hipSuccess) {
         hipLaunchKernelGGL(advance_position, dim3(1), dim3(64), 0, s, d->pos);

@@ -60,15 +60,9 @@ struct KParams {
     int32_t rpn;     // rows per N-block (INT4 runtime layout)
     int32_t x_vec4;  // x rows are 16-byte aligned and K % 4 == 0
     // fused decode prologue / epilogue (gemv_burst with M = 1 only)
-    const float *x2;   // PRO_SILU_MUL: second input (x = silu(x) * x2)
     const float *g;    // PRO_RMSNORM: norm weight [K]
     float eps;         // PRO_RMSNORM: epsilon
 };
-
-enum { PRO_NONE = 0, PRO_RMSNORM = 1, PRO_SILU_MUL = 2 };
-// EPI_SILU_PAIR: rows 2j and 2j + 1 are a gate and an up row; the output is
-// y[j] = silu(r[2j]) * r[2j + 1] (ModelRunner.swift:449-451).
-enum { EPI_STORE = 0, EPI_ACCUMULATE = 1, EPI_SILU_PAIR = 2 };
 
 // expf at full precision (not the hardware exp2 approximation).
 __device__ __forceinline__ float __expf_exact(float v) { return expf(v); }
@@ -460,13 +454,12 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
             xv[m][r] = float4{in ? t.x : 0.f, in ? t.y : 0.f, in ? t.z : 0.f, in ? t.w : 0.f};
         }
     }
-    float4 av[XR];  // PRO_RMSNORM: g;  PRO_SILU_MUL: x2
-    if constexpr (PRO != PRO_NONE) {
-        const float *ar = PRO == PRO_RMSNORM ? p.g : p.x2;
+    float4 av[XR];  // PRO_RMSNORM: g
+    if constexpr (PRO == PRO_RMSNORM) {
 #pragma unroll
         for (int r = 0; r < XR; ++r) {
             const int k = 4 * (tid + 256 * r);
-            const float4 t = *(const float4 *)(ar + min(k, p.K - 4));
+            const float4 t = *(const float4 *)(p.g + min(k, p.K - 4));
             const bool in = k < p.K;
             av[r] = float4{in ? t.x : 0.f, in ? t.y : 0.f, in ? t.z : 0.f, in ? t.w : 0.f};
         }
@@ -514,9 +507,8 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
     // Nothing that consumes a load may be scheduled above this point.
     __builtin_amdgcn_sched_barrier(0);
 
-    // ---- fused prologue: x <- rmsnorm(x) * g or silu(x) * x2 (reference
-    // order of operations: Tensor.swift:1543-1556, :1135-1141;
-    // ModelRunner.swift:449-451)
+    // ---- fused prologue: x <- rmsnorm(x) * g (reference order of
+    // operations: Tensor.swift:1543-1556)
     if constexpr (PRO == PRO_RMSNORM) {
         float ss = 0.0f;
 #pragma unroll
@@ -535,14 +527,6 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
             xv[0][r].y = xv[0][r].y * inv * av[r].y;
             xv[0][r].z = xv[0][r].z * inv * av[r].z;
             xv[0][r].w = xv[0][r].w * inv * av[r].w;
-        }
-    } else if constexpr (PRO == PRO_SILU_MUL) {
-#pragma unroll
-        for (int r = 0; r < XR; ++r) {
-            xv[0][r].x = xv[0][r].x / (1.0f + __expf_exact(-xv[0][r].x)) * av[r].x;
-            xv[0][r].y = xv[0][r].y / (1.0f + __expf_exact(-xv[0][r].y)) * av[r].y;
-            xv[0][r].z = xv[0][r].z / (1.0f + __expf_exact(-xv[0][r].z)) * av[r].z;
-            xv[0][r].w = xv[0][r].w / (1.0f + __expf_exact(-xv[0][r].w)) * av[r].w;
         }
     }
 
@@ -760,8 +744,6 @@ template <int PREC>
 hipError_t burst_fused(int pro, int epi, int I, int U, const KParams &p, size_t lds, hipStream_t s) {
     if (pro == PRO_RMSNORM && epi == EPI_STORE) return burst_i<PREC, 1, PRO_RMSNORM, EPI_STORE>(I, U, p, lds, s);
     if (pro == PRO_NONE && epi == EPI_ACCUMULATE) return burst_i<PREC, 1, PRO_NONE, EPI_ACCUMULATE>(I, U, p, lds, s);
-    if (pro == PRO_SILU_MUL && epi == EPI_ACCUMULATE)
-        return burst_i<PREC, 1, PRO_SILU_MUL, EPI_ACCUMULATE>(I, U, p, lds, s);
     if (pro == PRO_RMSNORM && epi == EPI_SILU_PAIR)
         return burst_i<PREC, 1, PRO_RMSNORM, EPI_SILU_PAIR>(I, U, p, lds, s);
     return hipErrorInvalidValue;
@@ -801,7 +783,6 @@ KParams make_params(const tbh_weight &w, const GemvArgs &a) {
         if (p.cpg > 0 && p.cpg == (1 << sh)) p.cpg_shift = sh;
     p.rpn = w.rows_per_nblock;
     p.x_vec4 = (w.K % 4 == 0 && a.ldx % 4 == 0 && ((uintptr_t)a.x & 15) == 0) ? 1 : 0;
-    p.x2 = a.x;
     p.g = a.x;
     p.eps = 0.0f;
     return p;
@@ -827,7 +808,17 @@ bool burst_shape(const tbh_weight &w, const KParams &p, int M, int *I_out, int *
     const int64_t cus = std::max(1, w.dev->cu_count);
     // U * I <= 16 weight chunks per lane; M * U <= 32 values in the reduce
     int U = 1;
-    while (2 * U * I <= 16 && 2 * U * M <= 32 && w.Np / (2 * U) >= burst_wpc * cus) U *= 2;
+    if (M == 1) {
+        // one x row: four rows per wave once that still leaves >= 8 waves
+        // per CU, else two (measured on every decode shape of the 1.1B and
+        // 7B models and the four INT4 shapes: one row per wave is slower
+        // even on 2048-row matrices, eight or more rows per wave slower
+        // everywhere)
+        if (4 * I <= 16 && w.Np / 4 >= 8 * cus) U = 4;
+        else if (2 * I <= 16) U = 2;
+    } else {
+        while (2 * U * I <= 16 && 2 * U * M <= 32 && w.Np / (2 * U) >= burst_wpc * cus) U *= 2;
+    }
     if (u_force > 0 && u_force * I <= 16 && u_force * M <= 32 && (u_force & (u_force - 1)) == 0) U = u_force;
     *I_out = I;
     *U_out = U;
@@ -849,10 +840,9 @@ bool gemv_fused_supported(const tbh_weight &w) {
 hipError_t launch_gemv_fused(const tbh_weight &w, const FusedGemvArgs &f, hipStream_t s) {
     GemvArgs a{f.x, w.K, f.y, w.N, 1};
     KParams p = make_params(w, a);
-    p.x2 = f.x2 ? f.x2 : f.x;
     p.g = f.g ? f.g : f.x;
     p.eps = f.eps;
-    if ((f.x2 && ((uintptr_t)f.x2 & 15)) || (f.g && ((uintptr_t)f.g & 15))) return hipErrorInvalidValue;
+    if (f.g && ((uintptr_t)f.g & 15)) return hipErrorInvalidValue;
     int I, U;
     int64_t lds;
     if (!burst_shape(w, p, 1, &I, &U, &lds)) return hipErrorInvalidValue;

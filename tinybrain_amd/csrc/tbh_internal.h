@@ -124,14 +124,18 @@ hipError_t launch_gemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s);
 int64_t gemv_max_rows(const tbh_weight &w);
 
 // Fused decode GEMV (M = 1, tbh_gemv.hip): y = W . pro(x) (+ y).
-//   prologue 0: x as given; 1: rmsnorm(x) * g with epsilon eps
-//   (Tensor.swift:1543-1556); 2: silu(x) * x2 (Tensor.swift:1135-1141,
-//   ModelRunner.swift:449-451).  epilogue 0: store; 1: y += result
-//   (the residual adds, ModelRunner.swift:434, :457); 2: rows 2j, 2j + 1
-//   are a gate and an up row, y[j] = silu(r[2j]) * r[2j + 1] (:449-451).
+enum {
+    PRO_NONE = 0,     // x as given
+    PRO_RMSNORM = 1,  // rmsnorm(x) * g with epsilon eps (Tensor.swift:1543-1556)
+};
+enum {
+    EPI_STORE = 0,       // y = result
+    EPI_ACCUMULATE = 1,  // y += result (the residual adds, ModelRunner.swift:434, :457)
+    EPI_SILU_PAIR = 2,   // rows 2j, 2j + 1 are a gate and an up row:
+                         // y[j] = silu(r[2j]) * r[2j + 1] (:449-451)
+};
 struct FusedGemvArgs {
     const float *x;
-    const float *x2;
     const float *g;
     float eps;
     float *y;
