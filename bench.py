@@ -48,13 +48,21 @@ PREFILL = {}
 for _m in (64, 128, 512, 2048):
     PREFILL[f"prefill_int8_m{_m}"] = ("int8", 0, (5632, 2048), _m)
     PREFILL[f"prefill_int4_m{_m}"] = ("int4", 32, (2048, 5632), _m)
-# Decode (BASELINE configs[2] and [5]): one token of a LLaMA-shaped model on
+# Decode (BASELINE configs[2] and [4]): one token of a LLaMA-shaped model on
 # the GPU decode step.  name: (precision, group, config kwargs, context)
+CFG_7B = dict(num_layers=32, hidden=4096, num_heads=32, num_kv_heads=32, intermediate=11008, vocab=32000)
 DECODE = {
     "decode_1p1b_int8": ("int8", 0, dict(num_layers=22, hidden=2048, num_heads=32, num_kv_heads=4,
                                          intermediate=5632, vocab=32000), 512),
-    "decode_7b_int4": ("int4", 32, dict(num_layers=32, hidden=4096, num_heads=32, num_kv_heads=32,
-                                        intermediate=11008, vocab=32000), 512),
+    "decode_7b_int4": ("int4", 32, CFG_7B, 512),
+}
+# The per-token projection set of the 7B shape (batch
+# M in {1, 8}): every layer's q, k, v, o, gate, up and down GEMV and the LM
+# head, each with M rows of x, one step = one token for each of M sequences.
+# name: (precision, group, config kwargs, M)
+PROJ = {
+    "proj_7b_int4_m1": ("int4", 32, CFG_7B, 1),
+    "proj_7b_int4_m8": ("int4", 32, CFG_7B, 8),
 }
 # The other backend protocols (softmax, RMSNorm, SiLU/GELU, attention) at the
 # shapes either side of the GEMV in a 1.1B-shaped model: one launch per step
@@ -281,12 +289,13 @@ def decode_bytes(prec, gs, c, ctx):
     return b + c["num_layers"] * 2 * ctx * kv * 4
 
 
-def cpu_baseline_decode(prec, gs, c, qts, budget_s: float = 15.0):
+def cpu_baseline_decode(prec, gs, c, qts, budget_s: float = 15.0, M: int = 1):
     """Reference CPU path for one step: every projection is dequantize()
-    (single-threaded, fresh buffer) + sgemm on all host cores
+    (single-threaded, fresh buffer) + sgemm of M rows on all host cores
     (QuantizedTensor.swift:640-642).  Timed on one layer's seven projections
     and the LM head; a step is num_layers layers + the LM head (attention,
-    norms and activations, which the CPU path also runs, are left out)."""
+    norms and activations, which the CPU path also runs, are left out) and
+    yields M tokens."""
     import oracle as O
 
     threads = min(os.cpu_count() or 1, 16)
@@ -298,11 +307,11 @@ def cpu_baseline_decode(prec, gs, c, qts, budget_s: float = 15.0):
     t0 = time.perf_counter()
     while True:
         for (K, N), q in zip(layer, oq[:7]):
-            x = np.random.default_rng(K).normal(size=(1, K)).astype(np.float32)
+            x = np.random.default_rng(K).normal(size=(M, K)).astype(np.float32)
             t1 = time.perf_counter()
             O.matmul_quantized_cpu(x, q, threads=threads)
             t_layer += time.perf_counter() - t1
-        x = np.random.default_rng(7).normal(size=(1, lm[0])).astype(np.float32)
+        x = np.random.default_rng(7).normal(size=(M, lm[0])).astype(np.float32)
         t1 = time.perf_counter()
         O.matmul_quantized_cpu(x, oq[7], threads=threads)
         t_lm += time.perf_counter() - t1
@@ -311,11 +320,11 @@ def cpu_baseline_decode(prec, gs, c, qts, budget_s: float = 15.0):
             break
     step_s = (c["num_layers"] * t_layer + t_lm) / reps
     return {
-        "value": round(1.0 / step_s, 4),
+        "value": round(M / step_s, 4),
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{reps} pass(es) over one layer's 7 projections + the LM head, scaled to "
+        "sample": f"{reps} pass(es) over one layer's 7 projections + the LM head at M={M}, scaled to "
                   f"{c['num_layers']} layers; projections only",
         "ms_per_step": round(1e3 * step_s, 1),
     }
@@ -385,7 +394,7 @@ def run_decode(args, backend, T, torch):
             "weights": ("INT8 symmetric per output channel" if prec == "int8" else
                         "INT4 symmetric, group 32 along K (converter layout)") +
                        "; one random init per projection shape, a device copy per layer",
-            "batch": 1, "launches_per_step": 5 * c["num_layers"] + 3,
+            "batch": 1, "launches_per_step": 6 * c["num_layers"] + 3,
         },
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -399,6 +408,97 @@ def run_decode(args, backend, T, torch):
         out["cpu_baseline"] = cpu_baseline_decode(prec, gs, c, qts, args.cpu_budget)
     print(json.dumps(out), flush=True)
     dec.close()
+    backend.close()
+
+
+def run_proj(args, backend, T, torch):
+    """The 7B projection set at M rows: num_layers x (q, k, v, o, gate, up,
+    down) + the LM head through tbh_matmul_device, captured in one HIP
+    graph.  Every layer has its own device copy of its seven weights (one
+    random init per shape), so a step streams the whole model from HBM."""
+    prec, gs, c, M = PROJ[args.workload]
+    dev = torch.device("cuda", 0)
+    layer, lm = decode_shapes(c)
+    t_setup = time.perf_counter()
+    qts = [make_weight(prec, gs, N, K, seed=0x7B1A0040 + j) for j, (K, N) in enumerate(layer)]
+    qts.append(make_weight(prec, gs, lm[1], lm[0], seed=0x7B1A0050))
+    weights = [[T.DeviceWeight(backend, q) for q in qts[:7]] for _ in range(c["num_layers"])]
+    head = T.DeviceWeight(backend, qts[7])
+    setup_s = time.perf_counter() - t_setup
+    shapes = layer + [lm]
+    gen = torch.Generator(device=dev).manual_seed(3)
+    xs = {K: torch.randn((M, K), generator=gen, device=dev, dtype=torch.float32) for K, _ in shapes}
+    ys = {N: torch.empty((M, N), device=dev, dtype=torch.float32) for _, N in shapes}
+    cap = torch.cuda.Stream(dev)
+    cap.wait_stream(torch.cuda.current_stream(dev))
+
+    def step():
+        for ws in weights:
+            for (K, N), w in zip(layer, ws):
+                backend.matmul_device(xs[K], w, out=ys[N], stream=cap)
+        backend.matmul_device(xs[lm[0]], head, out=ys[lm[1]], stream=cap)
+
+    step()                                    # eager: sizes the split-K workspace of `cap`
+    torch.cuda.synchronize()
+    eager = {N: y.clone() for N, y in ys.items()}
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=cap):
+        step()
+    for _ in range(2):
+        for y in ys.values():
+            y.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        for N, y in ys.items():
+            if not torch.equal(y, eager[N]):
+                raise RuntimeError("graph replay differs from the eager launches")
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(cap):
+        for _ in range(args.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record(cap)
+        for _ in range(args.steps):
+            graph.replay()
+        e1.record(cap)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    step_us = e0.elapsed_time(e1) * 1e3 / args.steps
+    byts = c["num_layers"] * sum(alg_bytes(prec, gs, N, K, M) for K, N in layer) + \
+        alg_bytes(prec, gs, lm[1], lm[0], M)
+    achieved = byts / step_us / 1e3
+    out = {
+        "metric": f"7B projection-set tokens/s at batch M={M} (INT4 g32), 1 GPU",
+        "value": round(M * args.steps / wall, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(1e3 * wall / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": args.workload, **c, "M": M,
+            "weights": "INT4 symmetric, group 32 along K (converter layout); one random init per "
+                       "projection shape, a device copy per layer",
+            "step": "q, k, v, o, gate, up, down of every layer + LM head (no attention or norms)",
+            "launches_per_step": 7 * c["num_layers"] + 1,
+        },
+        "roofline": {
+            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "projection step (graph of all launches)", "kernel_us": round(step_us, 2),
+            "alg_bytes_per_launch": int(byts),
+        },
+        "setup_s": round(setup_s, 1),
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline_decode(prec, gs, c, qts, args.cpu_budget, M=M)
+    print(json.dumps(out), flush=True)
     backend.close()
 
 
@@ -540,7 +640,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="int4_g32_gemv_m1", choices=sorted(WORKLOADS) + sorted(PREFILL) + sorted(DECODE) + sorted(OPS))
+    ap.add_argument("--workload", default="int4_g32_gemv_m1",
+                    choices=sorted(WORKLOADS) + sorted(PREFILL) + sorted(DECODE) + sorted(PROJ) + sorted(OPS))
     ap.add_argument("--pool-gib", type=float, default=2.2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
@@ -563,6 +664,8 @@ def main():
         return run_prefill(args, backend, T, torch)
     if args.workload in DECODE:
         return run_decode(args, backend, T, torch)
+    if args.workload in PROJ:
+        return run_proj(args, backend, T, torch)
     if args.workload in OPS:
         return run_op(args, backend, T, torch)
     prec, gs, shapes, M = WORKLOADS[args.workload]

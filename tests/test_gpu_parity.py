@@ -143,10 +143,11 @@ def test_int4_baseline_config1(backend, K, N):
     _check(backend, _product(qt, (K, N), T.Layout.NK_FLAT), qt, Ms=(1, 4, 8))
 
 
-# Burst GEMV (M in {1, 2, 4}; M = 8 runs as two M = 4 launches; no zero
-# points, 16-byte aligned x, K % 4 == 0): one case
-# per chunk-iteration count I = ceil(chunks / 64) = 1..6 and per rows-per-wave
-# U = 1..16, which the launch picks from N and the CU count (256 on MI355X).
+# Burst GEMV (M in {1, 2, 4}; no zero points, 16-byte aligned x, K % 4 == 0):
+# one case per chunk-iteration count I = ceil(chunks / 64) = 1..6 and across
+# the rows per wave U the launch picks from N, M and the CU count (256 on
+# MI355X): 2 or 4 at M = 1, up to 16 at M = 2.  M = 8 runs on the matrix-core
+# kernel (INT4) or as two M = 4 launches (INT8).
 @pytest.mark.parametrize("prec,K,N", [
     ("int4", 2048, 40960),   # I=1, U=16
     ("int4", 2048, 20000),   # I=1, U=8
@@ -168,6 +169,14 @@ def test_burst_shapes(backend, prec, K, N):
         oq = _int4_nk(43 + K, K, N, 32)
         pq = _product(oq, (K, N), T.Layout.NK_FLAT)
     _check(backend, pq, oq, Ms=(1, 2, 4, 8), cpu_path=False)
+
+
+@pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 11008), (11008, 4096), (4096, 32000)])
+def test_int4_7b_projection_shapes(backend, K, N):
+    # the 7B projection set (q/k/v/o, gate/up, down, LM
+    # head), INT4 g32 along K, batch M in {1, 8}
+    qt = _int4_nk(0x7B1A0070 + K + N, K, N, 32)
+    _check(backend, _product(qt, (K, N), T.Layout.NK_FLAT), qt, Ms=(1, 8), cpu_path=False)
 
 
 @pytest.mark.parametrize("K,N,gs,path", [(256, 512, 32, "int4_ngroup"), (2048, 2048, 32, "int4_ngroup"),
