@@ -343,18 +343,23 @@ hipError_t launch_sgemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s) {
     while ((1 << p.cpg_shift) < w.chunks_per_group) ++p.cpg_shift;
     p.chunks = (int32_t)(w.Kp / kInt4ChunkElems);
 
-    // K split: enough blocks for about 3/4 of the CUs, each block a multiple
-    // of 16 chunks and at most 64 (its loads all in flight: NS <= 16 steps;
-    // its x fragments within LDS; its x units within kXUnits per thread).
+    // K split: none when the row blocks alone give 3/4 of the CUs a block;
+    // otherwise enough splits for about three blocks per CU (a wave keeps
+    // only two steps of loads in flight, so a small grid is latency-bound:
+    // the 7B projection set at M = 8 ran 10 % faster with three blocks per
+    // CU than with 3/4 of a block).  Each block covers a multiple of 16
+    // chunks and at most 64 (its loads all in flight: NS <= 16 steps; its x
+    // fragments within LDS; its x units within kXUnits per thread).
     constexpr int kGrain = 16, kMaxChunks = 64;
     static_assert(kMaxChunks * 8 * 8 <= 512 * kXUnits, "x units of M = 8 rows per thread");
     const int64_t nblk = (w.Np + kRows - 1) / kRows;
     const int64_t cus = std::max(1, w.dev->cu_count);
     static const int split_pct = [] {
         const char *v = std::getenv("TBH_SGEMV_SPLIT_PCT");   // percent of the CUs to fill by K splits
-        return v && *v ? std::atoi(v) : 75;
+        return v && *v ? std::atoi(v) : 300;
     }();
-    const int64_t want = std::max<int64_t>(1, (split_pct * cus / 100 + nblk - 1) / nblk);
+    const int64_t want =
+        4 * nblk >= 3 * cus ? 1 : std::max<int64_t>(1, (split_pct * cus / 100 + nblk - 1) / nblk);
     int64_t kchunks = ((p.chunks + want - 1) / want + kGrain - 1) / kGrain * kGrain;
     kchunks = std::min<int64_t>(kchunks, kMaxChunks);
     int64_t splits = (p.chunks + kchunks - 1) / kchunks;
