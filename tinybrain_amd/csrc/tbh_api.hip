@@ -636,11 +636,8 @@ static tbh_status matmul_enqueue(const tbh_weight *w, const float *x, int64_t M,
     // 16.7 us at 32000 x 2048); below that the VALU kernels are as fast or
     // faster.  TBH_SGEMV_MIN_ROWS sets one threshold for every shape (2..9;
     // 9 turns the MFMA path off).
-    static const int min_env = [] {
-        const char *v = std::getenv("TBH_SGEMV_MIN_ROWS");
-        return v && *v ? std::max(2, std::atoi(v)) : 0;
-    }();
-    const int64_t sg_min = min_env ? min_env : (w->N >= 16384 ? 4 : 5);
+    const char *min_env = std::getenv("TBH_SGEMV_MIN_ROWS");
+    const int64_t sg_min = min_env && *min_env ? std::max(2, std::atoi(min_env)) : (w->N >= 16384 ? 4 : 5);
     const bool sg = M >= sg_min && sgemv_supported(*w);
     const int64_t rows = w->mfma_tiles || sg ? 8 : gemv_max_rows(*w);
     for (int64_t m0 = 0; m0 < M;) {
