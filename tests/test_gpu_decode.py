@@ -102,6 +102,21 @@ def test_decode_long_context(backend, heads):
     dec.close()
 
 
+def test_decode_merge_beyond_one_load_round(backend):
+    # head_dim 128: the merge kernel loads 16 ranges (1024 positions) per
+    # head in its first round and loops over the rest; 1100 steps reach 18
+    # ranges, so every range past the 16th goes through that loop
+    cfg = T.DecoderConfig(**dict(SMALL, num_layers=1, num_heads=2, num_kv_heads=1, max_seq=1104))
+    dec, ref = _model(backend, cfg, "int8", seed=71)
+    rng = np.random.default_rng(71)
+    for i, tok in enumerate(rng.integers(0, cfg.vocab, size=1100)):
+        y = dec.step(int(tok))
+        r = ref.step(int(tok))
+        if i % 50 == 0 or i >= 1020:
+            assert _gated(y, r) <= GATE, (i, _gated(y, r))
+    dec.close()
+
+
 def test_decode_reset_is_deterministic(backend):
     cfg = T.DecoderConfig(**SMALL)
     dec, _ = _model(backend, cfg, "int8", seed=31)
