@@ -9,8 +9,8 @@
 // 1 KiB of contiguous HBM.
 //
 // Two schedules:
-//   * gemv_burst (M <= 2, no zero points, rows up to 64 * 6 chunks): one wave
-//     per U rows, every load of the wave issued at kernel start, so a launch
+//   * gemv_burst (M in {1, 2, 4}, no zero points, rows up to 64 * 6 chunks):
+//     one wave per U rows, every load of the wave issued at kernel start, so a launch
 //     puts the whole matrix's reads in flight at once and pays HBM latency
 //     about once -- the decode shapes are only 2-70 MB, a few microseconds
 //     of HBM time, so latency and ramp dominate otherwise;
