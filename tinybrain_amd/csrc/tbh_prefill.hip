@@ -397,13 +397,36 @@ hipError_t launch_split(const tbh_weight &w, PParams p, int64_t tiles, int bpc, 
 
 template <int PREC>
 hipError_t launch_prec(const tbh_weight &w, const PParams &p, hipStream_t s) {
-    // Largest tile that still gives every CU a block; below that, 64 x 64
-    // tiles split along K until there are two blocks per CU (a 64 x 64 block
-    // does little work per K step, so one per CU leaves its latency exposed).
     const int64_t cus = std::max(1, w.dev->cu_count);
     const int64_t t128 = ((p.Np + 127) / 128) * ((p.M + 127) / 128);
     const int64_t t64x128 = ((p.Np + 127) / 128) * ((p.M + 63) / 64);
     const int64_t t64 = ((p.Np + 63) / 64) * ((p.M + 63) / 64);
+    static const int force = [] {   // 1: 64 x 64, 2: 64 x 128, 3: 128 x 128 tiles
+        const char *v = std::getenv("TBH_PREFILL_TILE");
+        return v && *v ? std::atoi(v) : 0;
+    }();
+    if (force == 1) return launch_split<PREC, 64, 64>(w, p, t64, 2, s);
+    if (force == 2) return launch_split<PREC, 64, 128>(w, p, t64x128, 1, s);
+    if (force == 3) return launch_split<PREC, 128, 128>(w, p, t128, 1, s);
+    if (p.M >= 256) {
+        // The largest tile that still gives two blocks per CU without a K
+        // split; with none, 128 x 128 tiles split along K to a block per CU.
+        // A CU holding one block runs its K steps with nothing to overlap
+        // the global-load waits, dequantization and barriers of one wave
+        // per SIMD, while two blocks on a CU took 1.2x the time of one
+        // (timestamps inside the kernel).  Measured against the 64-row rule
+        // below: INT8 5632x2048 M = 512 35.1 -> 30.6 us (64 x 64), INT4
+        // 2048x5632 M = 512 52.2 -> 43.7 us (128 x 128, 4 splits), M = 2048
+        // 136 -> 118 us (64 x 128); INT8 M = 2048 stays 128 x 128.
+        if (t128 >= 2 * cus) return launch_split<PREC, 128, 128>(w, p, t128, 1, s);
+        if (t64x128 >= 2 * cus) return launch_split<PREC, 64, 128>(w, p, t64x128, 1, s);
+        if (t64 >= 2 * cus) return launch_split<PREC, 64, 64>(w, p, t64, 2, s);
+        return launch_split<PREC, 128, 128>(w, p, t128, 1, s);
+    }
+    // Fewer rows (HBM-bound): the largest tile that still gives every CU a
+    // block; below that, 64 x 64 tiles split along K until there are two
+    // blocks per CU (a 64 x 64 block does little work per K step, so one
+    // per CU leaves its latency exposed).
     if (t128 >= cus) return launch_split<PREC, 128, 128>(w, p, t128, 1, s);
     if (t64x128 >= cus) return launch_split<PREC, 64, 128>(w, p, t64x128, 1, s);
     return launch_split<PREC, 64, 64>(w, p, t64, 2, s);
