@@ -7,8 +7,9 @@
 // Tensor.swift:839-861) or as the MSL dequant kernels one output per thread
 // (Shaders/Dequant.metal:49-79, DequantINT4.metal:95-137).
 //
-// A 256-thread block owns a BM x BN output tile; its four waves own
-// (BM/2) x (BN/2) each, as TM x TN tiles of v_mfma_f32_16x16x32_bf16.  Per
+// A block of four or eight waves owns a BM x BN output tile; its waves, as
+// 2 x (waves / 2), own (BM/2) x (BN/(waves/2)) each, as TM x TN tiles of
+// v_mfma_f32_16x16x32_bf16 (eight waves: two per SIMD from one block).  Per
 // K step of 64 the block stages x (bf16, as given) and the dequantized weight
 // tile in LDS; global loads of step t+1 are in flight while step t's MFMAs
 // run.  Weight operands are exact:
@@ -73,17 +74,19 @@ __device__ __forceinline__ float ubyte(uint32_t w) {
     return (float)((w >> (8 * J)) & 0xFFu);
 }
 
-template <int PREC, int BM, int BN, bool ZP>
-__global__ __launch_bounds__(256) void gemm_bf16(const PParams p) {
+template <int PREC, int BM, int BN, bool ZP, int WV>
+__global__ __launch_bounds__(64 * WV) void gemm_bf16(const PParams p) {
+    constexpr int NT = 64 * WV;                   // threads; waves as 2 x (WV / 2)
+    constexpr int WC = WV / 2;
     constexpr int CE = PREC == 8 ? 16 : 32;       // elements per chunk
     constexpr int CPR = kBK / CE;                 // chunks per row per step
     constexpr int WCH = BN * CPR;                 // weight chunks per step
-    constexpr int WPT = (WCH + 255) / 256;        // per thread (last may idle)
+    constexpr int WPT = (WCH + NT - 1) / NT;      // per thread (last may idle)
     constexpr int XSEG = BM * (kBK / 8);          // 16-byte x segments per step
-    constexpr int XPT = XSEG / 256;
-    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int XPT = XSEG / NT;
+    constexpr int WM = BM / 2, WN = BN / WC;
     constexpr int TM = WM / 16, TN = WN / 16;
-    static_assert(XSEG % 256 == 0, "BM must be a multiple of 32");
+    static_assert(XSEG % NT == 0 && TN >= 1, "tile too small for the waves");
 
     // two LDS buffers: step t + 1 is staged while step t's MFMAs read
     __shared__ __attribute__((aligned(16))) uint16_t xs[2][BM * kLdsRow];
@@ -91,7 +94,7 @@ __global__ __launch_bounds__(256) void gemm_bf16(const PParams p) {
     __shared__ float ssc[2][PREC == 4 ? BN * CPR : 1];   // INT4: scale of each (row, K-slice)
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WC, wn = wave % WC;
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
     const int nsteps = (p.chunks * CE + kBK - 1) / kBK;
     // This block's K steps [t_begin, t_end); x past kend reads as zero, so
@@ -119,7 +122,7 @@ __global__ __launch_bounds__(256) void gemm_bf16(const PParams p) {
         const int k0 = t * kBK;
 #pragma unroll
         for (int j = 0; j < XPT; ++j) {
-            const int s = tid + 256 * j;
+            const int s = tid + NT * j;
             const int row = s / (kBK / 8), kq = s % (kBK / 8);
             const int m = min(m0 + row, p.M - 1), k = k0 + 8 * kq;
             // K % 8 == 0: a segment is all in or out.  Rows past M read row
@@ -129,7 +132,7 @@ __global__ __launch_bounds__(256) void gemm_bf16(const PParams p) {
         }
 #pragma unroll
         for (int j = 0; j < WPT; ++j) {
-            const int s = tid + 256 * j;
+            const int s = tid + NT * j;
             const int row = s / CPR, c = t * CPR + s % CPR;
             const int n = n0 + row;
             const bool in = s < WCH && n < p.Np && c < p.chunks;
@@ -151,13 +154,13 @@ __global__ __launch_bounds__(256) void gemm_bf16(const PParams p) {
     auto store_step = [&](int d, int bb) {
 #pragma unroll
         for (int j = 0; j < XPT; ++j) {
-            const int s = tid + 256 * j;
+            const int s = tid + NT * j;
             const int row = s / (kBK / 8), kq = s % (kBK / 8);
             *(u32x4 *)&xs[bb][row * kLdsRow + 8 * kq] = xin[d][j] ? xr[d][j] : u32x4{0, 0, 0, 0};
         }
 #pragma unroll
         for (int j = 0; j < WPT; ++j) {
-            const int s = tid + 256 * j;
+            const int s = tid + NT * j;
             if (s < WCH) {
                 const int row = s / CPR, cl = s % CPR;
                 uint16_t *dst = &ws[bb][row * kLdsRow + cl * CE];
@@ -333,11 +336,19 @@ __global__ __launch_bounds__(256) void split_sum(const float *__restrict__ part,
 
 template <int PREC, int BM, int BN>
 hipError_t launch_tile(const PParams &p, int splits, hipStream_t s) {
+    static const int waves = [] {   // 4 or 8 forces the waves per block
+        const char *v = std::getenv("TBH_PREFILL_WAVES");
+        return v && *v ? std::atoi(v) : 0;
+    }();
     const dim3 grid((unsigned)((p.Np + BN - 1) / BN), (unsigned)((p.M + BM - 1) / BM), (unsigned)splits);
-    if (p.zp)
-        hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, true>), grid, dim3(256), 0, s, p);
-    else
-        hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, false>), grid, dim3(256), 0, s, p);
+    const bool w8 = waves == 8 || (waves != 4 && BN == 128 && p.M >= 256);
+    if (p.zp) {
+        if (w8) hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, true, 8>), grid, dim3(512), 0, s, p);
+        else hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, true, 4>), grid, dim3(256), 0, s, p);
+    } else {
+        if (w8) hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, false, 8>), grid, dim3(512), 0, s, p);
+        else hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, false, 4>), grid, dim3(256), 0, s, p);
+    }
     return hipGetLastError();
 }
 
@@ -409,16 +420,18 @@ hipError_t launch_prec(const tbh_weight &w, const PParams &p, hipStream_t s) {
     if (force == 2) return launch_split<PREC, 64, 128>(w, p, t64x128, 1, s);
     if (force == 3) return launch_split<PREC, 128, 128>(w, p, t128, 1, s);
     if (p.M >= 256) {
-        // The largest tile that still gives two blocks per CU without a K
-        // split; with none, 128 x 128 tiles split along K to a block per CU.
-        // A CU holding one block runs its K steps with nothing to overlap
-        // the global-load waits, dequantization and barriers of one wave
-        // per SIMD, while two blocks on a CU took 1.2x the time of one
-        // (timestamps inside the kernel).  Measured against the 64-row rule
-        // below: INT8 5632x2048 M = 512 35.1 -> 30.6 us (64 x 64), INT4
-        // 2048x5632 M = 512 52.2 -> 43.7 us (128 x 128, 4 splits), M = 2048
-        // 136 -> 118 us (64 x 128); INT8 M = 2048 stays 128 x 128.
-        if (t128 >= 2 * cus) return launch_split<PREC, 128, 128>(w, p, t128, 1, s);
+        // Timestamps inside the kernel showed a block with one wave per SIMD
+        // spending three quarters of each K step on global-load waits,
+        // dequantization, LDS traffic and barriers that nothing overlaps;
+        // two blocks on a CU took 1.2x the time of one.  So: 128 x 128 tiles
+        // as 8-wave blocks (two waves per SIMD) when they give every CU a
+        // block; else the widest tile giving two blocks per CU without a K
+        // split; else 128 x 128 split along K to a block per CU.  Measured
+        // against 4-wave blocks chosen to give every CU a block: INT8
+        // 5632x2048 M = 512 35.1 -> 31 us (64 x 64), INT4 2048x5632 M = 512
+        // 52.2 -> 32.5 us (128 x 128, 4 splits), M = 2048 136 -> 89 us; INT8
+        // M = 2048 unchanged at 77 us.
+        if (t128 >= cus) return launch_split<PREC, 128, 128>(w, p, t128, 1, s);
         if (t64x128 >= 2 * cus) return launch_split<PREC, 64, 128>(w, p, t64x128, 1, s);
         if (t64 >= 2 * cus) return launch_split<PREC, 64, 64>(w, p, t64, 2, s);
         return launch_split<PREC, 128, 128>(w, p, t128, 1, s);
