@@ -29,10 +29,11 @@
 // across the wave's four 16-lane rows (v_permlane32_swap, v_permlane16_swap)
 // then gives lane (n, kb) word kb of chunks c .. c + 3 -- one B operand per
 // MFMA -- and all four scales.  The x fragments of the block's K range are
-// built in LDS first and shared by the block's eight waves; the weight loads
-// then run two steps ahead of the MFMAs (a wave that issues all of its loads
-// at once sits at the issue until most of them are accepted, then computes
-// every step after the data has arrived).  Small N is split along K over blocks; a
+// built in LDS and shared by the block's eight waves; the weight loads run
+// two steps ahead of the MFMAs, the first two issued right behind the x
+// loads so that they land while x is staged (a wave that issues all of its
+// loads at once sits at the issue until most of them are accepted, then
+// computes every step after the data has arrived).  Small N is split along K over blocks; a
 // second kernel adds the splits in split order (deterministic).
 #include <cmath>
 #include <cstdlib>
@@ -149,7 +150,27 @@ __global__ __launch_bounds__(512) void sgemv_int4(const SParams p) {
         xv[i] = float4{in ? t.x : 0.f, in ? t.y : 0.f, in ? t.z : 0.f, in ? t.w : 0.f};
     }
 
-    // ---- 2. x fragments: per-row exponent from the block's max |x[m]|
+    // ---- 2. weight and scale loads, D steps ahead of their use: lane (n, r)
+    // takes chunk cb + 4 t + r of row n for step t.  Chunks past the row
+    // re-read its last chunk and meet x = 0.  The first D steps go out right
+    // behind the x loads, so they land while x is staged; the rest follow
+    // one step at a time (a wave that issues every load of its range at once
+    // stalls at the issue -- each load touches 16 rows' cache lines -- and
+    // cannot compute meanwhile).
+    const uint8_t *wrow = p.data + (int64_t)row * p.row_bytes;
+    const float *srow = p.scales + (int64_t)(row >> 2) * p.G * 4 + (row & 3);
+    u32x4 wr[D];
+    float sr[D];
+    auto load_step = [&](int t) {
+        const int c = min(cb + kStepChunks * t + g, p.chunks - 1);
+        wr[t % D] = __builtin_nontemporal_load((const u32x4 *)(wrow + 16 * c));
+        sr[t % D] = srow[4 * (c >> p.cpg_shift)];
+    };
+#pragma unroll
+    for (int t = 0; t < D && t < NS; ++t) load_step(t);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- 3. x fragments: per-row exponent from the block's max |x[m]|
     // (each thread's units, then its wave by DPP, then the eight waves)
     float mx[M];
 #pragma unroll
@@ -210,22 +231,6 @@ __global__ __launch_bounds__(512) void sgemv_int4(const SParams p) {
     }
     lds_barrier();
 
-    // ---- 3. weight and scale loads, D steps ahead of their use: lane (n, r)
-    // takes chunk cb + 4 t + r of row n for step t.  Chunks past the row
-    // re-read its last chunk and meet x = 0.  Issued after x is staged: a
-    // wave that issues every load of its range at once stalls at the issue
-    // (each load touches 16 rows' cache lines) and cannot compute meanwhile.
-    const uint8_t *wrow = p.data + (int64_t)row * p.row_bytes;
-    const float *srow = p.scales + (int64_t)(row >> 2) * p.G * 4 + (row & 3);
-    u32x4 wr[D];
-    float sr[D];
-    auto load_step = [&](int t) {
-        const int c = min(cb + kStepChunks * t + g, p.chunks - 1);
-        wr[t % D] = __builtin_nontemporal_load((const u32x4 *)(wrow + 16 * c));
-        sr[t % D] = srow[4 * (c >> p.cpg_shift)];
-    };
-#pragma unroll
-    for (int t = 0; t < D && t < NS; ++t) load_step(t);
 
     // ---- 4. per step: transpose, then per chunk j unpack, MFMA, scale
     const uint32_t kMagic = opaque(0x64006400u), kLo = opaque(0x000F000Fu), kHi = opaque(0x00F000F0u);
