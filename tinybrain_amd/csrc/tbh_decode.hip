@@ -26,6 +26,7 @@
 // in device memory and the step ends with a one-thread kernel that advances
 // it, so a captured step replays as the next one.
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <vector>
@@ -69,6 +70,7 @@ struct AttnParams {
     int32_t *pos;            // [0] position, [1] overflow flag
     int32_t nh, nkv, hd, kvd, hidden, max_seq;
     int32_t rep, splits;
+    int32_t wpb;             // attention_split waves per block: min(4, rep)
     float rope_base, scale;
 };
 
@@ -97,10 +99,12 @@ __device__ __forceinline__ void wave_lds_fence() {
 // Attention of one decode step, split over the cache.  One wave per (query
 // head, range of kSplit positions <= pos): it writes the range's softmax
 // partial -- max m, sum l of exp(score - m), and sum of exp(score - m) * v --
-// and attention_merge combines the ranges.  A block's four waves are four
+// and attention_merge combines the ranges.  A block's waves are up to four
 // query heads of one KV head (ModelRunner.swift:524-536, kvHead = head /
-// repeats), so they share the range's key and value rows through L1; the
-// grid covers max_seq and waves past pos return at once.
+// repeats), so they share the range's key and value rows through L1; a KV
+// head with fewer than four query heads gets blocks of that many waves (no
+// idle waves to dispatch).  The grid covers max_seq and waves past pos
+// return at once.
 //
 // Every global load is issued before the position is read: the position,
 // this step's q, k, v and RoPE frequencies, and the range's cache rows (the
@@ -121,11 +125,11 @@ __global__ __launch_bounds__(256) void attention_split(const AttnParams a) {
     __shared__ float ps[4][kSplit];
     __shared__ float4 red[4][64];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int nquad = (a.rep + 3) / 4;
+    const int nquad = (a.rep + a.wpb - 1) / a.wpb;
     const int split = blockIdx.x % a.splits;
     const int quad = (blockIdx.x / a.splits) % nquad;
     const int kvh = blockIdx.x / (a.splits * nquad);
-    const int hg = quad * 4 + w;                // head within the KV group
+    const int hg = quad * a.wpb + w;            // head within the KV group
     if (hg >= a.rep) return;
     const int head = kvh * a.rep + hg;
     const int c0 = split * kSplit;
@@ -336,8 +340,9 @@ __global__ __launch_bounds__(64) void attention_merge(const AttnParams a) {
 
 template <int HD>
 void launch_attention_hd(const AttnParams &ap, hipStream_t s) {
-    const int nquad = (ap.rep + 3) / 4;
-    hipLaunchKernelGGL(attention_split<HD>, dim3((unsigned)(ap.nkv * nquad * ap.splits)), dim3(256), 0, s, ap);
+    const int nquad = (ap.rep + ap.wpb - 1) / ap.wpb;
+    hipLaunchKernelGGL(attention_split<HD>, dim3((unsigned)(ap.nkv * nquad * ap.splits)),
+                       dim3((unsigned)(64 * ap.wpb)), 0, s, ap);
     hipLaunchKernelGGL(attention_merge<HD>, dim3((unsigned)ap.nh), dim3(64), 0, s, ap);
 }
 
@@ -711,6 +716,13 @@ tbh_status tbh_decoder_step_device(tbh_decoder *d, int32_t token, float *logits,
     ap.part_ml = d->attn_ml;
     ap.theta = d->rope_theta;
     ap.rep = c.num_heads / c.num_kv_heads;
+    {
+        static const int wpb_force = [] {
+            const char *v = std::getenv("TBH_ATTN_WPB");
+            return v && *v ? std::atoi(v) : 0;
+        }();
+        ap.wpb = wpb_force == 4 ? 4 : std::min(4, ap.rep);
+    }
     ap.splits = d->attn_splits;
     ap.scale = 1.0f / std::sqrt((float)d->head_dim);
     hipError_t e = hipSuccess;
