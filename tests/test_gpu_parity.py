@@ -146,8 +146,9 @@ def test_int4_baseline_config1(backend, K, N):
 # Burst GEMV (M in {1, 2, 4}; no zero points, 16-byte aligned x, K % 4 == 0):
 # one case per chunk-iteration count I = ceil(chunks / 64) = 1..6 and across
 # the rows per wave U the launch picks from N, M and the CU count (256 on
-# MI355X): 2 or 4 at M = 1, up to 16 at M = 2.  M = 8 runs on the matrix-core
-# kernel (INT4) or as two M = 4 launches (INT8).
+# MI355X): 2 or 4 at M = 1, up to 16 at M = 2.  The matrix-core kernel is
+# switched off here (large-K INT4 weights take it from 2 rows on by default),
+# so M = 8 runs as two M = 4 launches.
 @pytest.mark.parametrize("prec,K,N", [
     ("int4", 2048, 40960),   # I=1, U=16
     ("int4", 2048, 20000),   # I=1, U=8
@@ -161,7 +162,8 @@ def test_int4_baseline_config1(backend, K, N):
     ("int8", 5632, 2048),    # I=6 (1.1B down projection)
     ("int8", 4000, 777),     # I=4, ragged N
 ])
-def test_burst_shapes(backend, prec, K, N):
+def test_burst_shapes(backend, monkeypatch, prec, K, N):
+    monkeypatch.setenv("TBH_SGEMV_MIN_ROWS", "9")
     if prec == "int8":
         oq = _int8_pc(41 + K, K, N)
         pq = _product(oq, (K, N))
@@ -174,9 +176,10 @@ def test_burst_shapes(backend, prec, K, N):
 @pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 11008), (11008, 4096), (4096, 32000)])
 def test_int4_7b_projection_shapes(backend, K, N):
     # the 7B projection set (q/k/v/o, gate/up, down, LM
-    # head), INT4 g32 along K, batch M in {1, 8}
+    # head), INT4 g32 along K, batch M in {1, 8}; M = 2..4 cross the default
+    # VALU / matrix-core thresholds of these shapes
     qt = _int4_nk(0x7B1A0070 + K + N, K, N, 32)
-    _check(backend, _product(qt, (K, N), T.Layout.NK_FLAT), qt, Ms=(1, 8), cpu_path=False)
+    _check(backend, _product(qt, (K, N), T.Layout.NK_FLAT), qt, Ms=(1, 2, 3, 4, 8), cpu_path=False)
 
 
 @pytest.mark.parametrize("K,N,gs,path", [(256, 512, 32, "int4_ngroup"), (2048, 2048, 32, "int4_ngroup"),

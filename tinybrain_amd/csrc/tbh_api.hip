@@ -626,18 +626,35 @@ extern "C" {
 // ---------------------------------------------------------------------------
 // matmul
 // ---------------------------------------------------------------------------
+
+// Fewest rows of x sent to the matrix-core GEMV (9: never).  The VALU
+// kernels' time grows with M * N * K (their multiply-adds are the bound from
+// 4 rows on), the matrix-core kernel's hardly with M, so the crossover falls
+// with the weight's size and K.  Measured crossovers (INT4 g32, us per launch
+// VALU / matrix cores): 4096 x 11008 at M = 2 16.5 / 12.4; 11008 x 4096 at
+// M = 3 12.2 / 11.5; 32000 x 4096 at M = 3 28.7 / 22.1; 4096 x 4096 at M = 4
+// 10.7 / 7.8 (M = 3: 7.2 / 7.8); 2048 x 5632 at M = 4 9.3 / 8.0; 5632 x 2048
+// at M = 5 9.9 / 8.0 (M = 4: 6.5 / 7.6); 2048 x 2048 never (M = 8: 7.5 / 8.5,
+// the matrix-core launch needs a K split and its split sum).
+static int64_t sgemv_min_rows(const tbh_weight &w) {
+    const int64_t nk = w.N * w.K;
+    if (w.K >= 8192) return 2;
+    if (nk >= (int64_t)40 << 20) return 3;
+    if (w.K >= 4096) return 4;
+    if (nk >= (int64_t)8 << 20) return 5;
+    return 9;
+}
+
 static tbh_status matmul_enqueue(const tbh_weight *w, const float *x, int64_t M, float *y,
                                  hipStream_t s) {
     if (!weight_arrays_ok(*w))
         return set_error(TBH_E_INVALID, "weight device arrays are inconsistent with its layout");
     // 2..8 rows of x per launch on the matrix cores when the weight allows
-    // it: from 5 rows on (at M = 8 under half the time of two 4-row VALU
-    // launches), and from 4 rows on for tall weights (N >= 16384: 12.9 against
-    // 16.7 us at 32000 x 2048); below that the VALU kernels are as fast or
-    // faster.  TBH_SGEMV_MIN_ROWS sets one threshold for every shape (2..9;
-    // 9 turns the MFMA path off).
+    // it and M reaches sgemv_min_rows; below that the VALU kernels are as
+    // fast or faster.  TBH_SGEMV_MIN_ROWS sets one threshold for every shape
+    // (2..9; 9 turns the MFMA path off).
     const char *min_env = std::getenv("TBH_SGEMV_MIN_ROWS");
-    const int64_t sg_min = min_env && *min_env ? std::max(2, std::atoi(min_env)) : (w->N >= 16384 ? 4 : 5);
+    const int64_t sg_min = min_env && *min_env ? std::max(2, std::atoi(min_env)) : sgemv_min_rows(*w);
     const bool sg = M >= sg_min && sgemv_supported(*w);
     const int64_t rows = w->mfma_tiles || sg ? 8 : gemv_max_rows(*w);
     for (int64_t m0 = 0; m0 < M;) {
