@@ -394,7 +394,7 @@ def run_decode(args, backend, T, torch):
             "weights": ("INT8 symmetric per output channel" if prec == "int8" else
                         "INT4 symmetric, group 32 along K (converter layout)") +
                        "; one random init per projection shape, a device copy per layer",
-            "batch": 1, "launches_per_step": 6 * c["num_layers"] + 3,
+            "batch": 1, "launches_per_step": 6 * c["num_layers"] + 1,
         },
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

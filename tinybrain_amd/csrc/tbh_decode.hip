@@ -359,16 +359,6 @@ void launch_attention(const AttnParams &ap, hipStream_t s) {
     }
 }
 
-__global__ void embed_row(const float *emb, int32_t token, int32_t hidden, float *h) {
-    const int64_t base = (int64_t)token * hidden;
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < hidden; i += gridDim.x * blockDim.x)
-        h[i] = emb[base + i];
-}
-
-__global__ void advance_position(int32_t *pos) {
-    if (threadIdx.x == 0 && blockIdx.x == 0) pos[0] += 1;
-}
-
 // ---- host: concatenation of projection weights along N ---------------------
 
 struct OwnedDesc {
@@ -699,8 +689,6 @@ tbh_status tbh_decoder_step_device(tbh_decoder *d, int32_t token, float *logits,
     hipStream_t s = (hipStream_t)stream;
     const size_t H = (size_t)c.hidden;
     float *out = logits ? logits : d->logits;
-    hipLaunchKernelGGL(embed_row, dim3((unsigned)((H + 255) / 256)), dim3(256), 0, s, d->emb, token,
-                       c.hidden, d->h);
     AttnParams ap{};
     ap.qkv = d->qkv;
     ap.ctx = d->ctx;
@@ -729,7 +717,14 @@ tbh_status tbh_decoder_step_device(tbh_decoder *d, int32_t token, float *logits,
     for (int32_t l = 0; l < c.num_layers && e == hipSuccess; ++l) {
         const auto &L = d->layers[(size_t)l];
         const float *g_in = d->norms + (2 * (size_t)l) * H, *g_post = g_in + H;
-        e = launch_gemv_fused(*L.qkv, FusedGemvArgs{d->h, g_in, c.rms_eps, d->qkv, PRO_RMSNORM, EPI_STORE}, s);
+        // layer 0 reads the token's embedding row and stores it as the
+        // residual stream h (ModelRunner.swift:170); later layers read h
+        FusedGemvArgs qa{d->h, g_in, c.rms_eps, d->qkv, PRO_RMSNORM, EPI_STORE};
+        if (l == 0) {
+            qa.x = d->emb + (size_t)token * H;
+            qa.x_copy = d->h;
+        }
+        e = launch_gemv_fused(*L.qkv, qa, s);
         if (e != hipSuccess) break;
         ap.kcache = d->kcache + (size_t)l * c.max_seq * d->kv_dim;
         ap.vcache = d->vcache + (size_t)l * c.max_seq * d->kv_dim;
@@ -741,14 +736,12 @@ tbh_status tbh_decoder_step_device(tbh_decoder *d, int32_t token, float *logits,
         if (e != hipSuccess) break;
         e = launch_gemv_fused(*L.down, FusedGemvArgs{d->gu, nullptr, 0.0f, d->h, PRO_NONE, EPI_ACCUMULATE}, s);
     }
-    if (e == hipSuccess)
-        e = launch_gemv_fused(*d->lm_head,
-                              FusedGemvArgs{d->h, d->norms + 2 * (size_t)c.num_layers * H, c.rms_eps, out,
-                                            PRO_RMSNORM, EPI_STORE},
-                              s);
     if (e == hipSuccess) {
-        hipLaunchKernelGGL(advance_position, dim3(1), dim3(64), 0, s, d->pos);
-        e = hipGetLastError();
+        // the LM head also advances the position: every launch that reads it
+        // (the layers' attention) precedes it on the stream
+        FusedGemvArgs la{d->h, d->norms + 2 * (size_t)c.num_layers * H, c.rms_eps, out, PRO_RMSNORM, EPI_STORE};
+        la.advance = d->pos;
+        e = launch_gemv_fused(*d->lm_head, la, s);
     }
     if (e != hipSuccess) return hip_error(e, "decoder step launch");
     return TBH_OK;

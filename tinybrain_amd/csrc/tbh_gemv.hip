@@ -62,6 +62,8 @@ struct KParams {
     // fused decode prologue / epilogue (gemv_burst with M = 1 only)
     const float *g;    // PRO_RMSNORM: norm weight [K]
     float eps;         // PRO_RMSNORM: epsilon
+    float *xcopy;      // non-null: block 0 also stores x as given here ([K])
+    int32_t *advance;  // non-null: block 0 adds 1 to advance[0]
 };
 
 // expf at full precision (not the hardware exp2 approximation).
@@ -507,6 +509,20 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
     // Nothing that consumes a load may be scheduled above this point.
     __builtin_amdgcn_sched_barrier(0);
 
+    // ---- decode-step duties of block 0: keep x as given (the step's
+    // residual stream when x is an embedding row) and advance the position
+    // (no other launch of the step is running)
+    if constexpr (M == 1) {
+        if (p.xcopy != nullptr && blockIdx.x == 0) {
+#pragma unroll
+            for (int r = 0; r < XR; ++r) {
+                const int k = 4 * (tid + 256 * r);
+                if (k < p.K) *(float4 *)(p.xcopy + k) = xv[0][r];
+            }
+        }
+    }
+    if (p.advance != nullptr && blockIdx.x == 0 && tid == 0) p.advance[0] += 1;
+
     // ---- fused prologue: x <- rmsnorm(x) * g (reference order of
     // operations: Tensor.swift:1543-1556)
     if constexpr (PRO == PRO_RMSNORM) {
@@ -842,6 +858,8 @@ hipError_t launch_gemv_fused(const tbh_weight &w, const FusedGemvArgs &f, hipStr
     KParams p = make_params(w, a);
     p.g = f.g ? f.g : f.x;
     p.eps = f.eps;
+    p.xcopy = f.x_copy;
+    p.advance = f.advance;
     if (f.g && ((uintptr_t)f.g & 15)) return hipErrorInvalidValue;
     int I, U;
     int64_t lds;

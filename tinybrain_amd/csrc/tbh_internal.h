@@ -141,6 +141,8 @@ struct FusedGemvArgs {
     float *y;
     int prologue;
     int epilogue;
+    float *x_copy = nullptr;     // also store x as given here ([K], not aliasing x or y)
+    int32_t *advance = nullptr;  // also add 1 to advance[0] (read by no other work of the launch)
 };
 bool gemv_fused_supported(const tbh_weight &w);
 hipError_t launch_gemv_fused(const tbh_weight &w, const FusedGemvArgs &f, hipStream_t s);
