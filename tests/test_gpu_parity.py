@@ -476,6 +476,16 @@ def test_prefill_bf16_large_m(backend):
     _prefill_check(backend, _product(oq, (5632, 2048), T.Layout.NK_FLAT), oq, 2048, seed=9)
 
 
+def test_prefill_bf16_int4_k128_steps(backend):
+    # INT4 with every CU holding a 128 x 128 tile (16 x 16 tiles on 256 CUs)
+    # stages K steps of 128: ragged M and N, K = 1056 ending in a partial
+    # step (1056 = 8 * 128 + 32), zero points
+    K, N, M = 1056, 2000, 2000
+    q4 = _int4_nk(89, K, N, 32)
+    q4.zero_points = ((np.arange(q4.scales.size) % 5) - 2).astype(np.int8)
+    _prefill_check(backend, _product(q4, (K, N), T.Layout.NK_FLAT), q4, M, seed=23)
+
+
 def test_prefill_bf16_zero_points_and_groups(backend):
     qi = _int8_pc(73, 512, 96)
     qi.zero_points = ((np.arange(96) % 9) - 4).astype(np.int8)

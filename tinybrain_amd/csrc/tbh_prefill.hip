@@ -10,9 +10,9 @@
 // A block of four or eight waves owns a BM x BN output tile; its waves, as
 // 2 x (waves / 2), own (BM/2) x (BN/(waves/2)) each, as TM x TN tiles of
 // v_mfma_f32_16x16x32_bf16 (eight waves: two per SIMD from one block).  Per
-// K step of 64 the block stages x (bf16, as given) and the dequantized weight
-// tile in LDS; global loads of step t+1 are in flight while step t's MFMAs
-// run.  Weight operands are exact:
+// K step of 64 (128 for unsplit INT4 128 x 128 tiles) the block stages x
+// (bf16, as given) and the dequantized weight tile in LDS; global loads of
+// step t+1 are in flight while step t's MFMAs run.  Weight operands are exact:
 //   * INT8 (one scale per row): q - zp is an integer of magnitude <= 255,
 //     exact in bf16; the row scale multiplies the fp32 result once.
 //   * INT4 K-groups: groups are whole multiples of 32 along K, so each
@@ -33,9 +33,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kBK = 64;           // K per staged step (two MFMA K-steps of 32)
+constexpr int kBK = 64;           // K per staged step (two MFMA K-steps of 32) unless a launch takes 128
 constexpr int kRowPad = 8;        // bf16 of padding per LDS row (16 bytes)
-constexpr int kLdsRow = kBK + kRowPad;
 constexpr int kDepth = 2;         // K steps whose global loads are in flight at once
 
 struct PParams {
@@ -74,15 +73,16 @@ __device__ __forceinline__ float ubyte(uint32_t w) {
     return (float)((w >> (8 * J)) & 0xFFu);
 }
 
-template <int PREC, int BM, int BN, bool ZP, int WV>
+template <int PREC, int BM, int BN, bool ZP, int WV, int BK>
 __global__ __launch_bounds__(64 * WV) void gemm_bf16(const PParams p) {
+    constexpr int kLdsRow = BK + kRowPad;
     constexpr int NT = 64 * WV;                   // threads; waves as 2 x (WV / 2)
     constexpr int WC = WV / 2;
     constexpr int CE = PREC == 8 ? 16 : 32;       // elements per chunk
-    constexpr int CPR = kBK / CE;                 // chunks per row per step
+    constexpr int CPR = BK / CE;                 // chunks per row per step
     constexpr int WCH = BN * CPR;                 // weight chunks per step
     constexpr int WPT = (WCH + NT - 1) / NT;      // per thread (last may idle)
-    constexpr int XSEG = BM * (kBK / 8);          // 16-byte x segments per step
+    constexpr int XSEG = BM * (BK / 8);          // 16-byte x segments per step
     constexpr int XPT = XSEG / NT;
     constexpr int WM = BM / 2, WN = BN / WC;
     constexpr int TM = WM / 16, TN = WN / 16;
@@ -96,12 +96,12 @@ __global__ __launch_bounds__(64 * WV) void gemm_bf16(const PParams p) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int wm = wave / WC, wn = wave % WC;
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-    const int nsteps = (p.chunks * CE + kBK - 1) / kBK;
+    const int nsteps = (p.chunks * CE + BK - 1) / BK;
     // This block's K steps [t_begin, t_end); x past kend reads as zero, so
     // the padded steps at a split's end add nothing.
     const int t_begin = blockIdx.z * p.split_steps;
     const int t_end = min(nsteps, t_begin + p.split_steps);
-    const int kend = min(p.K, t_end * kBK);
+    const int kend = min(p.K, t_end * BK);
 
     // INT8 row scales of this lane's output columns, loaded before the K loop
     float scn[TN];
@@ -119,11 +119,11 @@ __global__ __launch_bounds__(64 * WV) void gemm_bf16(const PParams p) {
     // Only addresses are computed here; everything that uses a loaded value
     // (masks, conversions) happens in store_step, kDepth - 1 steps later.
     auto load_step = [&](int t, int d) {
-        const int k0 = t * kBK;
+        const int k0 = t * BK;
 #pragma unroll
         for (int j = 0; j < XPT; ++j) {
             const int s = tid + NT * j;
-            const int row = s / (kBK / 8), kq = s % (kBK / 8);
+            const int row = s / (BK / 8), kq = s % (BK / 8);
             const int m = min(m0 + row, p.M - 1), k = k0 + 8 * kq;
             // K % 8 == 0: a segment is all in or out.  Rows past M read row
             // M-1 (finite values; their outputs are never stored).
@@ -155,7 +155,7 @@ __global__ __launch_bounds__(64 * WV) void gemm_bf16(const PParams p) {
 #pragma unroll
         for (int j = 0; j < XPT; ++j) {
             const int s = tid + NT * j;
-            const int row = s / (kBK / 8), kq = s % (kBK / 8);
+            const int row = s / (BK / 8), kq = s % (BK / 8);
             *(u32x4 *)&xs[bb][row * kLdsRow + 8 * kq] = xin[d][j] ? xr[d][j] : u32x4{0, 0, 0, 0};
         }
 #pragma unroll
@@ -208,7 +208,7 @@ __global__ __launch_bounds__(64 * WV) void gemm_bf16(const PParams p) {
 
     auto compute = [&](int bb) {
 #pragma unroll
-        for (int ks = 0; ks < kBK / 32; ++ks) {
+        for (int ks = 0; ks < BK / 32; ++ks) {
             const int kofs = ks * 32 + 8 * (lane >> 4);
             bf16x8 af[TM];
 #pragma unroll
@@ -334,7 +334,7 @@ __global__ __launch_bounds__(256) void split_sum(const float *__restrict__ part,
     }
 }
 
-template <int PREC, int BM, int BN>
+template <int PREC, int BM, int BN, int BK>
 hipError_t launch_tile(const PParams &p, int splits, hipStream_t s) {
     static const int waves = [] {   // 4 or 8 forces the waves per block
         const char *v = std::getenv("TBH_PREFILL_WAVES");
@@ -343,11 +343,11 @@ hipError_t launch_tile(const PParams &p, int splits, hipStream_t s) {
     const dim3 grid((unsigned)((p.Np + BN - 1) / BN), (unsigned)((p.M + BM - 1) / BM), (unsigned)splits);
     const bool w8 = waves == 8 || (waves != 4 && BN == 128 && (p.M >= 256 || PREC == 4));
     if (p.zp) {
-        if (w8) hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, true, 8>), grid, dim3(512), 0, s, p);
-        else hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, true, 4>), grid, dim3(256), 0, s, p);
+        if (w8) hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, true, 8, BK>), grid, dim3(512), 0, s, p);
+        else hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, true, 4, BK>), grid, dim3(256), 0, s, p);
     } else {
-        if (w8) hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, false, 8>), grid, dim3(512), 0, s, p);
-        else hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, false, 4>), grid, dim3(256), 0, s, p);
+        if (w8) hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, false, 8, BK>), grid, dim3(512), 0, s, p);
+        else hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, false, 4, BK>), grid, dim3(256), 0, s, p);
     }
     return hipGetLastError();
 }
@@ -362,18 +362,19 @@ int blocks_per_cu(int dflt) {
     return v >= 0 ? v : dflt;
 }
 
-constexpr int kMinSplitSteps = 4;  // K steps of 64 a split keeps at least
+constexpr int kMinSplitK = 256;  // K a split keeps at least
 
-// K is split over blocks when there are fewer than bpc blocks per CU.
-template <int PREC, int BM, int BN>
+// K is split over blocks when there are fewer than bpc blocks per CU.  BK:
+// K per staged step (64 or 128).
+template <int PREC, int BM, int BN, int BK = kBK>
 hipError_t launch_split(const tbh_weight &w, PParams p, int64_t tiles, int bpc, hipStream_t s) {
-    const int nsteps = (int)((p.chunks * (PREC == 8 ? kInt8ChunkElems : kInt4ChunkElems) + kBK - 1) / kBK);
+    const int nsteps = (int)((p.chunks * (PREC == 8 ? kInt8ChunkElems : kInt4ChunkElems) + BK - 1) / BK);
     const int64_t cus = std::max(1, w.dev->cu_count);
     int splits = 1, sps = nsteps;
     bpc = blocks_per_cu(bpc);
     if (tiles < bpc * cus && p.ldy == p.N) {
         const int64_t want = (bpc * cus + tiles - 1) / tiles;
-        sps = (int)std::max<int64_t>(kMinSplitSteps, (nsteps + want - 1) / want);
+        sps = (int)std::max<int64_t>(kMinSplitK / BK, (nsteps + want - 1) / want);
         sps = (sps + kDepth - 1) / kDepth * kDepth;
         splits = (nsteps + sps - 1) / sps;
     }
@@ -392,7 +393,7 @@ hipError_t launch_split(const tbh_weight &w, PParams p, int64_t tiles, int bpc, 
         p.y = part;
         p.split_stride = n;
     }
-    hipError_t e = launch_tile<PREC, BM, BN>(p, splits, s);
+    hipError_t e = launch_tile<PREC, BM, BN, BK>(p, splits, s);
     if (e != hipSuccess || splits == 1) return e;
     const int64_t grid_cap = 4 * cus;
     if (n % 4 == 0 && ((uintptr_t)y & 15) == 0) {
@@ -431,7 +432,15 @@ hipError_t launch_prec(const tbh_weight &w, const PParams &p, hipStream_t s) {
         // 5632x2048 M = 512 35.1 -> 31 us (64 x 64), INT4 2048x5632 M = 512
         // 52.2 -> 32.5 us (128 x 128, 4 splits), M = 2048 136 -> 89 us; INT8
         // M = 2048 unchanged at 77 us.
-        if (t128 >= cus) return launch_split<PREC, 128, 128>(w, p, t128, 1, s);
+        // INT4 128 x 128 tiles without a K split stage K steps of 128 (half
+        // the barriers and loop trips per flop; its group scale per MFMA
+        // makes each step's VALU work larger): 2048x5632 M = 2048 90.4 ->
+        // 84.1 us.  INT8 launches measured slower with 128 (M = 512 on 64 x 64
+        // tiles 31.7 -> 33.6 us, M = 2048 79.0 -> 79.9 us), and the split INT4
+        // launch at M = 512 no faster (32.4 -> 32.8 us).
+        if (t128 >= cus)
+            return PREC == 4 ? launch_split<PREC, 128, 128, 128>(w, p, t128, 1, s)
+                             : launch_split<PREC, 128, 128>(w, p, t128, 1, s);
         if (t64x128 >= 2 * cus) return launch_split<PREC, 64, 128>(w, p, t64x128, 1, s);
         if (t64 >= 2 * cus) return launch_split<PREC, 64, 64>(w, p, t64, 2, s);
         return launch_split<PREC, 128, 128>(w, p, t128, 1, s);
