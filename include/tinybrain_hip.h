@@ -158,6 +158,15 @@ tbh_status tbh_matmul(tbh_device *dev, const float *x, int64_t M, int64_t K,
 tbh_status tbh_matmul_device(const tbh_weight *w, const float *x, int64_t M,
                              int64_t K, float *y, void *stream);
 
+/* Replaces LinearLayerWeights.apply(toRow:)
+ * (Sources/TinyBrainRuntime/ModelWeights.swift:47-68): y = x . dequantize(w)
+ * as tbh_matmul_device computes it, then y[m][n] += bias[n] (one fp32 add,
+ * after the product, as the reference's host loop does).  bias: device
+ * pointer to N floats, or NULL for no bias.  Device pointers, enqueued on
+ * `stream`. */
+tbh_status tbh_linear_device(const tbh_weight *w, const float *x, int64_t M,
+                             int64_t K, const float *bias, float *y, void *stream);
+
 /* Prefill: the same product for M >= 64 rows of bf16 activations, on bf16
  * MFMA.  The reference has no bf16 path; it multiplies
  * fp32 activations by dequantize(w) with cblas_sgemm

@@ -557,3 +557,43 @@ def test_prefill_bf16_unsupported(backend):
     with pytest.raises(T.HIPBackendError) as e:
         backend.matmul_bf16_device(x, backend.weight(_product(qi, (100, 16))))
     assert e.value.status == _abi.E_UNSUPPORTED
+
+
+# LinearLayerWeights.apply(toRow:) (ModelWeights.swift:47-68): the product,
+# then one fp32 add of bias[n] to every row.
+@pytest.mark.parametrize("prec,K,N,M", [("int8", 2048, 256, 1), ("int4", 2048, 5632, 4), ("int4", 4096, 1000, 8),
+                                        ("int8", 1000, 777, 3)])
+def test_linear_bias(backend, prec, K, N, M):
+    import torch
+
+    if prec == "int8":
+        oq = _int8_pc(111 + K, K, N)
+        pq = _product(oq, (K, N))
+    else:
+        oq = _int4_nk(113 + K, K, N, 32)
+        pq = _product(oq, (K, N), T.Layout.NK_FLAT)
+    W = _oracle_weight(oq, pq.layout)
+    x = O.fill_normal(29 + M, M * K).reshape(M, K)
+    bias = O.fill_normal(31, N, std=0.5)
+    lin = T.LinearLayerWeights(pq, bias)
+    y = lin.apply(x, backend)
+    # the product as tbh_matmul_device computes it, plus the bias in fp32:
+    # bit-identical to the reference order (product first, then the add)
+    w = backend.weight(pq)
+    yd = backend.matmul_device(torch.from_numpy(x).cuda(), w)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(y, yd.cpu().numpy() + bias[None, :])
+    err = O.parity_errors(y, O.gemm_f64(x, W) + bias[None, :].astype(np.float64))
+    assert err["gated"] <= GATE, err
+    # no bias: the plain product
+    np.testing.assert_array_equal(T.LinearLayerWeights(pq).apply(x, backend), yd.cpu().numpy())
+
+
+def test_linear_zero_weights_give_the_bias(backend):
+    # closed form: all-zero weights quantize to q = 0 (scale 1.0), so every
+    # output row is exactly the bias
+    K, N = 256, 96
+    oq = O.quantize_per_channel(np.zeros((K, N), np.float32))
+    bias = O.fill_normal(37, N, std=1.0)
+    y = T.LinearLayerWeights(_product(oq, (K, N)), bias).apply(O.fill_normal(41, 2 * K).reshape(2, K), backend)
+    np.testing.assert_array_equal(y, np.broadcast_to(bias, (2, N)))

@@ -171,3 +171,17 @@ def test_quantized_tensor_preconditions():
     d = qt.desc()
     assert (d.K, d.N, d.data_bytes, d.n_scales, d.group_size) == (5, 7, 18, 2, 32)
     assert ctypes.sizeof(_abi.QTensorDesc) == 80
+
+
+def test_linear_bias_precondition():
+    # ModelWeights.swift:53-54: "Bias must match output dimension", checked
+    # before anything reaches the GPU
+    import oracle as O
+
+    K, N = 64, 24
+    q = O.quantize_per_channel(O.fill_normal(3, K * N).reshape(K, N))
+    pq = T.QuantizedTensor((K, N), q.data, q.scales, T.QuantizationMode.perChannel)
+    with pytest.raises(T.PreconditionFailure):
+        T.LinearLayerWeights(pq, np.zeros(N + 1, np.float32)).apply(np.zeros((1, K), np.float32), None)
+    with pytest.raises(T.PreconditionFailure):
+        T.LinearLayerWeights(pq, np.zeros(N, np.float32)).apply(np.zeros((1, K + 1), np.float32), None)

@@ -7,6 +7,7 @@ package is the host-side mirror of the reference's operator API over it:
   * ``QuantizedTensor`` / ``quantize``       -- QuantizedTensor.swift
   * ``HIPBackend.matmulQuantized``            -- QuantizedMatMulBackend
                                                  (Backend.swift:173-175)
+  * ``LinearLayerWeights.apply``              -- ModelWeights.swift:47-68
 """
 from .quantized import (Layout, PreconditionFailure, QuantizationMode,  # noqa: F401
                         QuantizationPrecision, QuantizedTensor, packInt4,
@@ -14,10 +15,11 @@ from .quantized import (Layout, PreconditionFailure, QuantizationMode,  # noqa: 
                         unpack_int4_array, pack_int4_array)
 from .backend import DeviceWeight, HIPBackend, HIPBackendError  # noqa: F401
 from .decoder import Decoder, DecoderConfig  # noqa: F401
+from .linear import LinearLayerWeights  # noqa: F401
 from .tbf import TBFFile  # noqa: F401
 
 __all__ = [
-    "HIPBackend", "HIPBackendError", "DeviceWeight", "QuantizedTensor", "Decoder", "DecoderConfig", "TBFFile",
+    "HIPBackend", "HIPBackendError", "DeviceWeight", "QuantizedTensor", "LinearLayerWeights", "Decoder", "DecoderConfig", "TBFFile",
     "QuantizationMode", "QuantizationPrecision", "Layout", "PreconditionFailure",
     "quantize", "quantize_int4_flat", "packInt4", "unpackInt4",
 ]

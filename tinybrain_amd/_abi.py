@@ -24,7 +24,7 @@ EXPORTS = [
     "tbh_abi_version", "tbh_last_error", "tbh_status_string",
     "tbh_device_open", "tbh_device_close", "tbh_device_get_info",
     "tbh_weight_create", "tbh_weight_destroy", "tbh_weight_get_info",
-    "tbh_matmul", "tbh_matmul_device", "tbh_matmul_bf16_device",
+    "tbh_matmul", "tbh_matmul_device", "tbh_matmul_bf16_device", "tbh_linear_device",
     "tbh_dequantize", "tbh_dequantize_device",
     "tbh_decoder_create", "tbh_decoder_set_layer", "tbh_decoder_destroy",
     "tbh_decoder_set_position", "tbh_decoder_get_position",
@@ -152,6 +152,7 @@ def lib() -> ctypes.CDLL:
     L.tbh_weight_get_info.argtypes = [vp, ctypes.POINTER(WeightInfo)]
     L.tbh_matmul.argtypes = [vp, vp, i64, i64, vp, vp]
     L.tbh_matmul_device.argtypes = [vp, vp, i64, i64, vp, vp]
+    L.tbh_linear_device.argtypes = [vp, vp, i64, i64, vp, vp, vp]
     L.tbh_matmul_bf16_device.argtypes = [vp, vp, i64, i64, vp, vp]
     L.tbh_dequantize.argtypes = [vp, vp, vp]
     L.tbh_dequantize_device.argtypes = [vp, vp, vp]
@@ -193,7 +194,7 @@ def lib() -> ctypes.CDLL:
         getattr(L, name).restype = i32
     for name in ("tbh_device_open", "tbh_device_close", "tbh_device_get_info",
                  "tbh_weight_create", "tbh_weight_destroy", "tbh_weight_get_info",
-                 "tbh_matmul", "tbh_matmul_device", "tbh_matmul_bf16_device",
+                 "tbh_matmul", "tbh_matmul_device", "tbh_matmul_bf16_device", "tbh_linear_device",
                  "tbh_dequantize", "tbh_dequantize_device",
                  "tbh_softmax", "tbh_softmax_device", "tbh_rmsnorm", "tbh_rmsnorm_device",
                  "tbh_silu", "tbh_silu_device", "tbh_gelu", "tbh_gelu_device",

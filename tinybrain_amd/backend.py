@@ -169,6 +169,29 @@ class HIPBackend:
                                            out.data_ptr(), ctypes.c_void_p(s.cuda_stream)))
         return out
 
+    def linear_device(self, x, weight: DeviceWeight, bias=None, out=None, stream=None):
+        """Enqueue y = x . W (+ bias[n] on every row) on a HIP stream
+        (tbh_linear_device; LinearLayerWeights.apply(toRow:),
+        ModelWeights.swift:47-68).  bias: None or a float32 [N] cuda tensor."""
+        import torch
+
+        if x.dim() != 2 or x.shape[1] != weight.K:
+            raise PreconditionFailure("Dimensions must match")
+        if x.dtype != torch.float32 or not x.is_contiguous() or not x.is_cuda:
+            raise PreconditionFailure("x must be a contiguous float32 device tensor")
+        if bias is not None:
+            if tuple(bias.shape) != (weight.N,):
+                raise PreconditionFailure("Bias must match output dimension")
+            if bias.dtype != torch.float32 or not bias.is_contiguous() or not bias.is_cuda:
+                raise PreconditionFailure("bias must be a contiguous float32 device tensor")
+        if out is None:
+            out = torch.empty((x.shape[0], weight.N), dtype=torch.float32, device=x.device)
+        s = stream if stream is not None else torch.cuda.current_stream(x.device)
+        _check(self._lib.tbh_linear_device(weight.handle, x.data_ptr(), x.shape[0], x.shape[1],
+                                           None if bias is None else bias.data_ptr(), out.data_ptr(),
+                                           ctypes.c_void_p(s.cuda_stream)))
+        return out
+
     def matmul_bf16_device(self, x, weight: DeviceWeight, out=None, stream=None):
         """Prefill: enqueue y = x . W for bf16 activations on bf16 MFMA.
 

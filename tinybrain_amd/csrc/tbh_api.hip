@@ -688,6 +688,25 @@ tbh_status tbh_matmul_device(const tbh_weight *w, const float *x, int64_t M, int
     return matmul_enqueue(w, x, M, y, (hipStream_t)stream);
 }
 
+// y[m][n] += bias[n] over [M][N] (the bias add of ModelWeights.swift:51-63).
+static __global__ __launch_bounds__(256) void add_bias_rows(float *y, const float *bias, int64_t M, int64_t N) {
+    const int64_t total = M * N;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256)
+        y[i] += bias[i % N];
+}
+
+tbh_status tbh_linear_device(const tbh_weight *w, const float *x, int64_t M, int64_t K, const float *bias,
+                             float *y, void *stream) {
+    tbh_status st = tbh_matmul_device(w, x, M, K, y, stream);
+    if (st != TBH_OK || M == 0 || !bias) return st;
+    const int64_t total = M * w->N;
+    const int64_t blocks = std::min<int64_t>((total + 255) / 256, 4 * std::max(1, w->dev->cu_count));
+    hipLaunchKernelGGL(add_bias_rows, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, y, bias, M,
+                       w->N);
+    TBH_HIP(hipGetLastError(), "tbh_linear_device: bias launch");
+    return TBH_OK;
+}
+
 tbh_status tbh_matmul(tbh_device *dev, const float *x, int64_t M, int64_t K, const tbh_weight *w,
                       float *y) {
     if (!dev || !w) return set_error(TBH_E_INVALID, "tbh_matmul: NULL device or weight");
