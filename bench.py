@@ -11,12 +11,18 @@ metric "dequant-GEMV GB/s and % of HBM peak" is quoted on):
   distinct copies totalling >= 2 GiB so every launch streams from HBM rather
   than the 256 MiB Infinity Cache.  Inputs are resident in HBM before timing.
 
+Exactly --warmup untimed steps run first, then exactly --steps timed steps,
+each launched from HIP graphs of at most one pool sweep.
 value = algorithmic bytes of all GEMVs in the timed steps / wall time (GB/s),
-algorithmic bytes per GEMV = W + S + Z + 4*M*K + 4*M*N (BASELINE.md section 4).
+algorithmic bytes per GEMV = W + S + Z + 4*M*K + 4*M*N.
 The roofline object reports the dominant kernel (32000x2048) timed with HIP
-events on its own stream over back-to-back launches.  cpu_baseline times the
-restated reference CPU path (dequantize() then sgemm on all host cores) on a
-bounded sample of the same workload.
+events on its own stream over back-to-back launches (--roctx-regions marks
+exactly those launches for ``rocprofv3 --selected-regions``).  cpu_baseline
+times the restated reference CPU path (dequantize() single-threaded, then
+sgemm on every host CPU this process may use, capped by the CPU share
+OMP_NUM_THREADS grants) on a bounded sample of the same workload.  The
+default line also carries "decode_1p1b_int8": tokens/s of the 1.1B-shaped
+INT8 decode step (the headline metric's second half), same step counts.
 """
 from __future__ import annotations
 
@@ -101,6 +107,83 @@ def profiled_traffic(prec: str, N: int, K: int, M: int):
     return None
 
 
+def host_info() -> dict:
+    """Host cores as this process sees them: nproc, the CPUs it may run on,
+    the CPU share the environment grants (OMP_NUM_THREADS; 16 per GPU on the
+    MI355X boxes) and the lscpu model name."""
+    nproc = os.cpu_count() or 1
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        aff = nproc
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    model = ""
+    try:
+        import subprocess
+
+        for line in subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout.splitlines():
+            if line.startswith("Model name:"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except Exception:
+        pass
+    return {"nproc": nproc, "affinity_cpus": aff, "omp_num_threads": share or None, "model": model}
+
+
+def cpu_threads() -> int:
+    """Threads for the CPU baseline's sgemm: every CPU this process may run
+    on, capped by the CPU share the environment grants (OMP_NUM_THREADS)."""
+    h = host_info()
+    return max(1, min(h["affinity_cpus"], h["omp_num_threads"] or h["affinity_cpus"]))
+
+
+class Roctx:
+    """roctxProfilerResume / roctxProfilerPause (rocprofiler-sdk roctx), so that
+    ``rocprofv3 --selected-regions`` records only the launches a roofline
+    figure is measured on.  No-ops when the library is absent or no profiler
+    is attached."""
+
+    def __init__(self, enabled: bool):
+        self._lib = None
+        if enabled:
+            import ctypes
+
+            for name in ("librocprofiler-sdk-roctx.so.1", "librocprofiler-sdk-roctx.so"):
+                try:
+                    self._lib = ctypes.CDLL(name)
+                    break
+                except OSError:
+                    continue
+            if self._lib is not None:
+                self._lib.roctxProfilerPause.argtypes = [ctypes.c_uint64]
+                self._lib.roctxProfilerResume.argtypes = [ctypes.c_uint64]
+
+    def resume(self):
+        if self._lib is not None:
+            self._lib.roctxProfilerResume(0)
+
+    def pause(self):
+        if self._lib is not None:
+            self._lib.roctxProfilerPause(0)
+
+
+def step_graphs(torch, stream, launch_step, n_steps: int, per_graph: int, first: int = 0):
+    """HIP graphs that together launch steps first .. first + n_steps - 1
+    (launch_step(i) enqueues step i on `stream`), at most per_graph steps per
+    graph.  Returns the list of graphs in launch order."""
+    graphs = []
+    i = first
+    while i < first + n_steps:
+        n = min(per_graph, first + n_steps - i)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for j in range(i, i + n):
+                launch_step(j)
+        graphs.append(g)
+        i += n
+    return graphs
+
+
 def make_weight(prec: str, gs: int, N: int, K: int, seed: int):
     """Synthetic W ~ N(0, 0.02) as PyTorch [N, K], quantized with the
     product's restatement of the reference quantizers."""
@@ -119,7 +202,7 @@ def cpu_baseline(qts, shapes, M: int, budget_s: float = 15.0):
     sgemm on all host cores.  Times whole steps until ~budget_s."""
     import oracle as O
 
-    threads = min(os.cpu_count() or 1, 16)
+    threads = cpu_threads()
     oq = []
     for qt in qts:
         oq.append(O.QTensor(qt.shape, qt.data, qt.scales, qt.zeroPoints, int(qt.mode),
@@ -143,6 +226,7 @@ def cpu_baseline(qts, shapes, M: int, budget_s: float = 15.0):
         "value": round(byts / wall / 1e9, 4),
         "unit": "GB/s",
         "cores": threads,
+        "host": host_info(),
         "kind": "port",
         "sample": f"{steps} step(s) of the same workload (one GEMV per shape, M={M}); "
                   f"dequantize {t_deq:.2f}s single-threaded + sgemm {t_gemm:.2f}s on {threads} threads",
@@ -160,7 +244,7 @@ def cpu_baseline_prefill(qt, N, K, M, budget_s: float = 15.0):
     then sgemm of the (bf16-valued) fp32 activations on all host cores."""
     import oracle as O
 
-    threads = min(os.cpu_count() or 1, 16)
+    threads = cpu_threads()
     oq = O.QTensor(qt.shape, qt.data, qt.scales, qt.zeroPoints, int(qt.mode), int(qt.precision),
                    qt.groupSize)
     x = np.random.default_rng(1).normal(size=(M, K)).astype(np.float32)
@@ -179,6 +263,7 @@ def cpu_baseline_prefill(qt, N, K, M, budget_s: float = 15.0):
         "value": round(2.0 * M * N * K * steps / wall / 1e12, 5),
         "unit": "TFLOP/s",
         "cores": threads,
+        "host": host_info(),
         "kind": "port",
         "sample": f"{steps} GEMM(s) of the same shape; dequantize {t_deq:.2f}s single-threaded + "
                   f"sgemm {t_gemm:.2f}s on {threads} threads",
@@ -203,31 +288,37 @@ def run_prefill(args, backend, T, torch):
         backend.matmul_bf16_device(x, pool[i], out=y, stream=cap)
     torch.cuda.synchronize()
     eager = y.clone()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=cap):
-        for i in range(n_sets):
-            backend.matmul_bf16_device(x, pool[i], out=y, stream=cap)
+
+    def step(i):
+        backend.matmul_bf16_device(x, pool[i % n_sets], out=y, stream=cap)
+
+    check = step_graphs(torch, cap, step, n_sets, n_sets)[0]
     for _ in range(2):
         y.zero_()
-        graph.replay()
+        with torch.cuda.stream(cap):
+            check.replay()
         torch.cuda.synchronize()
         if not torch.equal(y, eager):
             raise RuntimeError("graph replay differs from the eager launches")
-    reps = max(1, -(-args.steps // n_sets))
-    warm = max(1, -(-args.warmup // n_sets))
+    del check
+    warm_graphs = step_graphs(torch, cap, step, args.warmup, n_sets)
+    timed_graphs = step_graphs(torch, cap, step, args.steps, n_sets, first=args.warmup)
+    roctx = Roctx(args.roctx_regions)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(cap):
-        for _ in range(warm):
-            graph.replay()
+        for g in warm_graphs:
+            g.replay()
         torch.cuda.synchronize()
+        roctx.resume()
         t0 = time.perf_counter()
         e0.record(cap)
-        for _ in range(reps):
-            graph.replay()
+        for g in timed_graphs:
+            g.replay()
         e1.record(cap)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-    steps_done = reps * n_sets
+        roctx.pause()
+    steps_done = args.steps
     kern_us = e0.elapsed_time(e1) * 1e3 / steps_done
     flops = 2.0 * M * N * K
     byts = prefill_bytes(prec, gs, N, K, M)
@@ -249,7 +340,7 @@ def run_prefill(args, backend, T, torch):
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": steps_done,
-        "warmup": warm * n_sets,
+        "warmup": args.warmup,
         "ms_per_step": round(1e3 * wall / steps_done, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -298,7 +389,7 @@ def cpu_baseline_decode(prec, gs, c, qts, budget_s: float = 15.0, M: int = 1):
     yields M tokens."""
     import oracle as O
 
-    threads = min(os.cpu_count() or 1, 16)
+    threads = cpu_threads()
     layer, lm = decode_shapes(c)
     oq = [O.QTensor(q.shape, q.data, q.scales, q.zeroPoints, int(q.mode), int(q.precision), q.groupSize)
           for q in qts]
@@ -323,6 +414,7 @@ def cpu_baseline_decode(prec, gs, c, qts, budget_s: float = 15.0, M: int = 1):
         "value": round(M / step_s, 4),
         "unit": "tokens/s",
         "cores": threads,
+        "host": host_info(),
         "kind": "port",
         "sample": f"{reps} pass(es) over one layer's 7 projections + the LM head at M={M}, scaled to "
                   f"{c['num_layers']} layers; projections only",
@@ -330,8 +422,11 @@ def cpu_baseline_decode(prec, gs, c, qts, budget_s: float = 15.0, M: int = 1):
     }
 
 
-def run_decode(args, backend, T, torch):
-    prec, gs, c, ctx = DECODE[args.workload]
+def measure_decode(args, backend, T, torch, workload):
+    """Decode tokens/s of one DECODE workload: a HIP graph of one step,
+    replayed exactly args.warmup times untimed and args.steps times timed.
+    Returns the result object (the bench line's fields)."""
+    prec, gs, c, ctx = DECODE[workload]
     dev = torch.device("cuda", 0)
     cfg = T.DecoderConfig(max_seq=ctx + args.warmup + args.steps + 8, **c)
     layer, lm = decode_shapes(c)
@@ -378,6 +473,7 @@ def run_decode(args, backend, T, torch):
     achieved = byts / step_us / 1e3
     out = {
         "metric": f"decode tokens/s, {c['num_layers']}-layer LLaMA shape ({prec.upper()}), 1 GPU",
+        "tokens_per_s": round(args.steps / wall, 2),
         "value": round(args.steps / wall, 2),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -390,7 +486,7 @@ def run_decode(args, backend, T, torch):
         "dtype": "f32",
         "data": "synthetic",
         "config": {
-            "workload": args.workload, **c, "context": ctx,
+            "workload": workload, **c, "context": ctx,
             "weights": ("INT8 symmetric per output channel" if prec == "int8" else
                         "INT4 symmetric, group 32 along K (converter layout)") +
                        "; one random init per projection shape, a device copy per layer",
@@ -406,8 +502,14 @@ def run_decode(args, backend, T, torch):
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline_decode(prec, gs, c, qts, args.cpu_budget)
-    print(json.dumps(out), flush=True)
     dec.close()
+    return out
+
+
+def run_decode(args, backend, T, torch):
+    out = measure_decode(args, backend, T, torch, args.workload)
+    out.pop("tokens_per_s")
+    print(json.dumps(out), flush=True)
     backend.close()
 
 
@@ -546,7 +648,8 @@ def cpu_baseline_op(op, c, budget_s):
         if el >= budget_s:
             break
     bytes_per = op_sizes(op, c)[2]
-    return {"value": round(bytes_per * n / el / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+    return {"value": round(bytes_per * n / el / 1e9, 3), "unit": "GB/s", "cores": 1, "host": host_info(),
+            "kind": "port",
             "sample": f"{n} full launches of the same shape through oracle/ops_ref.py (numpy float64), "
                       f"{el:.1f} s"}
 
@@ -585,30 +688,30 @@ def run_op(args, backend, T, torch):
         launch(i)
     torch.cuda.synchronize()
     eager = outs[0].clone()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=cap):
-        for i in range(n_sets):
-            launch(i)
+    step = lambda i: launch(i % n_sets)
+    check = step_graphs(torch, cap, step, n_sets, n_sets)[0]
     outs[0].zero_()
-    graph.replay()
+    with torch.cuda.stream(cap):
+        check.replay()
     torch.cuda.synchronize()
     if not torch.equal(outs[0], eager):
         raise RuntimeError("graph replay differs from the eager launches")
-    reps = max(1, -(-args.steps // n_sets))
-    warm = max(1, -(-args.warmup // n_sets))
+    del check
+    warm_graphs = step_graphs(torch, cap, step, args.warmup, n_sets)
+    timed_graphs = step_graphs(torch, cap, step, args.steps, n_sets, first=args.warmup)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(cap):
-        for _ in range(warm):
-            graph.replay()
+        for g in warm_graphs:
+            g.replay()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         e0.record(cap)
-        for _ in range(reps):
-            graph.replay()
+        for g in timed_graphs:
+            g.replay()
         e1.record(cap)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-    steps_done = reps * n_sets
+    steps_done = args.steps
     kern_us = e0.elapsed_time(e1) * 1e3 / steps_done
     achieved = byts / kern_us / 1e3
     out = {
@@ -617,7 +720,7 @@ def run_op(args, backend, T, torch):
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": steps_done,
-        "warmup": warm * n_sets,
+        "warmup": args.warmup,
         "ms_per_step": round(1e3 * wall / steps_done, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -645,6 +748,11 @@ def main():
     ap.add_argument("--pool-gib", type=float, default=2.2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--no-decode", action="store_true",
+                    help="int4_g32_gemv_m1: leave out the 1.1B decode-step measurement")
+    ap.add_argument("--roctx-regions", action="store_true",
+                    help="mark the launches the roofline kernel time is measured on with "
+                         "roctxProfilerResume/Pause, for rocprofv3 --selected-regions")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="for rocprofv3 --pmc: 5 plain copies of 64 MiB (calibration kernel of "
                          "known size) then 20 launches of the dominant GEMV; no timing")
@@ -700,11 +808,11 @@ def main():
         backend.close()
         return
 
-    # Launches are captured into HIP graphs (one graph = one sweep over the
-    # pool), so the timed region measures the GPU, not Python/ctypes launch
-    # overhead.  Replays are checked against an eager run on the capture
-    # stream (which also sizes that stream's split-K workspace, so the
-    # captured launches split K exactly as the eager ones do).
+    # Launches are captured into HIP graphs, so the timed region measures the
+    # GPU, not Python/ctypes launch overhead.  Step i runs one GEMV of each
+    # shape on pool set i mod n_sets.  Replays are checked against an eager
+    # run on the capture stream (which also sizes that stream's split-K
+    # workspace, so the captured launches split K exactly as the eager ones).
     cap = torch.cuda.Stream(dev)
     cap.wait_stream(stream)
 
@@ -717,38 +825,46 @@ def main():
         step(i)
     torch.cuda.synchronize()
     eager = [y.clone() for y in ys]
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=cap):
-        for i in range(n_sets):
-            for j, (N, K) in enumerate(shapes):
-                backend.matmul_device(xs[K], pool[i][j], out=ys[j], stream=cap)
+    # exactly `warmup` untimed steps, then exactly `steps` timed steps
+    # (continuing the rotation), in graphs of at most one pool sweep each
+    warm_graphs = step_graphs(torch, cap, step, args.warmup, n_sets)
+    timed_graphs = step_graphs(torch, cap, step, args.steps, n_sets, first=args.warmup)
+    check = step_graphs(torch, cap, step, n_sets, n_sets)[0]
     for r in range(2):
         for y in ys:
             y.zero_()
-        graph.replay()
+        with torch.cuda.stream(cap):
+            check.replay()
         torch.cuda.synchronize()
         for y, e in zip(ys, eager):
             if not torch.equal(y, e):
                 raise RuntimeError("graph replay differs from the eager launches")
+    del check
 
-    reps = max(1, -(-args.steps // n_sets))  # graph replays covering >= steps
-    warm = max(1, -(-args.warmup // n_sets))
-    for _ in range(warm):
-        graph.replay()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        graph.replay()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    steps_done = reps * n_sets
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(cap):
+        for g in warm_graphs:
+            g.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record(cap)
+        for g in timed_graphs:
+            g.replay()
+        e1.record(cap)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    steps_done = args.steps
     step_bytes = sum(alg_bytes(prec, gs, N, K, M) for N, K in shapes)
     value = step_bytes * steps_done / wall / 1e9
+    gpu_step_us = e0.elapsed_time(e1) * 1e3 / steps_done
+    del warm_graphs, timed_graphs
 
     # ---- per-shape kernel time: a graph of n_sets back-to-back launches of
     # one shape, bracketed by HIP events on the replay stream
     per_shape = {}
     shape_us = {}
+    jd = int(np.argmax([alg_bytes(prec, gs, N, K, M) for N, K in shapes]))
+    roctx = Roctx(args.roctx_regions)
     for j, (N, K) in enumerate(shapes):
         g1 = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g1, stream=cap):
@@ -761,18 +877,21 @@ def main():
         with torch.cuda.stream(cap):
             g1.replay()
             torch.cuda.synchronize()
+            if j == jd:
+                roctx.resume()        # rocprofv3 --selected-regions: these launches only
             e0.record(cap)
             for _ in range(nrep):
                 g1.replay()
             e1.record(cap)
         e1.synchronize()
+        if j == jd:
+            roctx.pause()
         us = e0.elapsed_time(e1) * 1e3 / (nrep * n_sets)
         b = alg_bytes(prec, gs, N, K, M)
         shape_us[j] = us
         per_shape[f"{N}x{K}"] = {"us": round(us, 3), "GB_s": round(b / us / 1e3, 1),
                                  "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
                                  "path": pool[0][j].path}
-    jd = int(np.argmax([alg_bytes(prec, gs, N, K, M) for N, K in shapes]))
     Nd, Kd = shapes[jd]
     kern_us = shape_us[jd]
     kbytes = alg_bytes(prec, gs, Nd, Kd, M)
@@ -786,7 +905,7 @@ def main():
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": steps_done,
-        "warmup": warm * n_sets,
+        "warmup": args.warmup,
         "ms_per_step": round(1e3 * wall / steps_done, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -798,6 +917,7 @@ def main():
             "weights": "INT4 symmetric, group 32 along K (converter layout)" if prec == "int4"
             else "INT8 symmetric per output channel",
             "shapes_NxK": [f"{N}x{K}" for N, K in shapes],
+            "gpu_us_per_step": round(gpu_step_us, 3),
             "M": M,
             "x": "fp32 N(0,1), W fp32 N(0,0.02) quantized",
             "pool_bytes": pool_bytes,
@@ -820,6 +940,13 @@ def main():
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(bases, shapes, M, args.cpu_budget)
+    del pool
+    if args.workload == "int4_g32_gemv_m1" and not args.no_decode:
+        # the second half of the headline metric: decode tokens/s at the
+        # 1.1B shape, same --steps / --warmup
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        out["decode_1p1b_int8"] = measure_decode(args, backend, T, torch, "decode_1p1b_int8")
     print(json.dumps(out), flush=True)
     backend.close()
 

@@ -133,6 +133,17 @@ tbh_status tbh_device_close(tbh_device *dev);
 /* HIP device ordinal and compute-unit count of an open device. */
 tbh_status tbh_device_get_info(const tbh_device *dev, int32_t *ordinal, int32_t *cu_count);
 
+/* Launch-rule overrides of an open device, for measurement and tests.  No
+ * reference counterpart (MetalBackend's launch shapes are fixed,
+ * MetalBackend.swift:949-956).  Every accepted value keeps results within
+ * the matmul tolerance; TBH_E_INVALID for unknown options or values.
+ *   TBH_OPT_SGEMV_MIN_ROWS: fewest rows of x (2..9, 9 = never) that go to the
+ *     matrix-core small-M GEMV for every weight; 0 restores the per-weight
+ *     rule.  The environment variable TBH_SGEMV_MIN_ROWS, read when the
+ *     device opens, sets the initial value. */
+enum { TBH_OPT_SGEMV_MIN_ROWS = 1 };
+tbh_status tbh_device_set_option(tbh_device *dev, int32_t option, int64_t value);
+
 /* ---- weights ----------------------------------------------------------- */
 /* Replaces the weight upload of MetalBackend.cachedQuantizedBuffers
  * (MetalBackend.swift:1282-1308) and cachedINT4Buffers (:1322-1359): copies

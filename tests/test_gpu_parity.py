@@ -162,15 +162,18 @@ def test_int4_baseline_config1(backend, K, N):
     ("int8", 5632, 2048),    # I=6 (1.1B down projection)
     ("int8", 4000, 777),     # I=4, ragged N
 ])
-def test_burst_shapes(backend, monkeypatch, prec, K, N):
-    monkeypatch.setenv("TBH_SGEMV_MIN_ROWS", "9")
+def test_burst_shapes(backend, prec, K, N):
     if prec == "int8":
         oq = _int8_pc(41 + K, K, N)
         pq = _product(oq, (K, N))
     else:
         oq = _int4_nk(43 + K, K, N, 32)
         pq = _product(oq, (K, N), T.Layout.NK_FLAT)
-    _check(backend, pq, oq, Ms=(1, 2, 4, 8), cpu_path=False)
+    backend.set_option(_abi.OPT_SGEMV_MIN_ROWS, 9)
+    try:
+        _check(backend, pq, oq, Ms=(1, 2, 4, 8), cpu_path=False)
+    finally:
+        backend.set_option(_abi.OPT_SGEMV_MIN_ROWS, 0)
 
 
 @pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 11008), (11008, 4096), (4096, 32000)])
@@ -293,9 +296,10 @@ def test_device_resident_entry_point(backend):
 # weights without zero points; small N splits K over blocks
 # ---------------------------------------------------------------------------
 @pytest.fixture
-def sgemv_from_two_rows(monkeypatch):
-    monkeypatch.setenv("TBH_SGEMV_MIN_ROWS", "2")   # the MFMA path for every M >= 2
+def sgemv_from_two_rows(backend):
+    backend.set_option(_abi.OPT_SGEMV_MIN_ROWS, 2)   # the MFMA path for every M >= 2
     yield
+    backend.set_option(_abi.OPT_SGEMV_MIN_ROWS, 0)
 
 
 @pytest.mark.parametrize("M", [2, 3, 4, 5, 6, 7, 9, 16])
@@ -371,6 +375,69 @@ def test_sgemv_split_k_determinism_and_graphs(backend, sgemv_from_two_rows):
         if phase == 1:
             np.testing.assert_array_equal(first, eager)
         del g
+
+
+def test_workspace_growth_keeps_captured_graphs_valid(backend, sgemv_from_two_rows):
+    # A graph captured with a split launch holds its stream's workspace.  A
+    # larger eager split launch on the same stream then grows that workspace:
+    # the old buffer must stay allocated (it is retired, not freed), so the
+    # graph still replays to the product, also after torch has allocated and
+    # filled memory in between.  Covers the matrix-core GEMV (tbh_matmul_device)
+    # and the prefill GEMM (tbh_matmul_bf16_device).
+    import torch
+
+    s = torch.cuda.Stream()
+    # small: 2 x [2048 -> 1024] splits K 4 ways (32 KiB of partials, the
+    # first 1 MiB workspace); large: 8 x [8192 -> 4096] splits K 16 ways (2 MiB)
+    qs = _int4_nk(811, 2048, 1024, 32)
+    ws = backend.weight(_product(qs, (2048, 1024), T.Layout.NK_FLAT))
+    ql = _int4_nk(812, 8192, 4096, 32)
+    wl = backend.weight(_product(ql, (8192, 4096), T.Layout.NK_FLAT))
+    xs_h = O.fill_normal(813, 2 * 2048).reshape(2, 2048)
+    xl_h = O.fill_normal(814, 8 * 8192).reshape(8, 8192)
+    ref_s = O.gemm_f64(xs_h, _oracle_weight(qs, T.Layout.NK_FLAT))
+    ref_l = O.gemm_f64(xl_h, _oracle_weight(ql, T.Layout.NK_FLAT))
+    # prefill, M = 64: [5632 -> 2048] splits K 15 ways (7.9 MB of partials,
+    # an 8 MiB workspace); [5632 -> 6000] 6 ways (9.2 MB, more than 8 MiB)
+    qp = _int4_nk(815, 5632, 2048, 32)
+    wp = backend.weight(_product(qp, (5632, 2048), T.Layout.NK_FLAT))
+    qp2 = _int4_nk(816, 5632, 6000, 32)
+    wp2 = backend.weight(_product(qp2, (5632, 6000), T.Layout.NK_FLAT))
+    xp_b = torch.from_numpy(O.fill_normal(817, 64 * 5632).reshape(64, 5632)).to(torch.bfloat16)
+    xp2_b = torch.from_numpy(O.fill_normal(818, 64 * 5632).reshape(64, 5632)).to(torch.bfloat16)
+    ref_p = O.gemm_f64(xp_b.float().numpy(), _oracle_weight(qp, T.Layout.NK_FLAT))
+    ref_p2 = O.gemm_f64(xp2_b.float().numpy(), _oracle_weight(qp2, T.Layout.NK_FLAT))
+
+    xs, xl = torch.from_numpy(xs_h).cuda(), torch.from_numpy(xl_h).cuda()
+    xp, xp2 = xp_b.cuda(), xp2_b.cuda()
+    ys = torch.empty((2, 1024), dtype=torch.float32, device="cuda")
+    yl = torch.empty((8, 4096), dtype=torch.float32, device="cuda")
+    yp = torch.empty((64, 2048), dtype=torch.float32, device="cuda")
+    yp2 = torch.empty((64, 6000), dtype=torch.float32, device="cuda")
+    for small, large, ref_small, ref_large, y_small, y_large in (
+        (lambda: backend.matmul_device(xs, ws, out=ys, stream=s),
+         lambda: backend.matmul_device(xl, wl, out=yl, stream=s), ref_s, ref_l, ys, yl),
+        (lambda: backend.matmul_bf16_device(xp, wp, out=yp, stream=s),
+         lambda: backend.matmul_bf16_device(xp2, wp2, out=yp2, stream=s), ref_p, ref_p2, yp, yp2),
+    ):
+        with torch.cuda.stream(s):
+            small()                       # sizes the stream's workspace for the small call
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            small()                       # the split launch, on that workspace
+        with torch.cuda.stream(s):
+            large()                       # grows the workspace: a new buffer
+        torch.cuda.synchronize()
+        assert O.parity_errors(y_large.cpu().numpy(), ref_large)["gated"] <= GATE
+        junk = [torch.full((1 << 18,), float("nan"), device="cuda") for _ in range(16)]
+        for _ in range(3):
+            y_small.zero_()
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert O.parity_errors(y_small.cpu().numpy(), ref_small)["gated"] <= GATE
+        del g, junk
 
 
 # ---------------------------------------------------------------------------
@@ -468,6 +535,51 @@ def test_prefill_bf16(backend, prec, K, N, M):
         oq = _int4_nk(67 + K + M, K, N, 32)
         pq = _product(oq, (K, N), T.Layout.NK_FLAT)
     _prefill_check(backend, pq, oq, M, seed=5 + M)
+
+
+def _prefill_tile(prec, N, M, cus=256):
+    """The launch rule of tbh_prefill.hip (launch_prec), restated to show
+    which tile family and wave count each case below reaches."""
+    Np = -(-N // 8) * 8
+    t128 = -(-Np // 128) * -(-M // 128)
+    t64x128 = -(-Np // 128) * -(-M // 64)
+    t64 = -(-Np // 64) * -(-M // 64)
+    if M >= 256:
+        if t128 >= cus:
+            return "128x128", 8
+        if t64 >= 2 * cus:
+            return "64x64", 4
+        return "128x128 split", 8
+    if prec == "int4":
+        return "64x128 split", 8
+    if t128 >= cus:
+        return "128x128", 4
+    if t64x128 >= cus:
+        return "64x128", 4
+    return "64x64 split", 4
+
+
+@pytest.mark.parametrize("K,N,M,tile", [
+    (2048, 5632, 2048, ("128x128", 8)),      # BASELINE configs[3] INT8 at M = 2048
+    (2048, 5632, 128, ("64x64 split", 4)),   # configs[3] INT8 at M = 128
+    (2048, 32000, 129, ("128x128", 4)),      # 4-wave 128 x 128, ragged M
+    (2048, 20480, 128, ("64x128", 4)),       # 64 x 128
+    (4096, 520, 300, ("128x128 split", 8)),  # 8-wave 128 x 128 split along K, ragged N
+])
+def test_prefill_bf16_int8_tiles(backend, K, N, M, tile):
+    # every INT8 tile family of the prefill launch rule under parity
+    assert backend.cu_count != 256 or _prefill_tile("int8", N, M) == tile
+    oq = _int8_pc(131 + K + N + M, K, N)
+    _prefill_check(backend, _product(oq, (K, N)), oq, M, seed=29 + M)
+
+
+def test_prefill_bf16_int4_64x64(backend):
+    # INT4 on 64 x 64 tiles without a K split (M >= 256, too few 128 x 128
+    # tiles for the CUs, enough 64 x 64 tiles for two per CU)
+    K, N, M = 2048, 5632, 512
+    assert backend.cu_count != 256 or _prefill_tile("int4", N, M) == ("64x64", 4)
+    oq = _int4_nk(137, K, N, 32)
+    _prefill_check(backend, _product(oq, (K, N), T.Layout.NK_FLAT), oq, M, seed=31)
 
 
 def test_prefill_bf16_large_m(backend):

@@ -190,6 +190,82 @@ def test_asymmetric_traps_on_all_positive():
     assert _rel(np.linspace(-1, 2, 16), O.dequantize(qt)) < 0.01
 
 
+def test_symmetric_is_per_channel_of_one_column():
+    # quantizeSymmetric (QuantizedTensor.swift:427-450) is quantizePerChannel
+    # (:379-424) of the same values laid out as one column: one abs-max, one
+    # scale, the same rounding and clamp.  Per-channel is pinned by its own
+    # closed forms above, so this reduction pins the symmetric quantizer.
+    for seed, shape in ((41, (37, 53)), (42, (1, 1000)), (43, (256, 3))):
+        w = O.fill_normal(seed, int(np.prod(shape)), std=0.3).reshape(shape)
+        sym = O.quantize_symmetric(w)
+        col = O.quantize_per_channel(w.reshape(-1, 1))
+        assert sym.scales.size == 1 and sym.zero_points is None
+        np.testing.assert_array_equal(sym.scales.view(np.uint32), col.scales.view(np.uint32))
+        np.testing.assert_array_equal(sym.data, col.data)
+        # the abs-max element maps to +-127, every value within +-127
+        i = np.abs(w.reshape(-1)).argmax()
+        assert abs(int(sym.data[i])) == 127 and np.abs(sym.data.astype(int)).max() <= 127
+
+
+def test_symmetric_known_answers():
+    # abs-max 127 gives scale exactly 1.0, so q = round(w) with Swift's
+    # half-away-from-zero rounding: 0.5 -> 1, -0.5 -> -1, 1.5 -> 2, -2.5 -> -3
+    # (numpy's half-to-even would give 0, -0, 2, -2)
+    w = np.array([127.0, 0.5, -0.5, 1.5, -2.5, -127.0, 3.49], np.float32)
+    qt = O.quantize_symmetric(w)
+    assert qt.scales[0] == np.float32(1.0)
+    np.testing.assert_array_equal(qt.data, np.array([127, 1, -1, 2, -3, -127, 3], np.int8))
+    assert np.array_equal(O.quantize_symmetric(w, O.ROUND_NUMPY).data,
+                          np.array([127, 0, 0, 2, -2, -127, 3], np.int8))
+    # all zero: scale 1.0 (absMax not above leastNonzeroMagnitude), q = 0
+    z = O.quantize_symmetric(np.zeros(9, np.float32))
+    assert z.scales[0] == np.float32(1.0) and not z.data.any()
+    # scale = absMax / 127 in fp32: absMax 254 gives exactly 2.0
+    two = O.quantize_symmetric(np.array([-254.0, 3.0, 5.0], np.float32))
+    assert two.scales[0] == np.float32(2.0)
+    np.testing.assert_array_equal(two.data, np.array([-127, 2, 3], np.int8))
+
+
+def test_asymmetric_known_answers():
+    # quantizeAsymmetric (QuantizedTensor.swift:452-476): [min, max] -> [-128, 127]
+    # min -1, max 254: range 255, scale exactly 1.0, zero point
+    # round(1 - 128) = -127; q = round(w / s) + zp (half away from zero)
+    w = np.array([-1.0, 254.0, 0.0, 2.5, -0.5, 100.0], np.float32)
+    qt = O.quantize_asymmetric(w)
+    assert qt.scales[0] == np.float32(1.0)
+    assert qt.zero_points.tolist() == [-127]
+    np.testing.assert_array_equal(qt.data, np.array([-128, 127, -127, -124, -128, -27], np.int8))
+    # min -64, max 63.5: range 127.5, scale exactly 0.5, zero point 0
+    w2 = np.array([-64.0, 63.5, 0.25, -0.25, 10.0], np.float32)
+    q2 = O.quantize_asymmetric(w2)
+    assert q2.scales[0] == np.float32(0.5) and q2.zero_points.tolist() == [0]
+    np.testing.assert_array_equal(q2.data, np.array([-128, 127, 1, -1, 20], np.int8))
+    # the endpoints come back exactly: (q - zp) * s
+    for qq, ww in ((qt, w), (q2, w2)):
+        d = O.dequantize(qq)
+        assert d[0] == ww[0] and d[1] == ww[1]
+    # constant data: range 0 -> scale 1.0; zero point round(-c - 128)
+    c = O.quantize_asymmetric(np.full(4, -3.0, np.float32))
+    assert c.scales[0] == np.float32(1.0) and c.zero_points.tolist() == [-125]
+    np.testing.assert_array_equal(c.data, np.full(4, -128, np.int8))
+
+
+def test_dequant_per_tensor_closed_form():
+    # dequantize() for .symmetric / .asymmetric (QuantizedTensor.swift:273-281):
+    # one scale and one zero point for every element, (Float(q) - Float(zp)) * s
+    # rounded once.  (q - zp) * s in float64 is exact (9-bit integer times a
+    # 24-bit significand), so rounding it to fp32 gives the expected bits.
+    rng = np.random.default_rng(12)
+    q = rng.integers(-128, 128, size=(19, 29)).astype(np.int8)
+    for mode, zp, s in ((O.MODE_SYMMETRIC, None, np.float32(0.0123)),
+                        (O.MODE_ASYMMETRIC, np.array([-37], np.int8), np.float32(3.7e-3)),
+                        (O.MODE_ASYMMETRIC, np.array([127], np.int8), np.float32(1.5))):
+        qt = O.QTensor((19, 29), q.reshape(-1), np.array([s], np.float32), zp, mode, O.PREC_INT8)
+        z = 0.0 if zp is None else float(zp[0])
+        want = ((q.astype(np.float64) - z) * np.float64(s)).astype(np.float32)
+        np.testing.assert_array_equal(O.dequantize(qt).view(np.uint32), want.view(np.uint32))
+
+
 # --------------------------------------------------------------------------
 # dequantize() (QuantizedTensor.swift:182-286)
 # --------------------------------------------------------------------------

@@ -18,11 +18,13 @@ MODE_SYMMETRIC, MODE_ASYMMETRIC, MODE_PER_CHANNEL, MODE_INT4, MODE_INT4_PER_CHAN
 LAYOUT_KN_FLAT, LAYOUT_NK_FLAT = 0, 1
 PATH_INT8_ROW, PATH_INT4_KGROUP, PATH_INT4_NGROUP, PATH_GENERIC = range(4)
 PATH_NAMES = {0: "int8_row", 1: "int4_kgroup", 2: "int4_ngroup", 3: "generic"}
+# device options (tbh_device_set_option)
+OPT_SGEMV_MIN_ROWS = 1
 
 # every symbol the header declares
 EXPORTS = [
     "tbh_abi_version", "tbh_last_error", "tbh_status_string",
-    "tbh_device_open", "tbh_device_close", "tbh_device_get_info",
+    "tbh_device_open", "tbh_device_close", "tbh_device_get_info", "tbh_device_set_option",
     "tbh_weight_create", "tbh_weight_destroy", "tbh_weight_get_info",
     "tbh_matmul", "tbh_matmul_device", "tbh_matmul_bf16_device", "tbh_linear_device",
     "tbh_dequantize", "tbh_dequantize_device",
@@ -147,6 +149,7 @@ def lib() -> ctypes.CDLL:
     L.tbh_device_open.argtypes = [i32, pp]
     L.tbh_device_close.argtypes = [vp]
     L.tbh_device_get_info.argtypes = [vp, ctypes.POINTER(i32), ctypes.POINTER(i32)]
+    L.tbh_device_set_option.argtypes = [vp, i32, i64]
     L.tbh_weight_create.argtypes = [vp, ctypes.POINTER(QTensorDesc), pp]
     L.tbh_weight_destroy.argtypes = [vp]
     L.tbh_weight_get_info.argtypes = [vp, ctypes.POINTER(WeightInfo)]
@@ -192,7 +195,7 @@ def lib() -> ctypes.CDLL:
                  "tbh_decoder_set_position", "tbh_decoder_get_position",
                  "tbh_decoder_step_device", "tbh_decoder_step"):
         getattr(L, name).restype = i32
-    for name in ("tbh_device_open", "tbh_device_close", "tbh_device_get_info",
+    for name in ("tbh_device_open", "tbh_device_close", "tbh_device_get_info", "tbh_device_set_option",
                  "tbh_weight_create", "tbh_weight_destroy", "tbh_weight_get_info",
                  "tbh_matmul", "tbh_matmul_device", "tbh_matmul_bf16_device", "tbh_linear_device",
                  "tbh_dequantize", "tbh_dequantize_device",

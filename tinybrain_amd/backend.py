@@ -98,6 +98,11 @@ class HIPBackend:
         self._cache: Dict[uuid.UUID, DeviceWeight] = {}
         self._lock = threading.Lock()
 
+    def set_option(self, option: int, value: int) -> None:
+        """tbh_device_set_option: a launch-rule override (e.g.
+        ``_abi.OPT_SGEMV_MIN_ROWS``; 0 restores the rule)."""
+        _check(self._lib.tbh_device_set_option(self._dev, int(option), int(value)))
+
     @staticmethod
     def isAvailable(device: int = 0) -> bool:
         """MetalBackend.isAvailable: a gfx950 device can be opened."""

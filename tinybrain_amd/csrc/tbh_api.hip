@@ -108,6 +108,8 @@ tbh_status tbh_device_open(int32_t ordinal, tbh_device **out) {
     auto dev = std::make_unique<tbh_device>();
     dev->ordinal = ordinal;
     dev->cu_count = prop.multiProcessorCount;
+    if (const char *v = std::getenv("TBH_SGEMV_MIN_ROWS"); v && *v)   // read once, at open
+        dev->sgemv_min_rows.store(std::min(9, std::max(2, std::atoi(v))), std::memory_order_relaxed);
     TBH_HIP(hipStreamCreateWithFlags(&dev->stream, hipStreamNonBlocking), "hipStreamCreate");
     *out = dev.release();
     return TBH_OK;
@@ -117,15 +119,27 @@ tbh_status tbh_device_close(tbh_device *dev) {
     if (!dev) return TBH_OK;
     // teardown: statuses are not actionable here, the handle goes away regardless
     (void)use_device(dev->ordinal);
-    if (dev->stream) (void)hipStreamSynchronize(dev->stream);
+    // One device-wide wait covers every stream that used a workspace; those
+    // streams belong to the caller and may already be destroyed.
+    (void)hipDeviceSynchronize();
     if (dev->stage) (void)hipFree(dev->stage);
-    for (auto &ws : dev->workspaces) {
-        (void)hipStreamSynchronize(ws.stream);
-        (void)hipFree(ws.ptr);
-    }
+    for (auto &ws : dev->workspaces) (void)hipFree(ws.ptr);
+    for (void *p : dev->retired) (void)hipFree(p);
     if (dev->stream) (void)hipStreamDestroy(dev->stream);
     delete dev;
     return TBH_OK;
+}
+
+tbh_status tbh_device_set_option(tbh_device *dev, int32_t option, int64_t value) {
+    if (!dev) return set_error(TBH_E_INVALID, "tbh_device_set_option: dev is NULL");
+    switch (option) {
+    case TBH_OPT_SGEMV_MIN_ROWS:
+        if (value != 0 && (value < 2 || value > 9))
+            return set_error(TBH_E_INVALID, "TBH_OPT_SGEMV_MIN_ROWS takes 0 (per-weight rule) or 2..9");
+        dev->sgemv_min_rows.store((int)value, std::memory_order_relaxed);
+        return TBH_OK;
+    default: return set_error(TBH_E_INVALID, "tbh_device_set_option: unknown option");
+    }
 }
 
 tbh_status tbh_device_get_info(const tbh_device *dev, int32_t *ordinal, int32_t *cu_count) {
@@ -603,19 +617,21 @@ void *stream_workspace(tbh_device *dev, hipStream_t s, size_t bytes) {
     if (ws && ws->bytes >= bytes) return ws->ptr;
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(s, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return nullptr;
+    // Grow by replacement: work queued on this stream, and any graph captured
+    // on it, may still use the old buffer, so it stays allocated (retired)
+    // until tbh_device_close.  Growth doubles, so the retired bytes stay below
+    // the live buffer's.
+    const size_t mib = size_t(1) << 20;
+    size_t grown = (bytes + mib - 1) & ~(mib - 1);
+    if (ws) grown = std::max(grown, 2 * ws->bytes);
+    void *p = nullptr;
+    if (hipMalloc(&p, grown) != hipSuccess) return nullptr;
     if (!ws) {
         dev->workspaces.push_back({s, nullptr, 0});
         ws = &dev->workspaces.back();
     }
-    // The previous buffer may still be read by work queued on this stream.
-    if (ws->ptr && (hipStreamSynchronize(s) != hipSuccess || hipFree(ws->ptr) != hipSuccess)) return nullptr;
-    ws->ptr = nullptr;
-    ws->bytes = 0;
-    const size_t grown = (bytes + (size_t(1) << 20) - 1) & ~((size_t(1) << 20) - 1);
-    if (hipMalloc(&ws->ptr, grown) != hipSuccess) {
-        ws->ptr = nullptr;
-        return nullptr;
-    }
+    if (ws->ptr) dev->retired.push_back(ws->ptr);
+    ws->ptr = p;
     ws->bytes = grown;
     return ws->ptr;
 }
@@ -646,15 +662,15 @@ static int64_t sgemv_min_rows(const tbh_weight &w) {
 }
 
 static tbh_status matmul_enqueue(const tbh_weight *w, const float *x, int64_t M, float *y,
-                                 hipStream_t s) {
+                                 hipStream_t s, const Scratch &scr) {
     if (!weight_arrays_ok(*w))
         return set_error(TBH_E_INVALID, "weight device arrays are inconsistent with its layout");
     // 2..8 rows of x per launch on the matrix cores when the weight allows
     // it and M reaches sgemv_min_rows; below that the VALU kernels are as
-    // fast or faster.  TBH_SGEMV_MIN_ROWS sets one threshold for every shape
-    // (2..9; 9 turns the MFMA path off).
-    const char *min_env = std::getenv("TBH_SGEMV_MIN_ROWS");
-    const int64_t sg_min = min_env && *min_env ? std::max(2, std::atoi(min_env)) : sgemv_min_rows(*w);
+    // fast or faster.  The device option TBH_OPT_SGEMV_MIN_ROWS sets one
+    // threshold for every shape (2..9; 9 turns the MFMA path off).
+    const int forced = w->dev->sgemv_min_rows.load(std::memory_order_relaxed);
+    const int64_t sg_min = forced > 0 ? std::max(2, forced) : sgemv_min_rows(*w);
     const bool sg = M >= sg_min && sgemv_supported(*w);
     const int64_t rows = w->mfma_tiles || sg ? 8 : gemv_max_rows(*w);
     for (int64_t m0 = 0; m0 < M;) {
@@ -662,7 +678,11 @@ static tbh_status matmul_enqueue(const tbh_weight *w, const float *x, int64_t M,
         GemvArgs a{x + m0 * w->K, w->K, y + m0 * w->N, w->N, mc};
         hipError_t e = hipErrorInvalidValue;
         if (w->mfma_tiles) e = launch_mgemv(*w, a, s);
-        else if (sg && mc >= sg_min) e = launch_sgemv(*w, a, s);
+        else if (sg && mc >= sg_min) e = launch_sgemv(*w, a, s, scr);
+        if (e == hipErrorOutOfMemory && scr.is_fixed())
+            return set_error(TBH_E_INVALID, "this call needs " + std::to_string(scr.shortfall) +
+                                                " bytes of scratch; the no-allocation entry point holds " +
+                                                std::to_string(scr.fixed_bytes));
         if (e == hipErrorInvalidValue && !w->mfma_tiles) {
             // the VALU kernels (at most gemv_max_rows rows per launch)
             const int64_t vr = gemv_max_rows(*w);
@@ -685,7 +705,9 @@ tbh_status tbh_matmul_device(const tbh_weight *w, const float *x, int64_t M, int
     if (!x || !y) return set_error(TBH_E_INVALID, "tbh_matmul_device: x or y is NULL");
     tbh_status st = use_device(w->dev->ordinal);
     if (st != TBH_OK) return st;
-    return matmul_enqueue(w, x, M, y, (hipStream_t)stream);
+    Scratch scr;
+    scr.dev = w->dev;
+    return matmul_enqueue(w, x, M, y, (hipStream_t)stream, scr);
 }
 
 // y[m][n] += bias[n] over [M][N] (the bias add of ModelWeights.swift:51-63).
@@ -730,7 +752,9 @@ tbh_status tbh_matmul(tbh_device *dev, const float *x, int64_t M, int64_t K, con
     float *dx = (float *)dev->stage;
     float *dy = (float *)((char *)dev->stage + ((xb + 255) & ~size_t(255)));
     TBH_HIP(hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, dev->stream), "tbh_matmul: copy x");
-    st = matmul_enqueue(w, dx, M, dy, dev->stream);
+    Scratch scr;
+    scr.dev = dev;
+    st = matmul_enqueue(w, dx, M, dy, dev->stream, scr);
     if (st != TBH_OK) return st;
     TBH_HIP(hipMemcpyAsync(y, dy, yb, hipMemcpyDeviceToHost, dev->stream), "tbh_matmul: copy y");
     TBH_HIP(hipStreamSynchronize(dev->stream), "tbh_matmul: synchronize");
@@ -755,7 +779,9 @@ tbh_status tbh_matmul_bf16_device(const tbh_weight *w, const uint16_t *x, int64_
         return set_error(TBH_E_INVALID, "weight device arrays are inconsistent with its layout");
     tbh_status st = use_device(w->dev->ordinal);
     if (st != TBH_OK) return st;
-    hipError_t e = launch_prefill(*w, x, K, M, y, w->N, (hipStream_t)stream);
+    Scratch scr;
+    scr.dev = w->dev;
+    hipError_t e = launch_prefill(*w, x, K, M, y, w->N, (hipStream_t)stream, scr);
     if (e != hipSuccess) return hip_error(e, "prefill kernel launch");
     return TBH_OK;
 }

@@ -339,23 +339,26 @@ __global__ __launch_bounds__(64) void attention_merge(const AttnParams a) {
 }
 
 template <int HD>
-void launch_attention_hd(const AttnParams &ap, hipStream_t s) {
+hipError_t launch_attention_hd(const AttnParams &ap, hipStream_t s) {
     const int nquad = (ap.rep + ap.wpb - 1) / ap.wpb;
     hipLaunchKernelGGL(attention_split<HD>, dim3((unsigned)(ap.nkv * nquad * ap.splits)),
                        dim3((unsigned)(64 * ap.wpb)), 0, s, ap);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL(attention_merge<HD>, dim3((unsigned)ap.nh), dim3(64), 0, s, ap);
+    return hipGetLastError();
 }
 
-void launch_attention(const AttnParams &ap, hipStream_t s) {
+hipError_t launch_attention(const AttnParams &ap, hipStream_t s) {
     switch (ap.hd) {
-    case 16: launch_attention_hd<16>(ap, s); break;
-    case 32: launch_attention_hd<32>(ap, s); break;
-    case 48: launch_attention_hd<48>(ap, s); break;
-    case 64: launch_attention_hd<64>(ap, s); break;
-    case 80: launch_attention_hd<80>(ap, s); break;
-    case 96: launch_attention_hd<96>(ap, s); break;
-    case 112: launch_attention_hd<112>(ap, s); break;
-    default: launch_attention_hd<128>(ap, s); break;
+    case 16: return launch_attention_hd<16>(ap, s);
+    case 32: return launch_attention_hd<32>(ap, s);
+    case 48: return launch_attention_hd<48>(ap, s);
+    case 64: return launch_attention_hd<64>(ap, s);
+    case 80: return launch_attention_hd<80>(ap, s);
+    case 96: return launch_attention_hd<96>(ap, s);
+    case 112: return launch_attention_hd<112>(ap, s);
+    default: return launch_attention_hd<128>(ap, s);
     }
 }
 
@@ -728,7 +731,8 @@ tbh_status tbh_decoder_step_device(tbh_decoder *d, int32_t token, float *logits,
         if (e != hipSuccess) break;
         ap.kcache = d->kcache + (size_t)l * c.max_seq * d->kv_dim;
         ap.vcache = d->vcache + (size_t)l * c.max_seq * d->kv_dim;
-        launch_attention(ap, s);
+        e = launch_attention(ap, s);
+        if (e != hipSuccess) break;
         e = launch_gemv_fused(*L.o, FusedGemvArgs{d->ctx, nullptr, 0.0f, d->h, PRO_NONE, EPI_ACCUMULATE}, s);
         if (e != hipSuccess) break;
         // gate and up rows interleaved: the epilogue writes silu(gate) * up

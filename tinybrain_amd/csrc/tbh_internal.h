@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdint>
 #include <mutex>
 #include <string>
@@ -50,11 +51,15 @@ struct tbh_device {
     int32_t cu_count = 0;
     hipStream_t stream = nullptr;
     std::mutex mu;               // serialises tbh_matmul / tbh_dequantize
+    std::atomic<int> sgemv_min_rows{0};   // TBH_OPT_SGEMV_MIN_ROWS; 0 = per-weight rule
     void *stage = nullptr;       // device staging for the host-pointer calls
     size_t stage_bytes = 0;
 
-    // Per-stream device workspaces (split-K partial sums of the prefill
-    // GEMM): calls on different streams never share one.
+    // Per-stream device workspaces (split-K partial sums): calls on different
+    // streams never share one.  A workspace that has to grow is replaced, not
+    // freed: the old buffer moves to `retired`, because a HIP graph captured
+    // earlier on that stream still holds its address.  Both lists are freed
+    // by tbh_device_close after one device-wide synchronisation.
     struct Workspace {
         hipStream_t stream;
         void *ptr;
@@ -62,6 +67,7 @@ struct tbh_device {
     };
     std::mutex ws_mu;
     std::vector<Workspace> workspaces;
+    std::vector<void *> retired;
 };
 
 struct tbh_weight {
@@ -152,7 +158,8 @@ hipError_t launch_gemv_fused(const tbh_weight &w, const FusedGemvArgs &f, hipStr
 // hipErrorInvalidValue for shapes it does not take (odd alignment of x,
 // M out of range, no workspace while capturing a long row).
 bool sgemv_supported(const tbh_weight &w);
-hipError_t launch_sgemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s);
+struct Scratch;
+hipError_t launch_sgemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s, const Scratch &scr);
 
 // MFMA dequant-GEMV for M <= 8 rows of x on MFMA-tiled weights (tbh_mgemv.hip).
 hipError_t launch_mgemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s);
@@ -165,13 +172,37 @@ hipError_t launch_generic(const tbh_weight &w, const GemvArgs &a, hipStream_t s)
 // == 0 and a 16-byte aligned x.
 bool prefill_supported(const tbh_weight &w);
 hipError_t launch_prefill(const tbh_weight &w, const uint16_t *x, int64_t ldx, int64_t M, float *y,
-                          int64_t ldy, hipStream_t s);
+                          int64_t ldy, hipStream_t s, const Scratch &scr);
 
 // Device workspace of at least `bytes` owned by (dev, stream), grown on
-// demand (tbh_api.hip).  Growing synchronises the stream first.  Returns
-// nullptr when it would have to grow while the stream is being captured into
-// a graph, or when the allocation fails.
+// demand (tbh_api.hip).  Growing allocates a new buffer and keeps the old one
+// until the device closes.  Returns nullptr when it would have to grow while
+// the stream is being captured into a graph, or when the allocation fails.
 void *stream_workspace(tbh_device *dev, hipStream_t s, size_t bytes);
+
+// Where a launch takes its scratch memory (split-K partial sums) from: the
+// per-stream workspace of `dev`, grown on demand, or a fixed buffer that is
+// never grown (the no-allocation entry point).
+struct Scratch {
+    tbh_device *dev = nullptr;
+    void *fixed = nullptr;
+    size_t fixed_bytes = 0;
+    mutable size_t shortfall = 0;   // bytes a fixed buffer could not provide
+
+    bool is_fixed() const { return fixed != nullptr; }
+    // nullptr when the bytes are not available: a fixed buffer too small
+    // (shortfall set; the launcher then returns hipErrorOutOfMemory before
+    // launching anything), or a workspace that cannot grow (capture, OOM;
+    // the launcher then takes a path without scratch).
+    void *get(hipStream_t s, size_t bytes) const {
+        if (fixed) {
+            if (bytes <= fixed_bytes) return fixed;
+            shortfall = bytes;
+            return nullptr;
+        }
+        return stream_workspace(dev, s, bytes);
+    }
+};
 
 // Bit-exact dequantization to [K, N] row-major (tbh_ref_kernels.hip).
 hipError_t launch_dequant(const tbh_weight &w, float *out, hipStream_t s);

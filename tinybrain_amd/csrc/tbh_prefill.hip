@@ -367,7 +367,8 @@ constexpr int kMinSplitK = 256;  // K a split keeps at least
 // K is split over blocks when there are fewer than bpc blocks per CU.  BK:
 // K per staged step (64 or 128).
 template <int PREC, int BM, int BN, int BK = kBK>
-hipError_t launch_split(const tbh_weight &w, PParams p, int64_t tiles, int bpc, hipStream_t s) {
+hipError_t launch_split(const tbh_weight &w, PParams p, int64_t tiles, int bpc, hipStream_t s,
+                        const Scratch &scr) {
     const int nsteps = (int)((p.chunks * (PREC == 8 ? kInt8ChunkElems : kInt4ChunkElems) + BK - 1) / BK);
     const int64_t cus = std::max(1, w.dev->cu_count);
     int splits = 1, sps = nsteps;
@@ -382,7 +383,8 @@ hipError_t launch_split(const tbh_weight &w, PParams p, int64_t tiles, int bpc, 
     const int64_t n = (int64_t)p.M * p.N;
     float *part = nullptr;
     if (splits > 1) {
-        part = (float *)stream_workspace(w.dev, s, (size_t)(splits * n) * sizeof(float));
+        part = (float *)scr.get(s, (size_t)(splits * n) * sizeof(float));
+        if (!part && scr.is_fixed()) return hipErrorOutOfMemory;
         if (!part) {          // no workspace (graph capture before any eager call): one pass
             splits = 1;
             sps = nsteps;
@@ -408,7 +410,7 @@ hipError_t launch_split(const tbh_weight &w, PParams p, int64_t tiles, int bpc, 
 }
 
 template <int PREC>
-hipError_t launch_prec(const tbh_weight &w, const PParams &p, hipStream_t s) {
+hipError_t launch_prec(const tbh_weight &w, const PParams &p, hipStream_t s, const Scratch &scr) {
     const int64_t cus = std::max(1, w.dev->cu_count);
     const int64_t t128 = ((p.Np + 127) / 128) * ((p.M + 127) / 128);
     const int64_t t64x128 = ((p.Np + 127) / 128) * ((p.M + 63) / 64);
@@ -417,17 +419,19 @@ hipError_t launch_prec(const tbh_weight &w, const PParams &p, hipStream_t s) {
         const char *v = std::getenv("TBH_PREFILL_TILE");
         return v && *v ? std::atoi(v) : 0;
     }();
-    if (force == 1) return launch_split<PREC, 64, 64>(w, p, t64, 2, s);
-    if (force == 2) return launch_split<PREC, 64, 128>(w, p, t64x128, 1, s);
-    if (force == 3) return launch_split<PREC, 128, 128>(w, p, t128, 1, s);
+    if (force == 1) return launch_split<PREC, 64, 64>(w, p, t64, 2, s, scr);
+    if (force == 2) return launch_split<PREC, 64, 128>(w, p, t64x128, 1, s, scr);
+    if (force == 3) return launch_split<PREC, 128, 128>(w, p, t128, 1, s, scr);
     if (p.M >= 256) {
         // Timestamps inside the kernel showed a block with one wave per SIMD
         // spending three quarters of each K step on global-load waits,
         // dequantization, LDS traffic and barriers that nothing overlaps;
         // two blocks on a CU took 1.2x the time of one.  So: 128 x 128 tiles
         // as 8-wave blocks (two waves per SIMD) when they give every CU a
-        // block; else the widest tile giving two blocks per CU without a K
-        // split; else 128 x 128 split along K to a block per CU.  Measured
+        // block; else 64 x 64 tiles when they give two blocks per CU without
+        // a K split (64 x 128 tiles never do here: there are at most twice as
+        // many as 128 x 128 tiles, which are fewer than the CUs); else 128 x
+        // 128 split along K to a block per CU.  Measured
         // against 4-wave blocks chosen to give every CU a block: INT8
         // 5632x2048 M = 512 35.1 -> 31 us (64 x 64), INT4 2048x5632 M = 512
         // 52.2 -> 32.5 us (128 x 128, 4 splits), M = 2048 136 -> 89 us; INT8
@@ -439,11 +443,10 @@ hipError_t launch_prec(const tbh_weight &w, const PParams &p, hipStream_t s) {
         // tiles 31.7 -> 33.6 us, M = 2048 79.0 -> 79.9 us), and the split INT4
         // launch at M = 512 no faster (32.4 -> 32.8 us).
         if (t128 >= cus)
-            return PREC == 4 ? launch_split<PREC, 128, 128, 128>(w, p, t128, 1, s)
-                             : launch_split<PREC, 128, 128>(w, p, t128, 1, s);
-        if (t64x128 >= 2 * cus) return launch_split<PREC, 64, 128>(w, p, t64x128, 1, s);
-        if (t64 >= 2 * cus) return launch_split<PREC, 64, 64>(w, p, t64, 2, s);
-        return launch_split<PREC, 128, 128>(w, p, t128, 1, s);
+            return PREC == 4 ? launch_split<PREC, 128, 128, 128>(w, p, t128, 1, s, scr)
+                             : launch_split<PREC, 128, 128>(w, p, t128, 1, s, scr);
+        if (t64 >= 2 * cus) return launch_split<PREC, 64, 64>(w, p, t64, 2, s, scr);
+        return launch_split<PREC, 128, 128>(w, p, t128, 1, s, scr);
     }
     // Fewer rows (HBM-bound).  INT4, whose K steps carry a group scale per
     // MFMA: 64 x 128 tiles as 8-wave blocks, split along K to a block per CU
@@ -453,10 +456,10 @@ hipError_t launch_prec(const tbh_weight &w, const PParams &p, hipStream_t s) {
     // does little work per K step, so one per CU leaves its latency exposed;
     // 8-wave 64 x 128 tiles measured the same at M = 64 and 4 % slower at
     // M = 128).
-    if (PREC == 4) return launch_split<PREC, 64, 128>(w, p, t64x128, 1, s);
-    if (t128 >= cus) return launch_split<PREC, 128, 128>(w, p, t128, 1, s);
-    if (t64x128 >= cus) return launch_split<PREC, 64, 128>(w, p, t64x128, 1, s);
-    return launch_split<PREC, 64, 64>(w, p, t64, 2, s);
+    if (PREC == 4) return launch_split<PREC, 64, 128>(w, p, t64x128, 1, s, scr);
+    if (t128 >= cus) return launch_split<PREC, 128, 128>(w, p, t128, 1, s, scr);
+    if (t64x128 >= cus) return launch_split<PREC, 64, 128>(w, p, t64x128, 1, s, scr);
+    return launch_split<PREC, 64, 64>(w, p, t64, 2, s, scr);
 }
 
 }  // namespace
@@ -466,7 +469,7 @@ bool prefill_supported(const tbh_weight &w) {
 }
 
 hipError_t launch_prefill(const tbh_weight &w, const uint16_t *x, int64_t ldx, int64_t M, float *y,
-                          int64_t ldy, hipStream_t s) {
+                          int64_t ldy, hipStream_t s, const Scratch &scr) {
     if (!prefill_supported(w) || M < 1 || w.K % 8 != 0 || ldx % 8 != 0 ||
         ((uintptr_t)x & 15) != 0)
         return hipErrorInvalidValue;
@@ -487,7 +490,7 @@ hipError_t launch_prefill(const tbh_weight &w, const uint16_t *x, int64_t ldx, i
     p.chunks = (int32_t)(w.Kp / (int8 ? kInt8ChunkElems : kInt4ChunkElems));
     p.G = (int32_t)w.groups_per_row;
     p.cpg = w.chunks_per_group;
-    return int8 ? launch_prec<8>(w, p, s) : launch_prec<4>(w, p, s);
+    return int8 ? launch_prec<8>(w, p, s, scr) : launch_prec<4>(w, p, s, scr);
 }
 
 }  // namespace tbh

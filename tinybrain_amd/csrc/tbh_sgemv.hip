@@ -328,7 +328,7 @@ bool sgemv_supported(const tbh_weight &w) {
     return cpg > 0 && (cpg & (cpg - 1)) == 0 && w.Np % 8 == 0;
 }
 
-hipError_t launch_sgemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s) {
+hipError_t launch_sgemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s, const Scratch &scr) {
     const int M = (int)a.M;
     if (!sgemv_supported(w) || M < 2 || M > 8) return hipErrorInvalidValue;
     if (w.K % 4 != 0 || a.ldx % 4 != 0 || ((uintptr_t)a.x & 15) != 0) return hipErrorInvalidValue;
@@ -369,7 +369,8 @@ hipError_t launch_sgemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s) {
     kchunks = std::min<int64_t>(kchunks, kMaxChunks);
     int64_t splits = (p.chunks + kchunks - 1) / kchunks;
     if (splits > 1) {
-        p.part = (float *)stream_workspace(w.dev, s, (size_t)(splits * M * w.N) * sizeof(float));
+        p.part = (float *)scr.get(s, (size_t)(splits * M * w.N) * sizeof(float));
+        if (!p.part && scr.is_fixed()) return hipErrorOutOfMemory;
         if (!p.part) {
             // no workspace (a graph being captured before any eager call): one
             // split when the whole row fits in one block, else the caller
