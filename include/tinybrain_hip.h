@@ -140,8 +140,11 @@ tbh_status tbh_device_get_info(const tbh_device *dev, int32_t *ordinal, int32_t 
  *   TBH_OPT_SGEMV_MIN_ROWS: fewest rows of x (2..9, 9 = never) that go to the
  *     matrix-core small-M GEMV for every weight; 0 restores the per-weight
  *     rule.  The environment variable TBH_SGEMV_MIN_ROWS, read when the
- *     device opens, sets the initial value. */
-enum { TBH_OPT_SGEMV_MIN_ROWS = 1 };
+ *     device opens, sets the initial value.
+ *   TBH_OPT_NOALLOC_SCRATCH_BYTES: the most scratch bytes
+ *     tbh_matmul_device_noalloc may use on this device, 1 .. 16 MiB; 0 (the
+ *     default) is the whole 16 MiB array.  A call needing more is rejected. */
+enum { TBH_OPT_SGEMV_MIN_ROWS = 1, TBH_OPT_NOALLOC_SCRATCH_BYTES = 2 };
 tbh_status tbh_device_set_option(tbh_device *dev, int32_t option, int64_t value);
 
 /* ---- weights ----------------------------------------------------------- */
@@ -168,6 +171,20 @@ tbh_status tbh_matmul(tbh_device *dev, const float *x, int64_t M, int64_t K,
  * weight's device; NULL = the null stream).  Returns after the launch. */
 tbh_status tbh_matmul_device(const tbh_weight *w, const float *x, int64_t M,
                              int64_t K, float *y, void *stream);
+
+/* No reference counterpart.  tbh_matmul_device for callers that cannot
+ * allocate device memory: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc.  Same product, same kernels, same
+ * arguments; the split-K partial sums of the matrix-core small-M GEMV go to a
+ * fixed 16 MiB scratch array per GPU (held until the process ends) instead of
+ * a per-stream workspace, and the call makes no allocation.  A call whose
+ * launch would need more than 16 MiB of scratch returns TBH_E_INVALID before
+ * enqueueing anything (decode shapes need at most a few MiB).  Every call on
+ * one GPU shares that GPU's array: calls that overlap on one GPU (different
+ * streams, or graphs replayed concurrently) race and must be serialised by
+ * the caller. */
+tbh_status tbh_matmul_device_noalloc(const tbh_weight *w, const float *x, int64_t M,
+                                     int64_t K, float *y, void *stream);
 
 /* Replaces LinearLayerWeights.apply(toRow:)
  * (Sources/TinyBrainRuntime/ModelWeights.swift:47-68): y = x . dequantize(w)

@@ -19,15 +19,15 @@ LAYOUT_KN_FLAT, LAYOUT_NK_FLAT = 0, 1
 PATH_INT8_ROW, PATH_INT4_KGROUP, PATH_INT4_NGROUP, PATH_GENERIC = range(4)
 PATH_NAMES = {0: "int8_row", 1: "int4_kgroup", 2: "int4_ngroup", 3: "generic"}
 # device options (tbh_device_set_option)
-OPT_SGEMV_MIN_ROWS = 1
+OPT_SGEMV_MIN_ROWS, OPT_NOALLOC_SCRATCH_BYTES = 1, 2
 
 # every symbol the header declares
 EXPORTS = [
     "tbh_abi_version", "tbh_last_error", "tbh_status_string",
     "tbh_device_open", "tbh_device_close", "tbh_device_get_info", "tbh_device_set_option",
     "tbh_weight_create", "tbh_weight_destroy", "tbh_weight_get_info",
-    "tbh_matmul", "tbh_matmul_device", "tbh_matmul_bf16_device", "tbh_linear_device",
-    "tbh_dequantize", "tbh_dequantize_device",
+    "tbh_matmul", "tbh_matmul_device", "tbh_matmul_device_noalloc", "tbh_matmul_bf16_device",
+    "tbh_linear_device", "tbh_dequantize", "tbh_dequantize_device",
     "tbh_decoder_create", "tbh_decoder_set_layer", "tbh_decoder_destroy",
     "tbh_decoder_set_position", "tbh_decoder_get_position",
     "tbh_decoder_step_device", "tbh_decoder_step",
@@ -155,6 +155,7 @@ def lib() -> ctypes.CDLL:
     L.tbh_weight_get_info.argtypes = [vp, ctypes.POINTER(WeightInfo)]
     L.tbh_matmul.argtypes = [vp, vp, i64, i64, vp, vp]
     L.tbh_matmul_device.argtypes = [vp, vp, i64, i64, vp, vp]
+    L.tbh_matmul_device_noalloc.argtypes = [vp, vp, i64, i64, vp, vp]
     L.tbh_linear_device.argtypes = [vp, vp, i64, i64, vp, vp, vp]
     L.tbh_matmul_bf16_device.argtypes = [vp, vp, i64, i64, vp, vp]
     L.tbh_dequantize.argtypes = [vp, vp, vp]
@@ -197,7 +198,8 @@ def lib() -> ctypes.CDLL:
         getattr(L, name).restype = i32
     for name in ("tbh_device_open", "tbh_device_close", "tbh_device_get_info", "tbh_device_set_option",
                  "tbh_weight_create", "tbh_weight_destroy", "tbh_weight_get_info",
-                 "tbh_matmul", "tbh_matmul_device", "tbh_matmul_bf16_device", "tbh_linear_device",
+                 "tbh_matmul", "tbh_matmul_device", "tbh_matmul_device_noalloc", "tbh_matmul_bf16_device",
+                 "tbh_linear_device",
                  "tbh_dequantize", "tbh_dequantize_device",
                  "tbh_softmax", "tbh_softmax_device", "tbh_rmsnorm", "tbh_rmsnorm_device",
                  "tbh_silu", "tbh_silu_device", "tbh_gelu", "tbh_gelu_device",

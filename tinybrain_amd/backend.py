@@ -174,6 +174,23 @@ class HIPBackend:
                                            out.data_ptr(), ctypes.c_void_p(s.cuda_stream)))
         return out
 
+    def matmul_device_noalloc(self, x, weight: DeviceWeight, out=None, stream=None):
+        """matmul_device through tbh_matmul_device_noalloc: no device memory
+        is allocated by the call (for code under graph capture); `out` must
+        then be given.  Calls overlapping on one GPU race on its scratch."""
+        import torch
+
+        if x.dim() != 2 or x.shape[1] != weight.K:
+            raise PreconditionFailure("Dimensions must match")
+        if x.dtype != torch.float32 or not x.is_contiguous() or not x.is_cuda:
+            raise PreconditionFailure("x must be a contiguous float32 device tensor")
+        if out is None or tuple(out.shape) != (x.shape[0], weight.N) or not out.is_contiguous():
+            raise PreconditionFailure("out must be a contiguous float32 [M, N] device tensor")
+        s = stream if stream is not None else torch.cuda.current_stream(x.device)
+        _check(self._lib.tbh_matmul_device_noalloc(weight.handle, x.data_ptr(), x.shape[0], x.shape[1],
+                                                   out.data_ptr(), ctypes.c_void_p(s.cuda_stream)))
+        return out
+
     def linear_device(self, x, weight: DeviceWeight, bias=None, out=None, stream=None):
         """Enqueue y = x . W (+ bias[n] on every row) on a HIP stream
         (tbh_linear_device; LinearLayerWeights.apply(toRow:),

@@ -11,6 +11,15 @@
 
 #include "tbh_internal.h"
 
+// Device memory of tbh_matmul_device_noalloc: its split-K partial sums live
+// here instead of in a per-stream workspace, so the call never allocates.
+// Each GPU the library runs on holds its own copy of the array (its own
+// address, looked up once per device in tbh_device_open) until the process
+// ends.  Host code only ever uses that looked-up address: the array's name
+// in host code is a host-side stand-in, not device memory.
+static constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
 namespace tbh {
 
 namespace {
@@ -107,6 +116,11 @@ tbh_status tbh_device_open(int32_t ordinal, tbh_device **out) {
     TBH_HIP(hipSetDevice(ordinal), "hipSetDevice");
     auto dev = std::make_unique<tbh_device>();
     dev->ordinal = ordinal;
+    // this device's copy of the no-allocation scratch array (device `ordinal`
+    // is current here)
+    TBH_HIP(hipGetSymbolAddress(&dev->noalloc_scratch, HIP_SYMBOL(scratch)),
+            "tbh_device_open: scratch address");
+    if (!dev->noalloc_scratch) return set_error(TBH_E_HIP, "tbh_device_open: scratch address is NULL");
     dev->cu_count = prop.multiProcessorCount;
     if (const char *v = std::getenv("TBH_SGEMV_MIN_ROWS"); v && *v)   // read once, at open
         dev->sgemv_min_rows.store(std::min(9, std::max(2, std::atoi(v))), std::memory_order_relaxed);
@@ -137,6 +151,12 @@ tbh_status tbh_device_set_option(tbh_device *dev, int32_t option, int64_t value)
         if (value != 0 && (value < 2 || value > 9))
             return set_error(TBH_E_INVALID, "TBH_OPT_SGEMV_MIN_ROWS takes 0 (per-weight rule) or 2..9");
         dev->sgemv_min_rows.store((int)value, std::memory_order_relaxed);
+        return TBH_OK;
+    case TBH_OPT_NOALLOC_SCRATCH_BYTES:
+        if (value < 0 || value > (int64_t)kNoAllocScratchBytes)
+            return set_error(TBH_E_INVALID, "TBH_OPT_NOALLOC_SCRATCH_BYTES takes 0 (all of it) or 1 .. " +
+                                                std::to_string(kNoAllocScratchBytes));
+        dev->noalloc_limit.store(value, std::memory_order_relaxed);
         return TBH_OK;
     default: return set_error(TBH_E_INVALID, "tbh_device_set_option: unknown option");
     }
@@ -707,6 +727,24 @@ tbh_status tbh_matmul_device(const tbh_weight *w, const float *x, int64_t M, int
     if (st != TBH_OK) return st;
     Scratch scr;
     scr.dev = w->dev;
+    return matmul_enqueue(w, x, M, y, (hipStream_t)stream, scr);
+}
+
+tbh_status tbh_matmul_device_noalloc(const tbh_weight *w, const float *x, int64_t M, int64_t K, float *y,
+                                     void *stream) {
+    if (!w) return set_error(TBH_E_INVALID, "tbh_matmul_device_noalloc: weight is NULL");
+    if (M < 0) return set_error(TBH_E_INVALID, "tbh_matmul_device_noalloc: M < 0");
+    if (K != w->K) return set_error(TBH_E_INVALID, "Dimensions must match (x K != weight K)");
+    if (M == 0) return TBH_OK;
+    if (!x || !y) return set_error(TBH_E_INVALID, "tbh_matmul_device_noalloc: x or y is NULL");
+    if (!w->dev->noalloc_scratch)
+        return set_error(TBH_E_INVALID, "tbh_matmul_device_noalloc: device has no scratch address");
+    tbh_status st = use_device(w->dev->ordinal);
+    if (st != TBH_OK) return st;
+    const int64_t limit = w->dev->noalloc_limit.load(std::memory_order_relaxed);
+    Scratch scr;
+    scr.fixed = w->dev->noalloc_scratch;
+    scr.fixed_bytes = limit > 0 ? (size_t)limit : kNoAllocScratchBytes;
     return matmul_enqueue(w, x, M, y, (hipStream_t)stream, scr);
 }
 

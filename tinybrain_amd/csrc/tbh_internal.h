@@ -54,6 +54,8 @@ struct tbh_device {
     std::atomic<int> sgemv_min_rows{0};   // TBH_OPT_SGEMV_MIN_ROWS; 0 = per-weight rule
     void *stage = nullptr;       // device staging for the host-pointer calls
     size_t stage_bytes = 0;
+    void *noalloc_scratch = nullptr;   // this GPU's scratch array (tbh_matmul_device_noalloc)
+    std::atomic<int64_t> noalloc_limit{0};   // TBH_OPT_NOALLOC_SCRATCH_BYTES; 0 = the whole array
 
     // Per-stream device workspaces (split-K partial sums): calls on different
     // streams never share one.  A workspace that has to grow is replaced, not
