@@ -143,8 +143,11 @@ tbh_status tbh_device_get_info(const tbh_device *dev, int32_t *ordinal, int32_t 
  *     device opens, sets the initial value.
  *   TBH_OPT_NOALLOC_SCRATCH_BYTES: the most scratch bytes
  *     tbh_matmul_device_noalloc may use on this device, 1 .. 16 MiB; 0 (the
- *     default) is the whole 16 MiB array.  A call needing more is rejected. */
-enum { TBH_OPT_SGEMV_MIN_ROWS = 1, TBH_OPT_NOALLOC_SCRATCH_BYTES = 2 };
+ *     default) is the whole 16 MiB array.  A call needing more is rejected.
+ *   TBH_OPT_MFMA_MIN_ROWS: fewest rows of fp32 x that tbh_matmul* send to the
+ *     MFMA GEMM (x split exactly into bf16 pieces) for every weight; 0
+ *     restores the per-weight rule. */
+enum { TBH_OPT_SGEMV_MIN_ROWS = 1, TBH_OPT_NOALLOC_SCRATCH_BYTES = 2, TBH_OPT_MFMA_MIN_ROWS = 3 };
 tbh_status tbh_device_set_option(tbh_device *dev, int32_t option, int64_t value);
 
 /* ---- weights ----------------------------------------------------------- */
@@ -163,7 +166,11 @@ tbh_status tbh_weight_get_info(const tbh_weight *w, tbh_weight_info *info);
  * MetalBackend.matmulQuantized / matmulINT4 (MetalBackend.swift:894-1048):
  * y[M,N] = x[M,K] . dequantize(w)[K,N] with fp32 accumulation.
  * Host pointers; synchronous (the reference commits and waits, :959-960).
- * Calls on one device are serialised. */
+ * Calls on one device are serialised.  Like the Metal kernels, one call
+ * covers any M (MetalBackend.swift:949-956): a few rows run on the GEMV
+ * kernels; from a per-weight row count (8..64, TBH_OPT_MFMA_MIN_ROWS) INT8
+ * rows and INT4 K-group weights without zero points run on the bf16 MFMA
+ * GEMM with every fp32 x row split exactly into three bf16 pieces. */
 tbh_status tbh_matmul(tbh_device *dev, const float *x, int64_t M, int64_t K,
                       const tbh_weight *w, float *y);
 
@@ -175,9 +182,9 @@ tbh_status tbh_matmul_device(const tbh_weight *w, const float *x, int64_t M,
 /* No reference counterpart.  tbh_matmul_device for callers that cannot
  * allocate device memory: code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc.  Same product, same kernels, same
- * arguments; the split-K partial sums of the matrix-core small-M GEMV go to a
- * fixed 16 MiB scratch array per GPU (held until the process ends) instead of
- * a per-stream workspace, and the call makes no allocation.  A call whose
+ * arguments; the split-K partial sums (matrix-core small-M GEMV, MFMA GEMM)
+ * go to a fixed 16 MiB scratch array per GPU (held until the process ends)
+ * instead of a per-stream workspace, and the call makes no allocation.  A call whose
  * launch would need more than 16 MiB of scratch returns TBH_E_INVALID before
  * enqueueing anything (decode shapes need at most a few MiB).  Every call on
  * one GPU shares that GPU's array: calls that overlap on one GPU (different

@@ -87,6 +87,20 @@ def test_decode_tinyllama_width(backend):
     dec.close()
 
 
+def test_decode_7b_width(backend):
+    # 7B layer shapes with 2 of the 32 layers: INT4
+    # group 32 along K, hidden 4096, 32 query and 32 KV heads (head_dim 128,
+    # one query head per KV head), FFN 11008, vocab 32000
+    cfg = T.DecoderConfig(num_layers=2, hidden=4096, num_heads=32, num_kv_heads=32, intermediate=11008,
+                          vocab=32000, max_seq=64)
+    dec, ref = _model(backend, cfg, "int4", seed=23)
+    for i, tok in enumerate([1, 31999, 450, 7]):
+        y = dec.step(tok)
+        r = ref.step(tok)
+        assert _gated(y, r) <= GATE, (i, _gated(y, r))
+    dec.close()
+
+
 @pytest.mark.parametrize("heads", [(4, 2), (16, 2), (8, 8)])
 def test_decode_long_context(backend, heads):
     # more than two 64-position attention ranges, so the step's attention

@@ -298,8 +298,10 @@ def test_device_resident_entry_point(backend):
 @pytest.fixture
 def sgemv_from_two_rows(backend):
     backend.set_option(_abi.OPT_SGEMV_MIN_ROWS, 2)   # the MFMA path for every M >= 2
+    backend.set_option(_abi.OPT_MFMA_MIN_ROWS, 1 << 30)   # and never the GEMM: M = 16 as two 8-row launches
     yield
     backend.set_option(_abi.OPT_SGEMV_MIN_ROWS, 0)
+    backend.set_option(_abi.OPT_MFMA_MIN_ROWS, 0)
 
 
 @pytest.mark.parametrize("M", [2, 3, 4, 5, 6, 7, 9, 16])
@@ -438,6 +440,122 @@ def test_workspace_growth_keeps_captured_graphs_valid(backend, sgemv_from_two_ro
             torch.cuda.synchronize()
             assert O.parity_errors(y_small.cpu().numpy(), ref_small)["gated"] <= GATE
         del g, junk
+
+
+# ---------------------------------------------------------------------------
+# many rows of fp32 x on the MFMA GEMM: each row split exactly into three bf16
+# pieces (tbh_matmul / tbh_matmul_device from the per-weight row threshold)
+# ---------------------------------------------------------------------------
+@pytest.fixture
+def mfma_from(backend):
+    def set_rows(rows):
+        backend.set_option(_abi.OPT_MFMA_MIN_ROWS, rows)
+    yield set_rows
+    backend.set_option(_abi.OPT_MFMA_MIN_ROWS, 0)
+
+
+def test_fp32_mfma_reference_shapes(backend, mfma_from):
+    # QuantizationTests.swift:117-135 (128 x 256 @ 256 x 512) and :137-151
+    # (10 x 768 @ 768 x 3072), INT8 per channel: through the rule (M = 128)
+    # and with the GEMM forced from one row (M = 10)
+    for (M, K, N), rows in (((128, 256, 512), 0), ((10, 768, 3072), 1)):
+        mfma_from(rows)
+        qt = _int8_pc(151 + K, K, N)
+        _check(backend, _product(qt, (K, N)), qt, Ms=(M,), seed=3)
+        # the reference's own bound: within 1% (L2) of the fp32 product
+        x = O.fill_normal(152 + M, M * K).reshape(M, K)
+        w = O.fill_normal(151 + K, K * N, std=0.02).reshape(K, N)
+        y = backend.matmulQuantized(x, _product(qt, (K, N)))
+        ref = x.astype(np.float64) @ w.astype(np.float64)
+        assert np.linalg.norm(y - ref) / np.linalg.norm(ref) < 0.01
+
+
+@pytest.mark.parametrize("prec,K,N,M", [
+    ("int8", 2048, 5632, 16), ("int8", 2048, 5632, 128), ("int8", 1000, 777, 33), ("int8", 64, 40, 300),
+    ("int4", 5632, 2048, 17), ("int4", 2048, 5632, 64), ("int4", 4096, 1000, 200), ("int4", 96, 24, 70),
+])
+def test_fp32_mfma_shapes(backend, prec, K, N, M):
+    # ragged M (the last row quad of a tile partly past M), ragged K and N,
+    # K-split and unsplit launches
+    if prec == "int8":
+        oq = _int8_pc(161 + K + M, K, N)
+        pq = _product(oq, (K, N))
+    else:
+        oq = _int4_nk(163 + K + M, K, N, 32)
+        pq = _product(oq, (K, N), T.Layout.NK_FLAT)
+    _check(backend, pq, oq, Ms=(M,), seed=7)
+
+
+def test_fp32_mfma_every_small_m(backend, mfma_from):
+    # forced from one row: M = 1 .. 9 as whole and ragged row quads
+    mfma_from(1)
+    qt = _int4_nk(171, 1024, 300, 64)
+    pq = _product(qt, (1024, 300), T.Layout.NK_FLAT)
+    _check(backend, pq, qt, Ms=(1, 2, 3, 4, 5, 7, 9), seed=9)
+
+
+def test_fp32_mfma_exact_split(backend, mfma_from):
+    # x values whose 24 significant bits all matter, across the exponent
+    # range, and zero rows: the three bf16 pieces carry x exactly, so the
+    # result stays within the matmul gate of the float64 product
+    mfma_from(1)
+    K, N, M = 512, 256, 8
+    qt = _int8_pc(181, K, N)
+    pq = _product(qt, (K, N))
+    W = O.dequantize(qt)
+    rng = np.random.default_rng(182)
+    mant = rng.integers(1 << 23, 1 << 24, size=(M, K)).astype(np.float64) / (1 << 23)
+    sign = np.where(rng.random((M, K)) < 0.5, -1.0, 1.0)
+    expo = rng.integers(-60, 60, size=(M, 1)).astype(np.float64)
+    expo[6], expo[7] = 100, -100
+    x = (sign * mant * np.exp2(expo)).astype(np.float32)
+    x[3] = 0.0
+    x[5, ::2] = 0.0
+    y = backend.matmulQuantized(x, pq)
+    y64 = O.gemm_f64(x, W)
+    for m in range(M):
+        assert O.parity_errors(y[m:m + 1], y64[m:m + 1])["gated"] <= GATE, m
+    assert np.all(y[3] == 0.0)
+    # error against sum_k |x_k w_kn|: fp32 accumulation gives about
+    # sqrt(K) 2^-24 (at most K 2^-24 = 3e-5); a split that kept only the
+    # upper 16 bits of x would give about 2^-9
+    mag = np.abs(x.astype(np.float64)) @ np.abs(W.astype(np.float64))
+    with np.errstate(invalid="ignore"):
+        rel = np.where(mag > 0, np.abs(y - y64) / mag, 0.0)
+    assert float(rel.max()) < 3e-5
+
+
+def test_fp32_mfma_device_and_graph(backend):
+    # tbh_matmul_device through the rule (M = 64): bit-identical across calls
+    # and graph replays, equal to the host entry point
+    import torch
+
+    K, N, M = 2048, 2048, 64
+    oq = _int4_nk(191, K, N, 32)
+    pq = _product(oq, (K, N), T.Layout.NK_FLAT)
+    w = backend.weight(pq)
+    xh = O.fill_normal(192, M * K).reshape(M, K)
+    host = backend.matmulQuantized(xh, pq)
+    x = torch.from_numpy(xh).cuda()
+    s = torch.cuda.Stream()
+    y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        backend.matmul_device(x, w, out=y, stream=s)
+    torch.cuda.synchronize()
+    eager = y.cpu().numpy().copy()
+    np.testing.assert_array_equal(eager, host)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        backend.matmul_device(x, w, out=y, stream=s)
+    for _ in range(3):
+        y.zero_()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(y.cpu().numpy(), eager)
+    del g
 
 
 # ---------------------------------------------------------------------------

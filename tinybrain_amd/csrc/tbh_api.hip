@@ -152,6 +152,11 @@ tbh_status tbh_device_set_option(tbh_device *dev, int32_t option, int64_t value)
             return set_error(TBH_E_INVALID, "TBH_OPT_SGEMV_MIN_ROWS takes 0 (per-weight rule) or 2..9");
         dev->sgemv_min_rows.store((int)value, std::memory_order_relaxed);
         return TBH_OK;
+    case TBH_OPT_MFMA_MIN_ROWS:
+        if (value < 0 || value > INT32_MAX)
+            return set_error(TBH_E_INVALID, "TBH_OPT_MFMA_MIN_ROWS takes 0 (per-weight rule) or a row count");
+        dev->mfma_min_rows.store((int)value, std::memory_order_relaxed);
+        return TBH_OK;
     case TBH_OPT_NOALLOC_SCRATCH_BYTES:
         if (value < 0 || value > (int64_t)kNoAllocScratchBytes)
             return set_error(TBH_E_INVALID, "TBH_OPT_NOALLOC_SCRATCH_BYTES takes 0 (all of it) or 1 .. " +
@@ -681,10 +686,37 @@ static int64_t sgemv_min_rows(const tbh_weight &w) {
     return 9;
 }
 
+// Fewest rows of fp32 x that go to the MFMA GEMM (each row split exactly into
+// three bf16 pieces; launch_prefill_f32) instead of the GEMV kernels, which
+// stream the whole weight once per 2..8 rows.  Measured crossovers, us per
+// call GEMV / GEMM: INT8 5632x2048 M = 8 13.5 / 10.9; INT8 2048x2048 M = 8
+// 7.5 / 7.9, M = 12 10.7 / 8.0; INT4 2048x2048 M = 12 11.4 / 10.1 (M = 8
+// 7.8 / 9.7); INT4 4096x11008 M = 32 61.0 / 44.6; INT4 11008x4096 M = 32
+// 56.5 / 49.9 (M = 24 42.2 / 49.1); INT4 32000x2048 M = 64 101.7 / 67.5
+// (M = 48 76.5 / 78.4).
+static int64_t mfma_min_rows(const tbh_weight &w) {
+    const int64_t nk = w.N * w.K;
+    if (w.precision == TBH_PREC_INT8) return nk >= ((int64_t)8 << 20) ? 8 : 12;
+    if (nk <= ((int64_t)24 << 20)) return 12;
+    return w.N >= 16384 ? 64 : 32;
+}
+
 static tbh_status matmul_enqueue(const tbh_weight *w, const float *x, int64_t M, float *y,
                                  hipStream_t s, const Scratch &scr) {
     if (!weight_arrays_ok(*w))
         return set_error(TBH_E_INVALID, "weight device arrays are inconsistent with its layout");
+    const int mfma_forced = w->dev->mfma_min_rows.load(std::memory_order_relaxed);
+    const int64_t mfma_min = mfma_forced > 0 ? mfma_forced : mfma_min_rows(*w);
+    if (M >= mfma_min && prefill_supported(*w) && !w->zp && w->K % 8 == 0 && ((uintptr_t)x & 15) == 0) {
+        const hipError_t e = launch_prefill_f32(*w, x, w->K, M, y, w->N, s, scr);
+        if (e == hipSuccess) return TBH_OK;
+        if (e == hipErrorOutOfMemory && scr.is_fixed())
+            return set_error(TBH_E_INVALID, "this call needs " + std::to_string(scr.shortfall) +
+                                                " bytes of scratch; the no-allocation entry point holds " +
+                                                std::to_string(scr.fixed_bytes));
+        if (e != hipErrorInvalidValue) return hip_error(e, "matmul kernel launch");
+        // shapes the GEMM does not take run on the GEMV kernels below
+    }
     // 2..8 rows of x per launch on the matrix cores when the weight allows
     // it and M reaches sgemv_min_rows; below that the VALU kernels are as
     // fast or faster.  The device option TBH_OPT_SGEMV_MIN_ROWS sets one

@@ -52,6 +52,7 @@ struct tbh_device {
     hipStream_t stream = nullptr;
     std::mutex mu;               // serialises tbh_matmul / tbh_dequantize
     std::atomic<int> sgemv_min_rows{0};   // TBH_OPT_SGEMV_MIN_ROWS; 0 = per-weight rule
+    std::atomic<int> mfma_min_rows{0};    // TBH_OPT_MFMA_MIN_ROWS; 0 = per-weight rule
     void *stage = nullptr;       // device staging for the host-pointer calls
     size_t stage_bytes = 0;
     void *noalloc_scratch = nullptr;   // this GPU's scratch array (tbh_matmul_device_noalloc)
@@ -175,6 +176,14 @@ hipError_t launch_generic(const tbh_weight &w, const GemvArgs &a, hipStream_t s)
 bool prefill_supported(const tbh_weight &w);
 hipError_t launch_prefill(const tbh_weight &w, const uint16_t *x, int64_t ldx, int64_t M, float *y,
                           int64_t ldy, hipStream_t s, const Scratch &scr);
+
+// The same GEMM for fp32 x [M][ldx] (16-byte aligned rows, K % 8 == 0, no
+// zero points): each x row is split exactly into three bf16 pieces and a zero
+// row, the four rows go through the bf16 MFMAs, and the epilogue adds each
+// row's four results (tbh_prefill.hip).  hipErrorInvalidValue for weights or
+// shapes it does not take.
+hipError_t launch_prefill_f32(const tbh_weight &w, const float *x, int64_t ldx, int64_t M, float *y,
+                              int64_t ldy, hipStream_t s, const Scratch &scr);
 
 // Device workspace of at least `bytes` owned by (dev, stream), grown on
 // demand (tbh_api.hip).  Growing allocates a new buffer and keeps the old one

@@ -39,6 +39,7 @@ constexpr int kDepth = 2;         // K steps whose global loads are in flight at
 
 struct PParams {
     const uint16_t *x;   // bf16 bits, [M][ldx]
+    const float *xf;     // fp32 mode: x as fp32 [Mout][ldx], row r of the product = piece r % 4 of row r / 4
     int64_t ldx;
     float *y;            // [M][ldy]; with split-K, split z writes y + z * split_stride
     int64_t ldy;
@@ -49,6 +50,7 @@ struct PParams {
     const float *scales;
     const int8_t *zp;
     int32_t M, K, N, Np;
+    int32_t Mout;    // output rows: M, or M / 4 in fp32 mode
     int32_t chunks;  // 16-byte chunks per row
     int32_t G;       // INT4 K-groups per row
     int32_t cpg;     // chunks per K-group
@@ -67,13 +69,33 @@ __device__ __forceinline__ uint32_t pack_hi16(float lo_elem, float hi_elem) {
                                  __builtin_bit_cast(uint32_t, lo_elem), 0x07060302u);
 }
 
+// A 32-bit word as fp32.  By value: __builtin_bit_cast applied directly to
+// an element of an ext_vector_type value (v[1]) reads element 0.
+__device__ __forceinline__ float as_f32(uint32_t u) { return __builtin_bit_cast(float, u); }
+
+// An fp32 value split exactly into three bf16 values, x = p[0] + p[1] + p[2]:
+// p[0] keeps the upper 16 bits of x, p[1] the upper 16 bits of the exact
+// remainder x - p[0] (at most 16 significant bits), p[2] the rest (at most 8
+// significant bits, so exact in bf16).  Non-finite x stays in p[0].
+__device__ __forceinline__ void split3(float x, float (&p)[3]) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, x);
+    p[0] = __builtin_bit_cast(float, b & 0xFFFF0000u);
+    const float r1 = (b & 0x7F800000u) != 0x7F800000u ? x - p[0] : 0.0f;
+    p[1] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, r1) & 0xFFFF0000u);
+    p[2] = r1 - p[1];
+}
+
 // Byte J of w as fp32 (v_cvt_f32_ubyteJ).
 template <int J>
 __device__ __forceinline__ float ubyte(uint32_t w) {
     return (float)((w >> (8 * J)) & 0xFFu);
 }
 
-template <int PREC, int BM, int BN, bool ZP, int WV, int BK>
+// XF (fp32 x): product row r is piece r % 4 of x row r / 4 (split3; piece 3
+// is zero), so
+// the four rows a lane holds in each 16 x 16 accumulator tile are the pieces
+// of one x row, and the epilogue adds them into that row's output.
+template <int PREC, int BM, int BN, bool ZP, int WV, int BK, bool XF>
 __global__ __launch_bounds__(64 * WV) void gemm_bf16(const PParams p) {
     constexpr int kLdsRow = BK + kRowPad;
     constexpr int NT = 64 * WV;                   // threads; waves as 2 x (WV / 2)
@@ -111,8 +133,13 @@ __global__ __launch_bounds__(64 * WV) void gemm_bf16(const PParams p) {
 
     // ---- global -> registers for one step, into register stage d of kDepth:
     // the loads of steps t+1 .. t+kDepth-1 are in flight while step t runs
-    u32x4 xr[kDepth][XPT];
-    bool xin[kDepth][XPT];   // segment within K, applied at the LDS store
+    // fp32 x: a segment is 8 fp32 of one x row (two 16-byte loads), staged
+    // as the four product rows of its pieces
+    constexpr int XSEGF = (BM / 4) * (BK / 8);
+    constexpr int XPTF = XF ? (XSEGF + NT - 1) / NT : 1;
+    constexpr int XPTL = XF ? XPTF : XPT;
+    u32x4 xr[kDepth][XPTL][XF ? 2 : 1];
+    bool xin[kDepth][XPTL];   // segment within K, applied at the LDS store
     u32x4 wr[kDepth][WPT];
     float sr[kDepth][WPT];
     int8_t zq[kDepth][WPT];
@@ -120,15 +147,28 @@ __global__ __launch_bounds__(64 * WV) void gemm_bf16(const PParams p) {
     // (masks, conversions) happens in store_step, kDepth - 1 steps later.
     auto load_step = [&](int t, int d) {
         const int k0 = t * BK;
+        if constexpr (XF) {
 #pragma unroll
-        for (int j = 0; j < XPT; ++j) {
-            const int s = tid + NT * j;
-            const int row = s / (BK / 8), kq = s % (BK / 8);
-            const int m = min(m0 + row, p.M - 1), k = k0 + 8 * kq;
-            // K % 8 == 0: a segment is all in or out.  Rows past M read row
-            // M-1 (finite values; their outputs are never stored).
-            xin[d][j] = k < kend;
-            xr[d][j] = *(const u32x4 *)(p.x + (int64_t)m * p.ldx + (k < p.K ? k : 0));
+            for (int j = 0; j < XPTF; ++j) {
+                const int s = min(tid + NT * j, XSEGF - 1);   // threads past the last segment repeat it
+                const int qrow = s / (BK / 8), kq = s % (BK / 8);
+                const int m = min(m0 / 4 + qrow, p.Mout - 1), k = k0 + 8 * kq;
+                xin[d][j] = k < kend;
+                const float *src = p.xf + (int64_t)m * p.ldx + (k < p.K ? k : 0);
+                xr[d][j][0] = *(const u32x4 *)src;
+                xr[d][j][XF ? 1 : 0] = *(const u32x4 *)(src + 4);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < XPT; ++j) {
+                const int s = tid + NT * j;
+                const int row = s / (BK / 8), kq = s % (BK / 8);
+                const int m = min(m0 + row, p.M - 1), k = k0 + 8 * kq;
+                // K % 8 == 0: a segment is all in or out.  Rows past M read row
+                // M-1 (finite values; their outputs are never stored).
+                xin[d][j] = k < kend;
+                xr[d][j][0] = *(const u32x4 *)(p.x + (int64_t)m * p.ldx + (k < p.K ? k : 0));
+            }
         }
 #pragma unroll
         for (int j = 0; j < WPT; ++j) {
@@ -152,11 +192,37 @@ __global__ __launch_bounds__(64 * WV) void gemm_bf16(const PParams p) {
 
     // ---- registers -> LDS (x as is; weights dequantized to bf16 pieces)
     auto store_step = [&](int d, int bb) {
+        if constexpr (XF) {
+            // segment (quad row qrow, kq) -> product rows 4 qrow + piece
 #pragma unroll
-        for (int j = 0; j < XPT; ++j) {
-            const int s = tid + NT * j;
-            const int row = s / (BK / 8), kq = s % (BK / 8);
-            *(u32x4 *)&xs[bb][row * kLdsRow + 8 * kq] = xin[d][j] ? xr[d][j] : u32x4{0, 0, 0, 0};
+            for (int j = 0; j < XPTF; ++j) {
+                const int s = tid + NT * j;
+                if (s < XSEGF) {
+                    const int qrow = s / (BK / 8), kq = s % (BK / 8);
+                    float pc[8][3];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        split3(xin[d][j] ? as_f32(xr[d][j][0][e]) : 0.0f, pc[e]);
+                        split3(xin[d][j] ? as_f32(xr[d][j][XF ? 1 : 0][e]) : 0.0f, pc[4 + e]);
+                    }
+                    uint16_t *dst = &xs[bb][(4 * qrow) * kLdsRow + 8 * kq];
+#pragma unroll
+                    for (int piece = 0; piece < 3; ++piece) {
+                        uint32_t o[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) o[e] = pack_hi16(pc[2 * e][piece], pc[2 * e + 1][piece]);
+                        *(u32x4 *)(dst + piece * kLdsRow) = u32x4{o[0], o[1], o[2], o[3]};
+                    }
+                    *(u32x4 *)(dst + 3 * kLdsRow) = u32x4{0, 0, 0, 0};
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < XPT; ++j) {
+                const int s = tid + NT * j;
+                const int row = s / (BK / 8), kq = s % (BK / 8);
+                *(u32x4 *)&xs[bb][row * kLdsRow + 8 * kq] = xin[d][j] ? xr[d][j][0] : u32x4{0, 0, 0, 0};
+            }
         }
 #pragma unroll
         for (int j = 0; j < WPT; ++j) {
@@ -265,6 +331,21 @@ __global__ __launch_bounds__(64 * WV) void gemm_bf16(const PParams p) {
     // ---- epilogue: lane holds C[4 (lane / 16) + e][lane % 16] of each tile
     float *out = p.y + (int64_t)blockIdx.z * p.split_stride;
     const int mrow = m0 + wm * WM + 4 * (lane >> 4), ncol = n0 + wn * WN + (lane & 15);
+    if constexpr (XF) {
+        // the lane's four rows are the pieces of x row (mrow + 16 a) / 4
+#pragma unroll
+        for (int b = 0; b < TN; ++b) {
+            const int n = ncol + b * 16;
+            if (n >= p.N) continue;
+#pragma unroll
+            for (int a = 0; a < TM; ++a) {
+                const int m = (mrow + a * 16) >> 2;
+                const float v = ((acc[a][b][0] + acc[a][b][1]) + acc[a][b][2]) + acc[a][b][3];
+                if (m < p.Mout) out[(int64_t)m * p.ldy + n] = v * scn[b];
+            }
+        }
+        return;
+    }
     if (m0 + BM <= p.M && n0 + BN <= p.N) {
         // whole tile in range: no per-element branches
 #pragma unroll
@@ -342,12 +423,16 @@ hipError_t launch_tile(const PParams &p, int splits, hipStream_t s) {
     }();
     const dim3 grid((unsigned)((p.Np + BN - 1) / BN), (unsigned)((p.M + BM - 1) / BM), (unsigned)splits);
     const bool w8 = waves == 8 || (waves != 4 && BN == 128 && (p.M >= 256 || PREC == 4));
-    if (p.zp) {
-        if (w8) hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, true, 8, BK>), grid, dim3(512), 0, s, p);
-        else hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, true, 4, BK>), grid, dim3(256), 0, s, p);
+    if (p.xf) {   // fp32 x (no zero points: the API routes those elsewhere)
+        if (p.zp) return hipErrorInvalidValue;
+        if (w8) hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, false, 8, BK, true>), grid, dim3(512), 0, s, p);
+        else hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, false, 4, BK, true>), grid, dim3(256), 0, s, p);
+    } else if (p.zp) {
+        if (w8) hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, true, 8, BK, false>), grid, dim3(512), 0, s, p);
+        else hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, true, 4, BK, false>), grid, dim3(256), 0, s, p);
     } else {
-        if (w8) hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, false, 8, BK>), grid, dim3(512), 0, s, p);
-        else hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, false, 4, BK>), grid, dim3(256), 0, s, p);
+        if (w8) hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, false, 8, BK, false>), grid, dim3(512), 0, s, p);
+        else hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, false, 4, BK, false>), grid, dim3(256), 0, s, p);
     }
     return hipGetLastError();
 }
@@ -380,7 +465,7 @@ hipError_t launch_split(const tbh_weight &w, PParams p, int64_t tiles, int bpc, 
         splits = (nsteps + sps - 1) / sps;
     }
     float *const y = p.y;
-    const int64_t n = (int64_t)p.M * p.N;
+    const int64_t n = (int64_t)p.Mout * p.N;
     float *part = nullptr;
     if (splits > 1) {
         part = (float *)scr.get(s, (size_t)(splits * n) * sizeof(float));
@@ -468,6 +553,37 @@ bool prefill_supported(const tbh_weight &w) {
     return !w.mfma_tiles && (w.path == Path::Int8Row || w.path == Path::Int4KGroup);
 }
 
+static PParams prefill_params(const tbh_weight &w, int64_t ldx, float *y, int64_t ldy) {
+    PParams p{};
+    p.ldx = ldx;
+    p.y = y;
+    p.ldy = ldy;
+    p.data = w.data;
+    p.row_bytes = w.row_bytes;
+    p.scales = w.scales;
+    p.zp = w.zp;
+    p.K = (int32_t)w.K;
+    p.N = (int32_t)w.N;
+    p.Np = (int32_t)w.Np;
+    const bool int8 = w.precision == TBH_PREC_INT8;
+    p.chunks = (int32_t)(w.Kp / (int8 ? kInt8ChunkElems : kInt4ChunkElems));
+    p.G = (int32_t)w.groups_per_row;
+    p.cpg = w.chunks_per_group;
+    return p;
+}
+
+hipError_t launch_prefill_f32(const tbh_weight &w, const float *x, int64_t ldx, int64_t M, float *y,
+                              int64_t ldy, hipStream_t s, const Scratch &scr) {
+    if (!prefill_supported(w) || w.zp || M < 1 || 4 * M > INT32_MAX || w.K % 8 != 0 || ldx % 4 != 0 ||
+        ((uintptr_t)x & 15) != 0)
+        return hipErrorInvalidValue;
+    PParams p = prefill_params(w, ldx, y, ldy);
+    p.xf = x;
+    p.M = (int32_t)(4 * M);
+    p.Mout = (int32_t)M;
+    return w.precision == TBH_PREC_INT8 ? launch_prec<8>(w, p, s, scr) : launch_prec<4>(w, p, s, scr);
+}
+
 hipError_t launch_prefill(const tbh_weight &w, const uint16_t *x, int64_t ldx, int64_t M, float *y,
                           int64_t ldy, hipStream_t s, const Scratch &scr) {
     if (!prefill_supported(w) || M < 1 || w.K % 8 != 0 || ldx % 8 != 0 ||
@@ -483,6 +599,7 @@ hipError_t launch_prefill(const tbh_weight &w, const uint16_t *x, int64_t ldx, i
     p.scales = w.scales;
     p.zp = w.zp;
     p.M = (int32_t)M;
+    p.Mout = (int32_t)M;
     p.K = (int32_t)w.K;
     p.N = (int32_t)w.N;
     p.Np = (int32_t)w.Np;
