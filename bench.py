@@ -16,8 +16,9 @@ each launched from HIP graphs of at most one pool sweep.
 value = algorithmic bytes of all GEMVs in the timed steps / wall time (GB/s),
 algorithmic bytes per GEMV = W + S + Z + 4*M*K + 4*M*N.
 The roofline object reports the dominant kernel (32000x2048) timed with HIP
-events on its own stream over back-to-back launches (--roctx-regions marks
-exactly those launches for ``rocprofv3 --selected-regions``).  cpu_baseline
+events on its own stream over back-to-back launches; they are that kernel's
+last launches in the run, which ``--trace-summary`` averages from a rocprofv3
+kernel trace.  cpu_baseline
 times the restated reference CPU path (dequantize() single-threaded, then
 sgemm on every host CPU this process may use, capped by the CPU share
 OMP_NUM_THREADS grants) on a bounded sample of the same workload.  The
@@ -135,36 +136,6 @@ def cpu_threads() -> int:
     on, capped by the CPU share the environment grants (OMP_NUM_THREADS)."""
     h = host_info()
     return max(1, min(h["affinity_cpus"], h["omp_num_threads"] or h["affinity_cpus"]))
-
-
-class Roctx:
-    """roctxProfilerResume / roctxProfilerPause (rocprofiler-sdk roctx), so that
-    ``rocprofv3 --selected-regions`` records only the launches a roofline
-    figure is measured on.  No-ops when the library is absent or no profiler
-    is attached."""
-
-    def __init__(self, enabled: bool):
-        self._lib = None
-        if enabled:
-            import ctypes
-
-            for name in ("librocprofiler-sdk-roctx.so.1", "librocprofiler-sdk-roctx.so"):
-                try:
-                    self._lib = ctypes.CDLL(name)
-                    break
-                except OSError:
-                    continue
-            if self._lib is not None:
-                self._lib.roctxProfilerPause.argtypes = [ctypes.c_uint64]
-                self._lib.roctxProfilerResume.argtypes = [ctypes.c_uint64]
-
-    def resume(self):
-        if self._lib is not None:
-            self._lib.roctxProfilerResume(0)
-
-    def pause(self):
-        if self._lib is not None:
-            self._lib.roctxProfilerPause(0)
 
 
 def step_graphs(torch, stream, launch_step, n_steps: int, per_graph: int, first: int = 0):
@@ -303,13 +274,11 @@ def run_prefill(args, backend, T, torch):
     del check
     warm_graphs = step_graphs(torch, cap, step, args.warmup, n_sets)
     timed_graphs = step_graphs(torch, cap, step, args.steps, n_sets, first=args.warmup)
-    roctx = Roctx(args.roctx_regions)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(cap):
         for g in warm_graphs:
             g.replay()
         torch.cuda.synchronize()
-        roctx.resume()
         t0 = time.perf_counter()
         e0.record(cap)
         for g in timed_graphs:
@@ -317,7 +286,6 @@ def run_prefill(args, backend, T, torch):
         e1.record(cap)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        roctx.pause()
     steps_done = args.steps
     kern_us = e0.elapsed_time(e1) * 1e3 / steps_done
     flops = 2.0 * M * N * K
@@ -738,6 +706,38 @@ def run_op(args, backend, T, torch):
     backend.close()
 
 
+def trace_summary(path: str, kernel_re: str, last: int) -> None:
+    """Markdown summary of a rocprofv3 kernel-trace CSV: per kernel, calls and
+    average / min / max duration over all dispatches; with --kernel and
+    --last, also over the last `last` dispatches of the matching kernel (the
+    launches a bench line's roofline kernel time is measured on: the dominant
+    shape's timed graph replays are its final launches in the run)."""
+    import csv
+    import re
+
+    rows = []
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            rows.append((int(r["Start_Timestamp"]), r["Kernel_Name"],
+                         int(r["End_Timestamp"]) - int(r["Start_Timestamp"])))
+    rows.sort()
+    per = {}
+    for _, name, d in rows:
+        per.setdefault(name, []).append(d)
+    print("| kernel | calls | avg us | min us | max us |")
+    print("|---|---|---|---|---|")
+    for name, ds in sorted(per.items(), key=lambda kv: -sum(kv[1])):
+        print(f"| `{name[:90]}` | {len(ds)} | {np.mean(ds) / 1e3:.3f} | {min(ds) / 1e3:.3f} | "
+              f"{max(ds) / 1e3:.3f} |")
+    if kernel_re and last > 0:
+        match = [(t, n, d) for t, n, d in rows if re.search(kernel_re, n)]
+        tail = [d for _, _, d in match[-last:]]
+        print()
+        print(f"Last {len(tail)} of {len(match)} dispatches matching `{kernel_re}`: "
+              f"avg {np.mean(tail) / 1e3:.3f} us, median {np.median(tail) / 1e3:.3f} us, "
+              f"min {min(tail) / 1e3:.3f} us, max {max(tail) / 1e3:.3f} us")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -750,14 +750,18 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-decode", action="store_true",
                     help="int4_g32_gemv_m1: leave out the 1.1B decode-step measurement")
-    ap.add_argument("--roctx-regions", action="store_true",
-                    help="mark the launches the roofline kernel time is measured on with "
-                         "roctxProfilerResume/Pause, for rocprofv3 --selected-regions")
+    ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
+                    help="summarise a rocprofv3 --kernel-trace CSV (no GPU work): per-kernel averages over "
+                         "all dispatches and over the last --last dispatches of kernels matching --kernel")
+    ap.add_argument("--kernel", default="", help="--trace-summary: kernel-name regex")
+    ap.add_argument("--last", type=int, default=0, help="--trace-summary: trailing dispatches to average")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="for rocprofv3 --pmc: 5 plain copies of 64 MiB (calibration kernel of "
                          "known size) then 20 launches of the dominant GEMV; no timing")
     args = ap.parse_args()
 
+    if args.trace_summary:
+        return trace_summary(args.trace_summary, args.kernel, args.last)
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; the GEMV would shard along N "
                                    "(see DESIGN.md) but no multi-GPU path is built", "n_gpus": args.gpus}))
@@ -862,9 +866,8 @@ def main():
     # ---- per-shape kernel time: a graph of n_sets back-to-back launches of
     # one shape, bracketed by HIP events on the replay stream
     per_shape = {}
-    shape_us = {}
+    shape_us, shape_n = {}, {}
     jd = int(np.argmax([alg_bytes(prec, gs, N, K, M) for N, K in shapes]))
-    roctx = Roctx(args.roctx_regions)
     for j, (N, K) in enumerate(shapes):
         g1 = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g1, stream=cap):
@@ -877,18 +880,15 @@ def main():
         with torch.cuda.stream(cap):
             g1.replay()
             torch.cuda.synchronize()
-            if j == jd:
-                roctx.resume()        # rocprofv3 --selected-regions: these launches only
             e0.record(cap)
             for _ in range(nrep):
                 g1.replay()
             e1.record(cap)
         e1.synchronize()
-        if j == jd:
-            roctx.pause()
         us = e0.elapsed_time(e1) * 1e3 / (nrep * n_sets)
         b = alg_bytes(prec, gs, N, K, M)
         shape_us[j] = us
+        shape_n[j] = nrep * n_sets
         per_shape[f"{N}x{K}"] = {"us": round(us, 3), "GB_s": round(b / us / 1e3, 1),
                                  "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
                                  "path": pool[0][j].path}
@@ -934,6 +934,7 @@ def main():
             "kernel": f"{Nd}x{Kd} ({pool[0][jd].path})",
             "kernel_us": round(kern_us, 3),
             "alg_bytes_per_launch": kbytes,
+            "timed_dispatches": shape_n[jd],
         },
         "per_shape": per_shape,
         "setup_s": round(setup_s, 1),
