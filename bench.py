@@ -47,6 +47,9 @@ WORKLOADS = {
     "int4_g32_gemv_m4": ("int4", 32, [(2048, 2048), (5632, 2048), (2048, 5632), (32000, 2048)], 4),
     "int4_g32_gemv_m8": ("int4", 32, [(2048, 2048), (5632, 2048), (2048, 5632), (32000, 2048)], 8),
     "int8_pc_gemv_m1": ("int8", 0, [(5632, 2048)], 1),
+    # the same shapes in the runtime layout Tensor.quantize(.int4) writes
+    # (groups of 32 along N of the [K, N] weight)
+    "int4_g32_gemv_m1_runtime": ("int4kn", 32, [(2048, 2048), (5632, 2048), (2048, 5632), (32000, 2048)], 1),
 }
 
 # Prefill: x [M x K] bf16 N(0,1), one dequant-GEMM on
@@ -86,7 +89,7 @@ RIDGE_FLOP_PER_BYTE = MFMA_BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
 
 
 def alg_bytes(prec: str, gs: int, N: int, K: int, M: int) -> int:
-    if prec == "int4":
+    if prec in ("int4", "int4kn"):
         w = (K * N + 1) // 2
         s = 4 * ((K * N + gs - 1) // gs)
     else:
@@ -164,6 +167,8 @@ def make_weight(prec: str, gs: int, N: int, K: int, seed: int):
     w_nk = rng.normal(0.0, 0.02, size=(N, K)).astype(np.float32)
     if prec == "int4":
         return T.quantize_int4_flat(w_nk, gs, shape=(K, N), layout=T.Layout.NK_FLAT)
+    if prec == "int4kn":     # runtime layout: [K, N] flattened, groups along N
+        return T.quantize_int4_flat(np.ascontiguousarray(w_nk.T), gs, layout=T.Layout.KN_FLAT)
     return T.quantize(np.ascontiguousarray(w_nk.T), T.QuantizationMode.perChannel)
 
 
@@ -900,7 +905,9 @@ def main():
 
     out = {
         "metric": (f"dequant-GEMV GB/s and % of HBM peak (INT4 g32, M={M}, 4 BASELINE shapes)"
-                   if prec == "int4" else f"dequant-GEMV GB/s and % of HBM peak (INT8 per-channel, M={M})"),
+                   if prec == "int4" else
+                   f"dequant-GEMV GB/s and % of HBM peak (INT4 g32 runtime layout, M={M}, 4 BASELINE shapes)"
+                   if prec == "int4kn" else f"dequant-GEMV GB/s and % of HBM peak (INT8 per-channel, M={M})"),
         "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -914,8 +921,9 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": args.workload,
-            "weights": "INT4 symmetric, group 32 along K (converter layout)" if prec == "int4"
-            else "INT8 symmetric per output channel",
+            "weights": {"int4": "INT4 symmetric, group 32 along K (converter layout)",
+                        "int4kn": "INT4 symmetric, group 32 along N (runtime layout, Tensor.quantize(.int4))",
+                        "int8": "INT8 symmetric per output channel"}[prec],
             "shapes_NxK": [f"{N}x{K}" for N, K in shapes],
             "gpu_us_per_step": round(gpu_step_us, 3),
             "M": M,

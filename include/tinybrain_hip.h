@@ -248,8 +248,10 @@ tbh_status tbh_decoder_create(tbh_device *dev, const tbh_decoder_config *cfg,
  * seven projections as [K, N] quantized tensors (q [hidden, hidden], k and v
  * [hidden, kv_dim], o [hidden, hidden], gate and up [hidden, intermediate],
  * down [intermediate, hidden]).  Q|K|V and gate|up are concatenated along N
- * into one repacked weight each.  Needs INT8 runtime-layout or INT4
- * converter-layout (K-group) weights without zero points. */
+ * into one repacked weight each.  Needs weights without zero points: INT8
+ * in the runtime layout, INT4 in the converter layout (groups along K) or
+ * INT4 in the runtime layout (Tensor.quantize(.int4), groups along N) whose
+ * groups tile every projection's N. */
 tbh_status tbh_decoder_set_layer(tbh_decoder *d, int32_t layer, const float *input_norm,
                                  const float *post_attention_norm,
                                  const tbh_qtensor_desc *q, const tbh_qtensor_desc *k,

@@ -29,6 +29,12 @@ def _weight(prec, seed, K, N, std=0.02):
         pq = T.QuantizedTensor((K, N), qt.data, qt.scales, qt.mode, qt.precision, qt.group_size,
                                qt.zero_points, T.Layout.KN_FLAT)
         return pq, O.dequantize(qt)
+    if prec == "int4kn":
+        # Tensor.quantize(.int4) on [K, N]: the runtime layout, groups of 32 along N
+        qt = O.quantize_int4(O.fill_normal(seed, K * N, std=std).reshape(K, N), 32, O.ROUND_SWIFT)
+        pq = T.QuantizedTensor((K, N), qt.data, qt.scales, qt.mode, qt.precision, qt.group_size,
+                               qt.zero_points, T.Layout.KN_FLAT)
+        return pq, O.dequantize(qt)
     qt = O.quantize_int4(O.fill_normal(seed, N * K, std=std).reshape(N, K), 32, O.ROUND_SWIFT)
     pq = T.QuantizedTensor((K, N), qt.data, qt.scales, qt.mode, qt.precision, qt.group_size,
                            qt.zero_points, T.Layout.NK_FLAT)
@@ -63,9 +69,11 @@ SMALL = dict(num_layers=2, hidden=256, num_heads=4, num_kv_heads=2, intermediate
              max_seq=32)
 
 
-@pytest.mark.parametrize("prec", ["int8", "int4"])
+@pytest.mark.parametrize("prec", ["int8", "int4", "int4kn"])
 def test_decode_small(backend, prec):
-    cfg = T.DecoderConfig(**SMALL)
+    # int4kn: the runtime INT4 layout (groups along N) needs a vocabulary the
+    # groups tile
+    cfg = T.DecoderConfig(**dict(SMALL, vocab=1024 if prec == "int4kn" else SMALL["vocab"]))
     dec, ref = _model(backend, cfg, prec, seed=11)
     for i, tok in enumerate([5, 17, 3, 999, 0, 42, 7, 7, 512, 1]):
         y = dec.step(tok)
@@ -81,6 +89,21 @@ def test_decode_tinyllama_width(backend):
                           vocab=32000, max_seq=64)
     dec, ref = _model(backend, cfg, "int8", seed=21)
     for i, tok in enumerate([1, 31999, 450]):
+        y = dec.step(tok)
+        r = ref.step(tok)
+        assert _gated(y, r) <= GATE, (i, _gated(y, r))
+    dec.close()
+
+
+def test_decode_tinyllama_width_runtime_int4(backend):
+    # TinyLlama-1.1B layer shapes, 2 layers, INT4 in the runtime layout that
+    # Tensor.quantize(.int4) and the perplexity harness write (groups of 32
+    # along N): Q|K|V concatenated, gate|up rows interleaved with one scale
+    # table per part
+    cfg = T.DecoderConfig(num_layers=2, hidden=2048, num_heads=32, num_kv_heads=4, intermediate=5632,
+                          vocab=32000, max_seq=64)
+    dec, ref = _model(backend, cfg, "int4kn", seed=27)
+    for i, tok in enumerate([1, 31999, 450, 9]):
         y = dec.step(tok)
         r = ref.step(tok)
         assert _gated(y, r) <= GATE, (i, _gated(y, r))
@@ -183,7 +206,8 @@ def test_decode_graph_replay_advances_position(backend):
     graphed.close()
 
 
-def test_decode_runtime_int4_layout_is_unsupported(backend):
+def test_decode_mixed_precision_qkv_is_rejected(backend):
+    # Q in INT4 (runtime layout), K and V in INT8: Q|K|V cannot be one weight
     cfg = T.DecoderConfig(**dict(SMALL, num_layers=1))
     H, kv, I = cfg.hidden, cfg.kv_dim, cfg.intermediate
     lm, _ = _weight("int8", 1, H, cfg.vocab)

@@ -195,6 +195,23 @@ def test_int4_runtime_layout(backend, K, N, gs, path):
     assert w.path == path
 
 
+@pytest.mark.parametrize("K,N,gs", [
+    (2048, 32000, 32),    # configs[1] shapes in the runtime layout, I = 1, U = 4
+    (2048, 5632, 32), (5632, 2048, 32),   # I = 3
+    (2048, 2048, 64),
+    (11008, 4096, 32),    # I = 6 (7B down projection)
+    (4096, 11008, 128),
+    (1024, 64, 128),      # group spans two k rows: every output shares each k-block's scale
+    (160, 96, 32),        # one chunk iteration, ragged
+])
+def test_int4_runtime_layout_burst(backend, K, N, gs):
+    # Tensor.quantize(.int4) weights (groups along N) on the burst GEMV: each
+    # block stages x times its N-block's per-k scale row
+    qt = _int4_kn(K + N + gs, K, N, gs)
+    w = _check(backend, _product(qt, (K, N)), qt, Ms=(1, 2, 4), cpu_path=False)
+    assert w.path == "int4_ngroup"
+
+
 def test_int4_zero_points(backend):
     qt = _int4_nk(91, 256, 24, 32)
     qt.zero_points = ((np.arange(qt.scales.size) % 7) - 3).astype(np.int8)

@@ -570,6 +570,74 @@ tbh_status tbh_weight_create(tbh_device *dev, const tbh_qtensor_desc *desc, tbh_
     return TBH_OK;
 }
 
+}  // extern "C"
+
+// Two INT4 runtime-layout weights (groups along N) of one shape as one weight
+// whose row 2j is a's output j and row 2j + 1 is b's: the decoder's gate|up
+// projection, whose GEMV epilogue pairs the two rows.  Scales: a's per-k
+// table then b's, nb_half N-blocks each.
+tbh_status tbh::create_ngroup_pair(tbh_device *dev, const tbh_qtensor_desc *a, const tbh_qtensor_desc *b,
+                                   tbh_weight **out) {
+    *out = nullptr;
+    for (const tbh_qtensor_desc *d : {a, b}) {
+        tbh_status st = validate_desc(d);
+        if (st != TBH_OK) return st;
+        if (d->precision != TBH_PREC_INT4 || d->layout != TBH_LAYOUT_KN_FLAT || d->group_size <= 0 ||
+            any_nonzero(d->zero_points, d->n_zero_points))
+            return set_error(TBH_E_UNSUPPORTED, "pair weight: needs INT4 runtime-layout weights without zero points");
+    }
+    if (a->K != b->K || a->N != b->N || a->group_size != b->group_size)
+        return set_error(TBH_E_INVALID, "pair weight: the two weights differ in shape or group size");
+    const int64_t K = a->K, Nh = a->N, gs = a->group_size;
+    int64_t rpn;
+    if (Nh % gs == 0) rpn = gs;            // groups of gs outputs share a scale per k
+    else if (gs % Nh == 0) rpn = 0;        // every output of a k-block shares one scale
+    else return set_error(TBH_E_UNSUPPORTED, "pair weight: groups must tile N");
+    tbh_status st = use_device(dev->ordinal);
+    if (st != TBH_OK) return st;
+    std::unique_ptr<tbh_weight, void (*)(tbh_weight *)> w(new tbh_weight, free_weight);
+    w->dev = dev;
+    w->K = K;
+    w->N = 2 * Nh;
+    w->precision = TBH_PREC_INT4;
+    w->mode = TBH_MODE_INT4;
+    w->layout = TBH_LAYOUT_KN_FLAT;
+    w->group_size = (int32_t)gs;
+    w->path = Path::Int4NGroup;
+    w->ng_pairs = true;
+    w->Kp = round_up(K, kInt4ChunkElems);
+    w->Np = round_up(2 * Nh, 8);
+    w->row_bytes = w->Kp / 2;
+    w->rows_per_nblock = (int32_t)(rpn ? rpn : w->Np);
+    const int64_t NBh = rpn ? (Nh + rpn - 1) / rpn : 1;
+    w->nb_half = (int32_t)NBh;
+    const std::vector<int8_t> qa = expand_nk(*a), qb = expand_nk(*b);
+    std::vector<int8_t> q((size_t)(2 * Nh * K));
+    for (int64_t j = 0; j < Nh; ++j) {
+        std::memcpy(&q[(size_t)(2 * j * K)], &qa[(size_t)(j * K)], (size_t)K);
+        std::memcpy(&q[(size_t)((2 * j + 1) * K)], &qb[(size_t)(j * K)], (size_t)K);
+    }
+    std::vector<uint8_t> packed;
+    pack_int4_rows(q, K, 2 * Nh, w->Kp, w->Np, packed);
+    std::vector<float> t((size_t)(2 * NBh * w->Kp), 0.0f);
+    for (int c = 0; c < 2; ++c) {
+        const tbh_qtensor_desc &d = c == 0 ? *a : *b;
+        for (int64_t nb = 0; nb < NBh; ++nb) {
+            const int64_t n = rpn ? nb * rpn : 0;
+            for (int64_t k = 0; k < K; ++k) t[(size_t)((c * NBh + nb) * w->Kp + k)] = d.scales[(k * Nh + n) / gs];
+        }
+    }
+    hipError_t e = upload(&w->data, packed.data(), packed.size(), w->device_bytes, w->n_data);
+    if (e == hipSuccess) e = upload(&w->scales, t.data(), t.size(), w->device_bytes, w->n_scales_dev);
+    if (e != hipSuccess) return hip_error(e, "pair weight: upload");
+    w->stream_bytes = 2 * ((K * Nh + 1) / 2 + 4 * a->n_scales);
+    if (!weight_arrays_ok(*w)) return set_error(TBH_E_INVALID, "pair weight: internal layout inconsistency");
+    *out = w.release();
+    return TBH_OK;
+}
+
+extern "C" {
+
 tbh_status tbh_weight_destroy(tbh_weight *w) {
     if (!w) return TBH_OK;
     use_device(w->dev->ordinal);
@@ -628,6 +696,7 @@ bool weight_arrays_ok(const tbh_weight &w) {
     }
     if (w.path == Path::Int4NGroup) {
         if (w.rows_per_nblock <= 0 || w.zp) return false;
+        if (w.ng_pairs) return w.nb_half > 0 && w.n_scales_dev == 2 * (int64_t)w.nb_half * w.Kp;
         const int64_t nb = (w.Np + w.rows_per_nblock - 1) / w.rows_per_nblock;
         return w.n_scales_dev == nb * w.Kp;
     }

@@ -380,7 +380,9 @@ int64_t expected_scales(const tbh_qtensor_desc &d) {
 // part's outputs in order.  INT8: the runtime [K][N] layout with one scale
 // per column or per tensor (a per-tensor scale is repeated per column).
 // INT4: the converter layout (groups of group_size along K, K % group_size ==
-// 0, even K * N_i), where concatenation is of the flat arrays.
+// 0, even K * N_i), where concatenation is of the flat arrays; or the runtime
+// [K][N] layout with groups along N (N_i % group_size == 0), where each k
+// row of the result is the parts' k rows (and their scales) side by side.
 tbh_status concat_n(const tbh_qtensor_desc *const *parts, int n, OwnedDesc &out) {
     for (int i = 0; i < n; ++i) {
         const tbh_qtensor_desc *d = parts[i];
@@ -422,6 +424,30 @@ tbh_status concat_n(const tbh_qtensor_desc *const *parts, int n, OwnedDesc &out)
         out.d.mode = TBH_MODE_PER_CHANNEL;
         out.d.data_bytes = K * N;
         out.d.n_scales = N;
+    } else if (parts[0]->layout == TBH_LAYOUT_KN_FLAT) {
+        const int32_t gs = parts[0]->group_size;
+        for (int i = 0; i < n; ++i)
+            if (parts[i]->layout != TBH_LAYOUT_KN_FLAT || parts[i]->mode != TBH_MODE_INT4 ||
+                parts[i]->group_size != gs || gs <= 0 || parts[i]->N % gs != 0 || gs % 2 != 0 ||
+                parts[i]->data_bytes != K * parts[i]->N / 2)
+                return set_error(TBH_E_UNSUPPORTED,
+                                 "decoder: runtime-layout INT4 weights need groups that tile N");
+        out.data.resize((size_t)(K * N / 2));
+        out.scales.resize((size_t)(K * N / gs));
+        if (has_zp) out.zp.resize(out.scales.size());
+        int64_t off = 0;   // in outputs
+        for (int i = 0; i < n; ++i) {
+            const tbh_qtensor_desc &d = *parts[i];
+            const int64_t ng = d.N / gs;
+            for (int64_t k = 0; k < K; ++k) {
+                std::memcpy(&out.data[(size_t)((k * N + off) / 2)], d.data + k * d.N / 2, (size_t)(d.N / 2));
+                std::memcpy(&out.scales[(size_t)((k * N + off) / gs)], d.scales + k * ng, (size_t)ng * sizeof(float));
+                if (has_zp) std::memcpy(&out.zp[(size_t)((k * N + off) / gs)], d.zero_points + k * ng, (size_t)ng);
+            }
+            off += d.N;
+        }
+        out.d.data_bytes = (int64_t)out.data.size();
+        out.d.n_scales = (int64_t)out.scales.size();
     } else {
         const int32_t gs = parts[0]->group_size;
         for (int i = 0; i < n; ++i)
@@ -495,6 +521,18 @@ void interleave_halves(OwnedDesc &od) {
 // interleave: two parts of equal N whose outputs alternate (gate|up rows).
 tbh_status make_weight(tbh_decoder *dec, const tbh_qtensor_desc *const *parts, int n, int64_t K,
                        int64_t N, tbh_weight **out, bool interleave = false) {
+    if (interleave && n == 2 && parts[0] && parts[1] && parts[0]->precision == TBH_PREC_INT4 &&
+        parts[0]->layout == TBH_LAYOUT_KN_FLAT) {
+        // runtime-layout INT4: a block's rows must share their N-block's
+        // scale per k, so the pair is built with one scale table per part
+        if (parts[0]->K != K || parts[1]->K != K || parts[0]->N + parts[1]->N != N)
+            return set_error(TBH_E_INVALID, "decoder: projection shape mismatch");
+        tbh_status st = create_ngroup_pair(dec->dev, parts[0], parts[1], out);
+        if (st != TBH_OK) return st;
+        if (!gemv_fused_supported(**out))
+            return set_error(TBH_E_UNSUPPORTED, "decoder: gate|up projection needs the burst GEMV path");
+        return TBH_OK;
+    }
     OwnedDesc od;
     tbh_status st = n == 1 ? TBH_OK : concat_n(parts, n, od);
     if (st != TBH_OK) return st;

@@ -58,6 +58,7 @@ struct KParams {
     int32_t cpg;     // chunks per K-group
     int32_t cpg_shift;  // log2(cpg) when cpg is a power of two, else -1
     int32_t rpn;     // rows per N-block (INT4 runtime layout)
+    int32_t nb_half; // INT4 runtime layout, gate|up rows interleaved: N-blocks of the first part
     int32_t x_vec4;  // x rows are 16-byte aligned and K % 4 == 0
     // fused decode prologue / epilogue (gemv_burst with M = 1 only)
     const float *g;    // PRO_RMSNORM: norm weight [K]
@@ -66,8 +67,6 @@ struct KParams {
     int32_t *advance;  // non-null: block 0 adds 1 to advance[0]
 };
 
-// expf at full precision (not the hardware exp2 approximation).
-__device__ __forceinline__ float __expf_exact(float v) { return expf(v); }
 
 __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
     return (a & m) | o;  // v_and_or_b32 when m and o are registers (see opaque)
@@ -425,14 +424,23 @@ __device__ __forceinline__ void lds_barrier() {
 // for the oldest outstanding load.  The grid is not persistent: one wave
 // per U rows, so a launch issues the whole matrix's reads in its first
 // microsecond when it fits the GPU, and HBM latency is paid about once.
-// INT8 rows (one scale per row) and INT4 K-groups without zero points.
-template <int PREC, int M, int U, int I, int PRO, int EPI>
+// INT8 rows (one scale per row) and INT4 K-groups without zero points; and
+// INT4 with groups along N (the runtime layout, NG > 0): rows of one N-block
+// share a scale per k, so the block stages x times that scale row in LDS and
+// the rows need no scale of their own.  NG = 1: the block's rows lie in one
+// N-block; NG = 2 (M = 1): rows alternate between two interleaved weights
+// (gate and up rows), the block stages one scaled copy of x for each, and
+// row u reads copy u & 1.
+template <int PREC, int M, int U, int I, int PRO, int EPI, int NG>
 __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
     constexpr int CE = PREC == 8 ? 16 : 32;
     constexpr int CS = CE + 4;
     constexpr int V = M * U;           // M and U are powers of two
     constexpr int XR = I * CE / 16;    // float4 x loads per thread and x row
+    constexpr int XC = NG == 2 ? 2 : M;   // x copies in LDS
     static_assert(PRO == PRO_NONE || M == 1, "fused prologues take one x row");
+    static_assert(NG == 0 || PREC == 4, "groups along N are INT4 only");
+    static_assert(NG != 2 || (M == 1 && U % 2 == 0), "interleaved pairs: one x row, whole pairs per wave");
     extern __shared__ float4 xs4[];
     __shared__ float red[4];
 
@@ -454,6 +462,21 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
             const float4 t = *(const float4 *)(xr + min(k, p.K - 4));  // x_vec4 holds
             const bool in = k < p.K;
             xv[m][r] = float4{in ? t.x : 0.f, in ? t.y : 0.f, in ? t.z : 0.f, in ? t.w : 0.f};
+        }
+    }
+    // NG: this block's per-k scale row(s), [Kp] each, read like x
+    float4 tv[NG == 2 ? 2 : 1][XR];
+    if constexpr (NG > 0) {
+        const int rb = blockIdx.x * 4 * U;   // the block's first row
+#pragma unroll
+        for (int c = 0; c < (NG == 2 ? 2 : 1); ++c) {
+            const int nb = NG == 2 ? c * p.nb_half + min((rb >> 1) / p.rpn, p.nb_half - 1) : rb / p.rpn;
+            const float *tr = p.scales + (int64_t)nb * p.Kp;
+#pragma unroll
+            for (int r = 0; r < XR; ++r) {
+                const int k = 4 * (tid + 256 * r);
+                tv[c][r] = *(const float4 *)(tr + min(k, p.Kp - 4));   // beyond Kp: x is zero
+            }
         }
     }
     float4 av[XR];  // PRO_RMSNORM: g
@@ -478,7 +501,7 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
         // a shift, not a division: a per-lane integer division here delays
         // every wave's first loads (measured 9.7 -> 9.0 us on 32000x2048)
         const int g = c >> p.cpg_shift;
-        if constexpr (PREC == 4 && U >= 4) {
+        if constexpr (PREC == 4 && NG == 0 && U >= 4) {
             // a row quad's four scales of group g in one 16-byte load, issued
             // ahead of the quad's weights so the first row need not wait for
             // the last load of the wave
@@ -499,7 +522,7 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
             const int row = min(r0 + u, p.Np - 1);
             const uint8_t *rp = p.data + uniform_offset((int64_t)row * p.row_bytes);
             w[i][u] = __builtin_nontemporal_load((const u32x4 *)(rp + (uint32_t)(16 * c)));
-            if (PREC == 4 && U < 4)
+            if (PREC == 4 && NG == 0 && U < 4)
                 s[i][u] = p.scales[(int64_t)(row >> 2) * p.G * 4 + (row & 3) + 4 * g];  // kgroup_index
         }
     }
@@ -550,11 +573,15 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
     // stores are unconditional (zeros beyond K): a conditional store would let
     // the compiler sink its x load behind the weight loads.
 #pragma unroll
-    for (int m = 0; m < M; ++m)
+    for (int m = 0; m < XC; ++m)
 #pragma unroll
         for (int r = 0; r < XR; ++r) {
             const int k = 4 * (tid + 256 * r);
-            float4 t = xv[m][r];
+            float4 t = xv[NG == 2 ? 0 : m][r];
+            if constexpr (NG > 0) {
+                const float4 sc = tv[NG == 2 ? m : 0][r];
+                t = float4{t.x * sc.x, t.y * sc.y, t.z * sc.z, t.w * sc.w};
+            }
             if (PREC == 4) { t.z *= 0.0625f; t.w *= 0.0625f; }
             xs4[(m * lds_row + lds_index<CE>(k)) >> 2] = t;
         }
@@ -578,9 +605,9 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
         const int c = lane + 64 * i;
         if (i < I - 1 || c < p.chunks) {
             constexpr int XQ = CE / 4;  // float4 of x per chunk and x row
-            float4 xq[M][XQ];
+            float4 xq[XC][XQ];
 #pragma unroll
-            for (int m = 0; m < M; ++m)
+            for (int m = 0; m < XC; ++m)
 #pragma unroll
                 for (int q = 0; q < XQ; ++q) xq[m][q] = xs4[(m * lds_row + c * CS + 4 * q) >> 2];
 #pragma unroll
@@ -623,7 +650,8 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
                         const h2 p3 = as_h2(and_or(w8, kHi, kMagic)) + c16;
 #pragma unroll
                         for (int m = 0; m < M; ++m) {
-                            const float4 xa = xq[m][2 * d], xb = xq[m][2 * d + 1];
+                            const int xc = NG == 2 ? (u & 1) : m;   // r0 is even: row r0 + u is a gate row when u is
+                            const float4 xa = xq[xc][2 * d], xb = xq[xc][2 * d + 1];
                             a0[m] = fmix(p0.x, xa.x, a0[m]);
                             a1[m] = fmix(p2.x, xb.x, a1[m]);
                             a0[m] = fmix(p0.y, xa.y, a0[m]);
@@ -636,7 +664,8 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
                     }
 #pragma unroll
                     for (int m = 0; m < M; ++m)
-                        acc[m][u] = __builtin_fmaf(s[i][u], a0[m] + a1[m], acc[m][u]);
+                        acc[m][u] = NG > 0 ? acc[m][u] + (a0[m] + a1[m])
+                                           : __builtin_fmaf(s[i][u], a0[m] + a1[m], acc[m][u]);
                 }
             }
         }
@@ -707,61 +736,65 @@ int env_int(const char *name, int dflt) {
 // wave U a power of two with U * I <= 16.
 constexpr int kBurstMaxI = 6;
 
-template <int PREC, int M, int U, int I, int PRO, int EPI>
+template <int PREC, int M, int U, int I, int PRO, int EPI, int NG>
 hipError_t launch_burst_one(const KParams &p, size_t lds, hipStream_t s) {
-    if constexpr (U * I > 16 || M * U > 32 || (EPI == EPI_SILU_PAIR && (U < 2 || M != 1))) {
+    if constexpr (U * I > 16 || M * U > 32 || (EPI == EPI_SILU_PAIR && (U < 2 || M != 1)) ||
+                  (NG > 0 && PREC != 4) || (NG == 2 && (M != 1 || U % 2 != 0))) {
         return hipErrorInvalidValue;
     } else {
         const int64_t waves = (p.Np + U - 1) / U;
         const unsigned blocks = (unsigned)((waves + 3) / 4);
-        hipLaunchKernelGGL((gemv_burst<PREC, M, U, I, PRO, EPI>), dim3(blocks), dim3(256), lds, s, p);
+        hipLaunchKernelGGL((gemv_burst<PREC, M, U, I, PRO, EPI, NG>), dim3(blocks), dim3(256), lds, s, p);
         return hipGetLastError();
     }
 }
 
-template <int PREC, int M, int I, int PRO, int EPI>
+template <int PREC, int M, int I, int PRO, int EPI, int NG>
 hipError_t burst_u(int U, const KParams &p, size_t lds, hipStream_t s) {
     switch (U) {
-    case 1: return launch_burst_one<PREC, M, 1, I, PRO, EPI>(p, lds, s);
-    case 2: return launch_burst_one<PREC, M, 2, I, PRO, EPI>(p, lds, s);
-    case 4: return launch_burst_one<PREC, M, 4, I, PRO, EPI>(p, lds, s);
-    case 8: return launch_burst_one<PREC, M, 8, I, PRO, EPI>(p, lds, s);
-    case 16: return launch_burst_one<PREC, M, 16, I, PRO, EPI>(p, lds, s);
+    case 1: return launch_burst_one<PREC, M, 1, I, PRO, EPI, NG>(p, lds, s);
+    case 2: return launch_burst_one<PREC, M, 2, I, PRO, EPI, NG>(p, lds, s);
+    case 4: return launch_burst_one<PREC, M, 4, I, PRO, EPI, NG>(p, lds, s);
+    case 8: return launch_burst_one<PREC, M, 8, I, PRO, EPI, NG>(p, lds, s);
+    case 16: return launch_burst_one<PREC, M, 16, I, PRO, EPI, NG>(p, lds, s);
     default: return hipErrorInvalidValue;
     }
 }
 
-template <int PREC, int M, int PRO, int EPI>
+template <int PREC, int M, int PRO, int EPI, int NG = 0>
 hipError_t burst_i(int I, int U, const KParams &p, size_t lds, hipStream_t s) {
     switch (I) {
-    case 1: return burst_u<PREC, M, 1, PRO, EPI>(U, p, lds, s);
-    case 2: return burst_u<PREC, M, 2, PRO, EPI>(U, p, lds, s);
-    case 3: return burst_u<PREC, M, 3, PRO, EPI>(U, p, lds, s);
-    case 4: return burst_u<PREC, M, 4, PRO, EPI>(U, p, lds, s);
-    case 5: return burst_u<PREC, M, 5, PRO, EPI>(U, p, lds, s);
-    case 6: return burst_u<PREC, M, 6, PRO, EPI>(U, p, lds, s);
+    case 1: return burst_u<PREC, M, 1, PRO, EPI, NG>(U, p, lds, s);
+    case 2: return burst_u<PREC, M, 2, PRO, EPI, NG>(U, p, lds, s);
+    case 3: return burst_u<PREC, M, 3, PRO, EPI, NG>(U, p, lds, s);
+    case 4: return burst_u<PREC, M, 4, PRO, EPI, NG>(U, p, lds, s);
+    case 5: return burst_u<PREC, M, 5, PRO, EPI, NG>(U, p, lds, s);
+    case 6: return burst_u<PREC, M, 6, PRO, EPI, NG>(U, p, lds, s);
     default: return hipErrorInvalidValue;
     }
 }
 
-template <int PREC>
+template <int PREC, int NG = 0>
 hipError_t burst_m(int M, int I, int U, const KParams &p, size_t lds, hipStream_t s) {
     switch (M) {
-    case 1: return burst_i<PREC, 1, PRO_NONE, EPI_STORE>(I, U, p, lds, s);
-    case 2: return burst_i<PREC, 2, PRO_NONE, EPI_STORE>(I, U, p, lds, s);
-    case 4: return burst_i<PREC, 4, PRO_NONE, EPI_STORE>(I, U, p, lds, s);
+    case 1: return burst_i<PREC, 1, PRO_NONE, EPI_STORE, NG>(I, U, p, lds, s);
+    case 2: return burst_i<PREC, 2, PRO_NONE, EPI_STORE, NG>(I, U, p, lds, s);
+    case 4: return burst_i<PREC, 4, PRO_NONE, EPI_STORE, NG>(I, U, p, lds, s);
     default: return hipErrorInvalidValue;
     }
 }
 
 // The fused decode variants (M = 1): the prologue / epilogue pairs a decode
-// step uses.
-template <int PREC>
+// step uses.  Interleaved gate|up weights with groups along N take the
+// two-copy form (NG = 2) of the pair epilogue.
+template <int PREC, int NG = 0>
 hipError_t burst_fused(int pro, int epi, int I, int U, const KParams &p, size_t lds, hipStream_t s) {
-    if (pro == PRO_RMSNORM && epi == EPI_STORE) return burst_i<PREC, 1, PRO_RMSNORM, EPI_STORE>(I, U, p, lds, s);
-    if (pro == PRO_NONE && epi == EPI_ACCUMULATE) return burst_i<PREC, 1, PRO_NONE, EPI_ACCUMULATE>(I, U, p, lds, s);
-    if (pro == PRO_RMSNORM && epi == EPI_SILU_PAIR)
-        return burst_i<PREC, 1, PRO_RMSNORM, EPI_SILU_PAIR>(I, U, p, lds, s);
+    if (NG < 2 && pro == PRO_RMSNORM && epi == EPI_STORE)
+        return burst_i<PREC, 1, PRO_RMSNORM, EPI_STORE, NG>(I, U, p, lds, s);
+    if (NG < 2 && pro == PRO_NONE && epi == EPI_ACCUMULATE)
+        return burst_i<PREC, 1, PRO_NONE, EPI_ACCUMULATE, NG>(I, U, p, lds, s);
+    if (NG != 1 && pro == PRO_RMSNORM && epi == EPI_SILU_PAIR)
+        return burst_i<PREC, 1, PRO_RMSNORM, EPI_SILU_PAIR, NG>(I, U, p, lds, s);
     return hipErrorInvalidValue;
 }
 
@@ -798,6 +831,7 @@ KParams make_params(const tbh_weight &w, const GemvArgs &a) {
     for (int sh = 0; sh < 31; ++sh)
         if (p.cpg > 0 && p.cpg == (1 << sh)) p.cpg_shift = sh;
     p.rpn = w.rows_per_nblock;
+    p.nb_half = w.nb_half;
     p.x_vec4 = (w.K % 4 == 0 && a.ldx % 4 == 0 && ((uintptr_t)a.x & 15) == 0) ? 1 : 0;
     p.g = a.x;
     p.eps = 0.0f;
@@ -816,10 +850,13 @@ bool burst_shape(const tbh_weight &w, const KParams &p, int M, int *I_out, int *
     static const int u_force = env_int("TBH_GEMV_U", 0);
     const int I = (p.chunks + 63) / 64;
     const int ce = w.precision == TBH_PREC_INT8 ? kInt8ChunkElems : kInt4ChunkElems;
-    const int64_t blds = (int64_t)M * 64 * I * (ce + 4) * (int64_t)sizeof(float);
+    const bool ng = w.path == Path::Int4NGroup;
+    const int copies = w.ng_pairs ? 2 : M;   // x copies the block stages in LDS
+    const int64_t blds = (int64_t)copies * 64 * I * (ce + 4) * (int64_t)sizeof(float);
     if (kernel_sel || !(M == 1 || M == 2 || M == 4) || w.zp != nullptr || I > kBurstMaxI || !p.x_vec4 ||
-        blds > kMaxLdsBytes || !(w.path == Path::Int8Row || w.path == Path::Int4KGroup) ||
-        (w.path == Path::Int4KGroup && p.cpg_shift < 0) || w.mfma_tiles)
+        blds > kMaxLdsBytes || !(w.path == Path::Int8Row || w.path == Path::Int4KGroup || ng) ||
+        (w.path == Path::Int4KGroup && p.cpg_shift < 0) || w.mfma_tiles || (w.ng_pairs && M != 1) ||
+        (ng && (p.rpn <= 0 || p.Kp % 4 != 0)))
         return false;
     const int64_t cus = std::max(1, w.dev->cu_count);
     // U * I <= 16 weight chunks per lane; M * U <= 32 values in the reduce
@@ -836,6 +873,14 @@ bool burst_shape(const tbh_weight &w, const KParams &p, int M, int *I_out, int *
         while (2 * U * I <= 16 && 2 * U * M <= 32 && w.Np / (2 * U) >= burst_wpc * cus) U *= 2;
     }
     if (u_force > 0 && u_force * I <= 16 && u_force * M <= 32 && (u_force & (u_force - 1)) == 0) U = u_force;
+    if (ng) {
+        // a block's 4 U rows (2 U rows of each weight when interleaved) lie
+        // in one N-block of the scale table
+        if (w.ng_pairs) U = std::max(U, 2);
+        const int per_block = w.ng_pairs ? 2 : 4;
+        while (U > 1 && p.rpn % (per_block * U) != 0) U /= 2;
+        if (p.rpn % (per_block * U) != 0 || (w.ng_pairs && U < 2) || U * I > 16) return false;
+    }
     *I_out = I;
     *U_out = U;
     *lds_out = blds;
@@ -868,13 +913,17 @@ hipError_t launch_gemv_fused(const tbh_weight &w, const FusedGemvArgs &f, hipStr
         if (w.N % 2 != 0 || 2 * I > 16) return hipErrorInvalidValue;
         U = std::max(U, 2);   // both rows of a pair in one wave
     }
-    return w.precision == TBH_PREC_INT8 ? burst_fused<8>(f.prologue, f.epilogue, I, U, p, (size_t)lds, s)
-                                        : burst_fused<4>(f.prologue, f.epilogue, I, U, p, (size_t)lds, s);
+    if (w.ng_pairs != (f.epilogue == EPI_SILU_PAIR && w.path == Path::Int4NGroup)) return hipErrorInvalidValue;
+    if (w.precision == TBH_PREC_INT8) return burst_fused<8>(f.prologue, f.epilogue, I, U, p, (size_t)lds, s);
+    if (w.path == Path::Int4NGroup)
+        return w.ng_pairs ? burst_fused<4, 2>(f.prologue, f.epilogue, I, U, p, (size_t)lds, s)
+                          : burst_fused<4, 1>(f.prologue, f.epilogue, I, U, p, (size_t)lds, s);
+    return burst_fused<4>(f.prologue, f.epilogue, I, U, p, (size_t)lds, s);
 }
 
 hipError_t launch_gemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s) {
     const int M = (int)a.M;
-    if (M < 1 || M > 4) return hipErrorInvalidValue;
+    if (M < 1 || M > 4 || w.ng_pairs) return hipErrorInvalidValue;
     const int64_t lds = lds_bytes_for(w, M);
     if (lds > kMaxLdsBytes) return hipErrorInvalidValue;
     KParams p = make_params(w, a);
@@ -882,9 +931,11 @@ hipError_t launch_gemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s) {
     {
         int I, U;
         int64_t blds;
-        if (burst_shape(w, p, M, &I, &U, &blds))
-            return w.path == Path::Int8Row ? burst_m<8>(M, I, U, p, (size_t)blds, s)
-                                           : burst_m<4>(M, I, U, p, (size_t)blds, s);
+        if (burst_shape(w, p, M, &I, &U, &blds)) {
+            if (w.path == Path::Int8Row) return burst_m<8>(M, I, U, p, (size_t)blds, s);
+            return w.path == Path::Int4NGroup ? burst_m<4, 1>(M, I, U, p, (size_t)blds, s)
+                                              : burst_m<4>(M, I, U, p, (size_t)blds, s);
+        }
     }
 
     // Persistent grid: a few 4-wave blocks per CU.  Rows per wave (R): as

@@ -87,6 +87,11 @@ struct tbh_weight {
     int64_t groups_per_row = 1;  // G (Int4KGroup)
     int32_t chunks_per_group = 1;
     int32_t rows_per_nblock = 1; // Int4NGroup
+    // Int4NGroup built by the decoder from two weights of equal shape whose
+    // rows are interleaved (row 2j: first weight's j, row 2j + 1: second's):
+    // scales are both weights' tables stacked, nb_half N-blocks each.
+    bool ng_pairs = false;
+    int32_t nb_half = 0;
     bool mfma_tiles = false;     // data in 1 KiB MFMA tiles (else K-contiguous rows)
 
     // generic path: the reference arrays as given
@@ -111,6 +116,12 @@ tbh_status set_error(tbh_status st, const std::string &msg);
 tbh_status hip_error(hipError_t e, const char *what);
 // Makes `ordinal` the calling thread's current HIP device (tbh_api.hip).
 tbh_status use_device(int32_t ordinal);
+
+// Two INT4 runtime-layout weights (groups along N) of one shape as one
+// Int4NGroup weight with their rows interleaved (row 2j: a's j, row 2j + 1:
+// b's j) for the decode step's gate|up pair epilogue (tbh_api.hip).
+tbh_status create_ngroup_pair(tbh_device *dev, const tbh_qtensor_desc *a, const tbh_qtensor_desc *b,
+                              tbh_weight **out);
 
 // Host-side check, before any launch, that the device arrays a weight's
 // kernels index exist and have the sizes those kernels assume.

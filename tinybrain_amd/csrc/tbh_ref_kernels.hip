@@ -195,6 +195,7 @@ hipError_t launch_generic(const tbh_weight &w, const GemvArgs &a, hipStream_t s)
 }
 
 hipError_t launch_dequant(const tbh_weight &w, float *out, hipStream_t s) {
+    if (w.ng_pairs) return hipErrorInvalidValue;   // decoder-internal interleaved weights
     DequantParams p{};
     p.out = out;
     p.K = w.K;
