@@ -875,7 +875,12 @@ bool burst_shape(const tbh_weight &w, const KParams &p, int M, int *I_out, int *
     if (u_force > 0 && u_force * I <= 16 && u_force * M <= 32 && (u_force & (u_force - 1)) == 0) U = u_force;
     if (ng) {
         // a block's 4 U rows (2 U rows of each weight when interleaved) lie
-        // in one N-block of the scale table
+        // in one N-block of the scale table.  Eight rows per wave make a
+        // block cover a 32-row N-block, so each scale row is read by one
+        // block instead of two (runtime layout, us per launch U = 4 / 8:
+        // 32000x2048 10.30 / 9.25, 5632x2048 4.19 / 4.00; 2048x2048 3.13 /
+        // 3.52 with too few waves)
+        if (u_force == 0 && M == 1 && !w.ng_pairs && 8 * I <= 16 && p.rpn % 32 == 0 && w.Np >= 4096) U = 8;
         if (w.ng_pairs) U = std::max(U, 2);
         const int per_block = w.ng_pairs ? 2 : 4;
         while (U > 1 && p.rpn % (per_block * U) != 0) U /= 2;
