@@ -98,11 +98,13 @@ def alg_bytes(prec: str, gs: int, N: int, K: int, M: int) -> int:
     return w + s + 4 * M * K + 4 * M * N
 
 
-def profiled_traffic(prec: str, N: int, K: int, M: int):
+def profiled_traffic(prec: str, N: int, K: int, M: int, kind: str = ""):
     """HBM bytes per launch of this kernel measured with rocprofv3 --pmc
     (FETCH_SIZE + WRITE_SIZE, calibrated against a streaming kernel of known
-    size), as recorded in profiles/; None when no matching record exists."""
-    path = os.path.join(ROOT, "profiles", f"traffic_{prec}_{N}x{K}_m{M}.txt")
+    size), as recorded in profiles/; None when no matching record exists.
+    kind "prefill": the bf16 MFMA GEMM's record (bytes per matmul call, the
+    split-K partial-sum launch included when the call makes one)."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{kind + '_' if kind else ''}{prec}_{N}x{K}_m{M}.txt")
     if not os.path.exists(path):
         return None
     for line in open(path):
@@ -260,6 +262,18 @@ def run_prefill(args, backend, T, torch):
     y = torch.empty((M, N), device=dev, dtype=torch.float32)
     cap = torch.cuda.Stream(dev)
     cap.wait_stream(torch.cuda.current_stream(dev))
+    if args.pmc_pass:
+        src = torch.ones(16 << 20, dtype=torch.float32, device=dev)   # 64 MiB
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        for i in range(20):
+            backend.matmul_bf16_device(x, pool[i % n_sets], out=y, stream=cap)
+        torch.cuda.synchronize()
+        print(json.dumps({"pmc_pass": True, "copy_bytes": src.numel() * 4, "workload": args.workload,
+                          "alg_bytes_per_launch": prefill_bytes(prec, gs, N, K, M)}), flush=True)
+        backend.close()
+        return
     for i in range(n_sets):
         backend.matmul_bf16_device(x, pool[i], out=y, stream=cap)
     torch.cuda.synchronize()
@@ -304,7 +318,8 @@ def run_prefill(args, backend, T, torch):
         roof = {"bound": "hbm", "achieved": round(byts / kern_us / 1e3, 1),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s"}
     roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
-    roof.update({"traffic": None, "kernel": f"gemm_bf16 {N}x{K} M={M} ({pool[0].path})",
+    roof.update({"traffic": profiled_traffic(prec, N, K, M, "prefill"),
+                 "kernel": f"gemm_bf16 {N}x{K} M={M} ({pool[0].path})",
                  "kernel_us": round(kern_us, 3), "alg_bytes_per_launch": byts,
                  "flops_per_launch": int(flops)})
     out = {
@@ -762,7 +777,8 @@ def main():
     ap.add_argument("--last", type=int, default=0, help="--trace-summary: trailing dispatches to average")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="for rocprofv3 --pmc: 5 plain copies of 64 MiB (calibration kernel of "
-                         "known size) then 20 launches of the dominant GEMV; no timing")
+                         "known size) then 20 launches of the dominant GEMV (of the GEMM for a "
+                         "prefill workload); no timing")
     args = ap.parse_args()
 
     if args.trace_summary:

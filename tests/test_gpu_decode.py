@@ -154,6 +154,36 @@ def test_decode_merge_beyond_one_load_round(backend):
     dec.close()
 
 
+def test_decode_long_context_head_dim_64(backend):
+    # head_dim 64 (the 1.1B model's), 1100 steps: 18 attention ranges of 64
+    # positions, all in the merge kernel's first load round (4 lane groups x
+    # 8 loads for head_dim 64)
+    cfg = T.DecoderConfig(**dict(SMALL, num_layers=1, max_seq=1104))
+    dec, ref = _model(backend, cfg, "int8", seed=73)
+    rng = np.random.default_rng(73)
+    for i, tok in enumerate(rng.integers(0, cfg.vocab, size=1100)):
+        y = dec.step(int(tok))
+        r = ref.step(int(tok))
+        if i % 50 == 0 or i in (511, 512, 513) or i >= 1020:
+            assert _gated(y, r) <= GATE, (i, _gated(y, r))
+    dec.close()
+
+
+def test_decode_merge_beyond_one_load_round_head_dim_64(backend):
+    # head_dim 64: the merge kernel's first load round covers 32 ranges
+    # (2048 positions); 2100 steps reach 33, so the last range goes through
+    # its loop
+    cfg = T.DecoderConfig(**dict(SMALL, num_layers=1, max_seq=2112))
+    dec, ref = _model(backend, cfg, "int8", seed=79)
+    rng = np.random.default_rng(79)
+    for i, tok in enumerate(rng.integers(0, cfg.vocab, size=2100)):
+        y = dec.step(int(tok))
+        r = ref.step(int(tok))
+        if i % 100 == 0 or i >= 2040:
+            assert _gated(y, r) <= GATE, (i, _gated(y, r))
+    dec.close()
+
+
 def test_decode_reset_is_deterministic(backend):
     cfg = T.DecoderConfig(**SMALL)
     dec, _ = _model(backend, cfg, "int8", seed=31)

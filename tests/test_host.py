@@ -185,3 +185,19 @@ def test_linear_bias_precondition():
         T.LinearLayerWeights(pq, np.zeros(N + 1, np.float32)).apply(np.zeros((1, K), np.float32), None)
     with pytest.raises(T.PreconditionFailure):
         T.LinearLayerWeights(pq, np.zeros(N, np.float32)).apply(np.zeros((1, K + 1), np.float32), None)
+
+
+def test_bench_reads_every_committed_traffic_record():
+    # bench.py puts these per-launch HBM byte counts into roofline.traffic:
+    # the default GEMV line's dominant shape and every prefill workload
+    import sys
+    sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+    import bench
+
+    assert bench.profiled_traffic("int4", 32000, 2048, 1) > 0
+    for name, (prec, gs, (N, K), M) in bench.PREFILL.items():
+        t = bench.profiled_traffic(prec, N, K, M, "prefill")
+        alg = bench.prefill_bytes(prec, gs, N, K, M)
+        assert t is not None, name
+        assert alg <= t <= 8 * alg, (name, t, alg)   # counted bytes cover at least the algorithmic ones
+    assert bench.profiled_traffic("int8", 7, 7, 7, "prefill") is None
