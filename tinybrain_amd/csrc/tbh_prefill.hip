@@ -34,7 +34,13 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBK = 64;           // K per staged step (two MFMA K-steps of 32) unless a launch takes 128
-constexpr int kRowPad = 8;        // bf16 of padding per LDS row (16 bytes)
+// bf16 of padding per LDS row (32 bytes): rows of 160 (K steps of 64) or 288
+// (of 128) bytes.  The MFMA fragment reads (lane l: row l % 16, 16-byte
+// column l / 16) measured conflict-free with these strides on gfx950 and
+// 2-way conflicted with 144 / 272-byte rows (16 bytes of padding), which
+// cost 1-6 % per launch (rocprofv3 SQ_LDS_BANK_CONFLICT per LDS
+// instruction 2.98 -> 1.02 on INT8 M = 2048).
+constexpr int kRowPad = 16;
 constexpr int kDepth = 2;         // K steps whose global loads are in flight at once
 
 struct PParams {
@@ -309,7 +315,10 @@ __global__ __launch_bounds__(64 * WV) void gemm_bf16(const PParams p) {
     // Steps are padded to a multiple of kDepth and every iteration loads and
     // computes unconditionally: steps past K read clamped addresses and meet
     // x = 0, so they add nothing, and the loop body has no branches at which
-    // the compiler would have to wait for every load in flight.
+    // the compiler would have to wait for every load in flight.  (Rings of
+    // four steps measured slower: INT8 5632x2048 at M = 2048 76.2 -> 84.7 us,
+    // M = 512 31.6 -> 32.4 us; six steps for split launches, INT8 M = 64
+    // 14.7 -> 18.6 us.)
     static_assert(kDepth == 2, "two register slots, two LDS buffers");
     const int t_stop = t_begin + ((t_end - t_begin + kDepth - 1) / kDepth) * kDepth;
     load_step(t_begin, 0);

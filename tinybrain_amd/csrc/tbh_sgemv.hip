@@ -54,7 +54,12 @@ constexpr int kRows = 128;      // weight rows per block: 8 waves x 16
 constexpr int kWaves = 8;
 constexpr int kStepChunks = 4;  // chunks per step: one per 16-lane row of a wave
 constexpr int kXUnits = 8;      // x float4 units per thread (M * kchunks * 8 <= 512 * kXUnits)
-constexpr int kFragRow = 40;    // f16 per LDS fragment row: 32 + 8 of padding (A reads free of bank conflicts)
+// f16 per LDS fragment row: 32 + 8 of padding.  These 80-byte rows leave
+// the A fragment reads (lane l: row l % 16, 16-byte column l / 16) 2-way
+// bank-conflicted on gfx950; 96-byte rows measured conflict-free but no
+// faster (M = 4, 8 and the 7B projection set within noise: the kernel waits
+// on its weight stream), so the smaller LDS footprint stays.
+constexpr int kFragRow = 40;
 
 struct SParams {
     const float *x;
