@@ -16,6 +16,7 @@ Parity pins (what checks each function beyond retyping it) are in
 from __future__ import annotations
 
 import ctypes
+import time
 import os
 import subprocess
 from dataclasses import dataclass
@@ -88,6 +89,8 @@ def lib() -> ctypes.CDLL:
                                                ctypes.POINTER(ctypes.c_double),
                                                ctypes.POINTER(ctypes.c_double)]
         L.orc_matmul_quantized_cpu.restype = i32
+        L.orc_matmul_quantized_fused.argtypes = [vp, i64, ctypes.POINTER(_QT), vp, i32, i32]
+        L.orc_matmul_quantized_fused.restype = i32
         _lib = L
     return _lib
 
@@ -263,6 +266,23 @@ def matmul_quantized_cpu(x: np.ndarray, qt: QTensor, threads: int = 0):
     if st != OK:
         raise ValueError(f"oracle matmul status {st}")
     return y, td.value, tg.value
+
+
+def matmul_quantized_fused(x: np.ndarray, qt: QTensor, threads: int = 0, nk: bool = False):
+    """Best-effort CPU fused dequant-GEMV (not a reference function: the host
+    upper bound reported beside the reference path).  nk: the weight's flat
+    data holds element (k, n) at n*K + k (the converter's INT4 storage).
+    Returns (y, seconds)."""
+    x = np.ascontiguousarray(x, np.float32)
+    m = x.shape[0]
+    y = np.empty((m, qt.shape[1]), np.float32)
+    c = qt._c()
+    t0 = time.perf_counter()
+    st = lib().orc_matmul_quantized_fused(_p(x), m, ctypes.byref(c), _p(y), threads, int(nk))
+    dt = time.perf_counter() - t0
+    if st != OK:
+        raise ValueError(f"oracle fused matmul status {st}")
+    return y, dt
 
 
 def parity_errors(y_hat: np.ndarray, y64: np.ndarray) -> dict:

@@ -432,3 +432,85 @@ int32_t orc_matmul_quantized_cpu(const float *x, int64_t M, const orc_qtensor *q
     if (gemm_seconds) *gemm_seconds = t2 - t1;
     return st;
 }
+
+/* ------------------------------------------------------------------------ */
+/* Best-effort CPU (not a reference function): the fused dequant-GEMV that   */
+/* the baseline plan reports beside the reference path as an upper bound     */
+/* for the host.  y = x . dequant(W) for M rows without writing the          */
+/* dequantized matrix: every quantized element is read once per 8 rows of x  */
+/* and dequantized in registers, on all threads.  The dequantized values are  */
+/* orc_dequantize's and the sum over k runs in orc_sgemm's order, so y       */
+/* equals the reference path's bit for bit.                                   */
+/*   nk = 0: element (k, n) at flat index k*N + n (the reference's indexing); */
+/*   nk = 1: element (k, n) at n*K + k (the converter's INT4 storage), with   */
+/*           groups of group_size along k.                                   */
+/* ------------------------------------------------------------------------ */
+int32_t orc_matmul_quantized_fused(const float *x, int64_t M, const orc_qtensor *qt, float *y,
+                                   int32_t threads, int32_t nk) {
+    if (orc_validate(qt) != ORC_OK || qt->rank != 2) return ORC_E_INVALID;
+    if (!(qt->mode == ORC_MODE_PER_CHANNEL || qt->mode == ORC_MODE_INT4)) return ORC_E_INVALID;
+    if (nk && qt->mode != ORC_MODE_INT4) return ORC_E_INVALID;
+    const int64_t K = qt->dims[0], N = qt->dims[1];
+    const int64_t gs = qt->group_size > 0 ? qt->group_size : K * N;
+#ifdef _OPENMP
+    int nt = threads > 0 ? threads : omp_get_max_threads();
+#endif
+    if (nk) {
+        /* one output column n at a time: its K elements are contiguous */
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic, 64) num_threads(nt)
+#endif
+        for (int64_t n = 0; n < N; ++n) {
+            for (int64_t m0 = 0; m0 < M; m0 += 8) {
+                int64_t mc = M - m0 < 8 ? M - m0 : 8;
+                float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+                int64_t i = n * K, g = i / gs, r = i % gs;
+                for (int64_t k = 0; k < K; ++k, ++i) {
+                    float wv = ((float)orc_int4_at(qt->data, i) - (float)zp_at(qt, g)) * qt->scales[g];
+                    if (++r == gs) { r = 0; ++g; }
+                    for (int64_t m = 0; m < mc; ++m) acc[m] += x[(m0 + m) * K + k] * wv;
+                }
+                for (int64_t m = 0; m < mc; ++m) y[(m0 + m) * N + n] = acc[m];
+            }
+        }
+        return ORC_OK;
+    }
+    int64_t nblocks = (N + ORC_NB - 1) / ORC_NB;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic, 1) num_threads(nt)
+#endif
+    for (int64_t nb = 0; nb < nblocks; ++nb) {
+        int64_t n0 = nb * ORC_NB;
+        int64_t n1 = n0 + ORC_NB < N ? n0 + ORC_NB : N;
+        int64_t w = n1 - n0;
+        float wrow[ORC_NB];
+        for (int64_t m0 = 0; m0 < M; m0 += 8) {
+            int64_t mc = M - m0 < 8 ? M - m0 : 8;
+            float acc[8][ORC_NB];
+            for (int64_t m = 0; m < mc; ++m)
+                for (int64_t j = 0; j < w; ++j) acc[m][j] = 0.0f;
+            for (int64_t k = 0; k < K; ++k) {
+                if (qt->mode == ORC_MODE_PER_CHANNEL) {
+                    const int8_t *d = qt->data + k * N + n0;
+                    for (int64_t j = 0; j < w; ++j)
+                        wrow[j] = ((float)d[j] - (float)zp_at(qt, n0 + j)) * qt->scales[n0 + j];
+                } else {
+                    int64_t i = k * N + n0, g = i / gs, r = i % gs;   /* group stepped, not divided */
+                    for (int64_t j = 0; j < w; ++j, ++i) {
+                        wrow[j] = ((float)orc_int4_at(qt->data, i) - (float)zp_at(qt, g)) * qt->scales[g];
+                        if (++r == gs) { r = 0; ++g; }
+                    }
+                }
+                for (int64_t m = 0; m < mc; ++m) {
+                    float a = x[(m0 + m) * K + k];
+                    float *am = acc[m];
+                    for (int64_t j = 0; j < w; ++j) am[j] += a * wrow[j];
+                }
+            }
+            for (int64_t m = 0; m < mc; ++m)
+                memcpy(y + (m0 + m) * N + n0, acc[m], (size_t)w * sizeof(float));
+        }
+    }
+    return ORC_OK;
+}
+

@@ -121,6 +121,14 @@ int32_t orc_matmul_quantized_cpu(const float *x, int64_t M, const orc_qtensor *q
                                  float *y, int32_t threads,
                                  double *dequant_seconds, double *gemm_seconds);
 
+/* Best-effort CPU fused dequant-GEMV (not a reference function; an upper
+ * bound for the host reported beside the reference path).  nk = 0: element
+ * (k, n) at flat index k*N + n; nk = 1: at n*K + k (converter INT4 storage).
+ * PER_CHANNEL (nk = 0 only) and INT4 modes.  Same y as
+ * orc_matmul_quantized_cpu over the same dequantized values. */
+int32_t orc_matmul_quantized_fused(const float *x, int64_t M, const orc_qtensor *qt, float *y,
+                                   int32_t threads, int32_t nk);
+
 #ifdef __cplusplus
 }
 #endif

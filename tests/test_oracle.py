@@ -407,3 +407,32 @@ def test_parity_errors_floor():
     e = O.parity_errors(y64 + np.array([[1e-4, 0, 1e-7]]), y64)
     # the 1e-9 output is floored at 1e-3 * 2 = 2e-3
     assert e["gated"] == pytest.approx(max(1e-4, 1e-7 / 2e-3))
+
+
+@pytest.mark.parametrize("M", [1, 3, 9])
+def test_best_effort_fused_gemv_equals_reference_path(M):
+    # The host upper bound reported beside the reference CPU path: fused
+    # dequant-GEMV, same dequantized values and the same order over k, so the
+    # same y bit for bit -- for INT8 per-channel and INT4 in the runtime flat
+    # order, and for the converter's INT4 storage (element (k, n) at n*K + k)
+    # against a float32 loop over k on its transposed dequantization.
+    K, N = 320, 4200          # N past one 2048-column block, ragged
+    rng = np.random.default_rng(M)
+    x = rng.normal(size=(M, K)).astype(np.float32)
+    q8 = O.quantize_per_channel(O.fill_normal(3, K * N, std=0.02).reshape(K, N))
+    q4 = O.quantize_int4(O.fill_normal(4, K * N, std=0.02).reshape(K, N), 32, O.ROUND_SWIFT)
+    for q in (q8, q4):
+        y_ref, _, _ = O.matmul_quantized_cpu(x, q, threads=4)
+        y_fused, _ = O.matmul_quantized_fused(x, q, threads=4)
+        np.testing.assert_array_equal(y_fused, y_ref)
+    qn = O.quantize_int4(O.fill_normal(5, N * K, std=0.02).reshape(N, K), 32, O.ROUND_SWIFT)
+    qc = O.QTensor((K, N), qn.data, qn.scales, qn.zero_points, qn.mode, qn.precision, qn.group_size)
+    W = np.ascontiguousarray(O.dequantize(qn).reshape(N, K).T)
+    y_loop = np.zeros((M, N), np.float32)
+    for k in range(K):
+        y_loop += x[:, k:k + 1] * W[k]
+    y_fused, _ = O.matmul_quantized_fused(x, qc, threads=4, nk=True)
+    np.testing.assert_array_equal(y_fused, y_loop)
+    # and against float64: the restated product, not just a self-consistent one
+    y64 = x.astype(np.float64) @ W.astype(np.float64)
+    assert O.parity_errors(y_fused, y64)["gated"] <= 1e-3   # the contract's gate
