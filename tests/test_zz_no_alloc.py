@@ -1,8 +1,9 @@
 """tbh_matmul_device_noalloc against tbh_matmul_device, through the C ABI.
 
 The no-allocation entry point runs the same kernels as tbh_matmul_device;
-only the split-K partial sums of the matrix-core small-M GEMV go to a fixed
-per-GPU scratch array instead of a per-stream workspace.  So every result is
+only the split-K partial sums (of the matrix-core small-M GEMV and of the
+fp32 MFMA GEMM route for more rows) go to a fixed per-GPU scratch array
+instead of a per-stream workspace.  So every result is
 bit-identical to tbh_matmul_device's on the same input, and within the matmul
 gate (floored max relative error <= 1e-3) of the float64 product of the
 bit-exact dequantized weights.
@@ -58,9 +59,10 @@ def test_noalloc_matches_device_entry_point(backend):
     # K 8 ways (2.8 MB of scratch); second, smaller: 3 rows on [2048 -> 1024]
     # with the matrix-core path forced from 2 rows (4 K splits, 48 KB of
     # scratch over what the first call left there); third: INT8 on the VALU
-    # GEMV (no scratch)
+    # GEMV (no scratch); fourth: 16 rows on [5632 -> 2048], the fp32 MFMA
+    # GEMM route with K split over the CUs (2 MB of scratch)
     cases = [(_int4_nk(901, 4096, 11008), 8, 0), (_int4_nk(902, 2048, 1024), 3, 2),
-             (_int8_pc(903, 2048, 512), 1, 0)]
+             (_int8_pc(903, 2048, 512), 1, 0), (_int4_nk(905, 5632, 2048), 16, 0)]
     try:
         for (pq, W), M, min_rows in cases:
             backend.set_option(_abi.OPT_SGEMV_MIN_ROWS, min_rows)
