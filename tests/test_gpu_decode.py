@@ -95,6 +95,58 @@ def test_decode_tinyllama_width(backend):
     dec.close()
 
 
+class _Scaled:
+    """x @ (W * f) for the float64 reference, without a copy of W per layer."""
+    __array_ufunc__ = None    # numpy defers x @ self to __rmatmul__
+
+    def __init__(self, w, f):
+        self.w, self.f = w, f
+
+    def __rmatmul__(self, x):
+        return (x @ self.w) * self.f
+
+
+def test_decode_tinyllama_full_depth(backend):
+    # BASELINE configs[2] at its full depth: 22 layers, hidden 2048, 32/4
+    # heads, FFN 5632, vocab 32000, INT8 per-channel.  One quantized matrix
+    # per projection shape is shared by the layers, with each layer's scales
+    # multiplied by 1 + 0.05 l and its own norm weights, so every layer's
+    # dequantized weights and caches differ; the float64 reference applies
+    # the factor to the shared dequantized matrix.
+    cfg = T.DecoderConfig(num_layers=22, hidden=2048, num_heads=32, num_kv_heads=4, intermediate=5632,
+                          vocab=32000, max_seq=64)
+    H, I, V, kv = cfg.hidden, cfg.intermediate, cfg.vocab, cfg.kv_dim
+    shapes = [(H, H), (H, kv), (H, kv), (H, H), (H, I), (H, I), (I, H)]
+    base = []
+    for j, (K, N) in enumerate(shapes):
+        qt = O.quantize_per_channel(O.fill_normal(601 + j, K * N, std=0.02).reshape(K, N))
+        base.append((qt, O.dequantize(qt).astype(np.float64)))
+    norm = lambda sd: (1.0 + 0.1 * O.fill_normal(sd, H)).astype(np.float32)
+    emb = O.fill_normal(611, V * H).reshape(V, H)
+    fn = norm(612)
+    lm, lm_w = _weight("int8", 613, H, V)
+    dec = T.Decoder(backend, cfg, emb, fn, lm)
+    layers, factors = [], []
+    for l in range(cfg.num_layers):
+        f = np.float32(1.0 + 0.05 * l)
+        factors.append(float(f))
+        ws = [T.QuantizedTensor((K, N), qt.data, (qt.scales * f).astype(np.float32), qt.mode, qt.precision,
+                                qt.group_size, qt.zero_points, T.Layout.KN_FLAT)
+              for (qt, _), (K, N) in zip(base, shapes)]
+        gi, gp = norm(700 + 2 * l), norm(701 + 2 * l)
+        dec.set_layer(l, gi, gp, ws)
+        layers.append(RefLayer(gi, gp, [w64 for _, w64 in base]))   # the same arrays: no copies
+    ref = RefDecoder(cfg.num_layers, H, cfg.num_heads, cfg.num_kv_heads, I, V, emb, fn, lm_w, layers,
+                     cfg.rms_eps, cfg.rope_base)
+    for l, f in enumerate(factors):
+        ref.layers[l].weights = [_Scaled(w, f) for w in ref.layers[l].weights]
+    for i, tok in enumerate([1, 31999, 450, 2048, 7]):
+        y = dec.step(tok)
+        r = ref.step(tok)
+        assert _gated(y, r) <= GATE, (i, _gated(y, r))
+    dec.close()
+
+
 def test_decode_tinyllama_width_runtime_int4(backend):
     # TinyLlama-1.1B layer shapes, 2 layers, INT4 in the runtime layout that
     # Tensor.quantize(.int4) and the perplexity harness write (groups of 32
