@@ -122,8 +122,10 @@ tbh_status tbh_device_open(int32_t ordinal, tbh_device **out) {
             "tbh_device_open: scratch address");
     if (!dev->noalloc_scratch) return set_error(TBH_E_HIP, "tbh_device_open: scratch address is NULL");
     dev->cu_count = prop.multiProcessorCount;
-    if (const char *v = std::getenv("TBH_SGEMV_MIN_ROWS"); v && *v)   // read once, at open
-        dev->sgemv_min_rows.store(std::min(9, std::max(2, std::atoi(v))), std::memory_order_relaxed);
+    if (const char *v = std::getenv("TBH_SGEMV_MIN_ROWS"); v && *v) {   // read once, at open; 0: the rule
+        const int r = std::atoi(v);
+        dev->sgemv_min_rows.store(r == 0 ? 0 : std::min(9, std::max(2, r)), std::memory_order_relaxed);
+    }
     TBH_HIP(hipStreamCreateWithFlags(&dev->stream, hipStreamNonBlocking), "hipStreamCreate");
     *out = dev.release();
     return TBH_OK;
@@ -894,7 +896,12 @@ tbh_status tbh_matmul(tbh_device *dev, const float *x, int64_t M, int64_t K, con
     Scratch scr;
     scr.dev = dev;
     st = matmul_enqueue(w, dx, M, dy, dev->stream, scr);
-    if (st != TBH_OK) return st;
+    if (st != TBH_OK) {
+        // the copy of the caller's x may still be queued: wait for it before
+        // the caller can release x (the status returned is the launch error)
+        (void)hipStreamSynchronize(dev->stream);
+        return st;
+    }
     TBH_HIP(hipMemcpyAsync(y, dy, yb, hipMemcpyDeviceToHost, dev->stream), "tbh_matmul: copy y");
     TBH_HIP(hipStreamSynchronize(dev->stream), "tbh_matmul: synchronize");
     return TBH_OK;
