@@ -107,13 +107,13 @@ __device__ __forceinline__ float sbyte(uint32_t w) {
 // output.
 //
 // Eight-wave blocks with K steps of 64 are held to four waves per SIMD, so
-// two blocks share a CU.  INT4 blocks with K steps of 128 (256 VGPRs) keep
-// the unscaled nibble unpack and the masked form of every K step: the 16 q
-// unpack or a second loop form spilled 8-17 more registers there.
+// two blocks share a CU.  INT4 blocks with K steps of 128 (256 VGPRs) run
+// every K step in its masked form: with a second, unmasked loop form their
+// spilled registers went from 2 to 14-17.
 template <int PREC, int BM, int BN, bool ZP, int WV, int BK, bool XF>
 __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(WV == 8 && BK == 64 ? 4 : 1)))
 void gemm_bf16(const PParams p) {
-    constexpr bool kLean = !(PREC == 4 && BK == 128);   // 16 (q - zp) staging, two-form K loop
+    constexpr bool kTwoForm = !(PREC == 4 && BK == 128);   // unmasked form for steps inside K
     constexpr int kLdsRow = BK + kRowPad;
     constexpr int NT = 64 * WV;                   // threads; waves as 2 x (WV / 2)
     constexpr int WC = WV / 2;
@@ -147,8 +147,7 @@ void gemm_bf16(const PParams p) {
     float scn[TN];
 #pragma unroll
     for (int b = 0; b < TN; ++b)
-        scn[b] = PREC == 8 ? p.scales[min(n0 + wn * WN + b * 16 + (lane & 15), p.Np - 1)]
-                           : (kLean ? 0.0625f : 1.0f);
+        scn[b] = PREC == 8 ? p.scales[min(n0 + wn * WN + b * 16 + (lane & 15), p.Np - 1)] : 0.0625f;
 
     // ---- global -> registers for one step, into register stage d of kDepth:
     // the loads of steps t+1 .. t+kDepth-1 are in flight while step t runs
@@ -169,7 +168,7 @@ void gemm_bf16(const PParams p) {
     // no segment masked (the K loop takes this form for all but its last
     // iterations).
     auto load_step = [&](int t, int d, auto full) {
-        constexpr bool FULL = decltype(full)::value && !XF && kLean;
+        constexpr bool FULL = decltype(full)::value && !XF && kTwoForm;
         const int k0 = t * BK;
         if constexpr (XF) {
 #pragma unroll
@@ -201,8 +200,8 @@ void gemm_bf16(const PParams p) {
             const int n = n0 + row;
             // (the INT4 128-deep kernel keeps the run-time s < WCH test here and in
             // store_step: with it folded, that kernel's register allocation
-            // spilled 8 more registers)
-            const bool in = ((kLean && WCH % NT == 0) || s < WCH) && (FULL || (n < p.Np && c < p.chunks));
+            // spilled 6-11 more registers)
+            const bool in = ((kTwoForm && WCH % NT == 0) || s < WCH) && (FULL || (n < p.Np && c < p.chunks));
             // Out-of-range chunks read a valid chunk: rows past N are never
             // stored and K padding meets x = 0, so the values do not matter.
             const int64_t nn = in ? n : 0, cc = in ? c : 0;
@@ -219,7 +218,7 @@ void gemm_bf16(const PParams p) {
 
     // ---- registers -> LDS (x as is; weights dequantized to bf16 pieces)
     auto store_step = [&](int d, int bb, auto full) {
-        constexpr bool FULL = decltype(full)::value && !XF && kLean;
+        constexpr bool FULL = decltype(full)::value && !XF && kTwoForm;
         if constexpr (XF) {
             // segment (quad row qrow, kq) -> product rows 4 qrow + piece
 #pragma unroll
@@ -255,7 +254,7 @@ void gemm_bf16(const PParams p) {
 #pragma unroll
         for (int j = 0; j < WPT; ++j) {
             const int s = tid + NT * j;
-            if ((kLean && WCH % NT == 0) || s < WCH) {
+            if ((kTwoForm && WCH % NT == 0) || s < WCH) {
                 const int row = s / CPR, cl = s % CPR;
                 uint16_t *dst = &ws[bb][row * kLdsRow + cl * CE];
                 if (PREC == 8) {
@@ -282,35 +281,18 @@ void gemm_bf16(const PParams p) {
                     // 4-bit two's complement value.  Moved into the upper half of
                     // its byte (high nibbles masked in place, low nibbles shifted
                     // up), a nibble reads as the signed byte 16 q.  Value 16 (q - zp).
-                    // Not kLean: each nibble pair (u & 0x000F000F after a shift)
-                    // converted as is, value q - zp.
-                    if constexpr (kLean) {
-                        const float zf = ZP ? 16.0f * (float)zq[d][j] : 0.0f;
+                    const float zf = ZP ? 16.0f * (float)zq[d][j] : 0.0f;
 #pragma unroll
-                        for (int q = 0; q < 4; ++q) {
-                            const uint32_t w = wr[d][j][q] ^ 0x88888888u;
-                            const uint32_t hi = w & 0xF0F0F0F0u;          // bytes: k + {2, 6, 3, 7}
-                            const uint32_t lo = (w << 4) & 0xF0F0F0F0u;   // bytes: k + {0, 4, 1, 5}
-                            uint32_t o[4];
-                            o[0] = pack_hi16(sbyte<0>(lo) - zf, sbyte<2>(lo) - zf);
-                            o[1] = pack_hi16(sbyte<0>(hi) - zf, sbyte<2>(hi) - zf);
-                            o[2] = pack_hi16(sbyte<1>(lo) - zf, sbyte<3>(lo) - zf);
-                            o[3] = pack_hi16(sbyte<1>(hi) - zf, sbyte<3>(hi) - zf);
-                            *(u32x4 *)(dst + 8 * q) = u32x4{o[0], o[1], o[2], o[3]};
-                        }
-                    } else {
-                        const float off = 8.0f + (ZP ? (float)zq[d][j] : 0.0f);
-#pragma unroll
-                        for (int q = 0; q < 4; ++q) {
-                            const uint32_t w = wr[d][j][q];
-                            uint32_t o[4];
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) {
-                                const uint32_t u = (w >> (4 * e)) & 0x000F000Fu;
-                                o[e] = pack_hi16((float)(u & 0xFFu) - off, (float)((u >> 16) & 0xFFu) - off);
-                            }
-                            *(u32x4 *)(dst + 8 * q) = u32x4{o[0], o[1], o[2], o[3]};
-                        }
+                    for (int q = 0; q < 4; ++q) {
+                        const uint32_t w = wr[d][j][q] ^ 0x88888888u;
+                        const uint32_t hi = w & 0xF0F0F0F0u;          // bytes: k + {2, 6, 3, 7}
+                        const uint32_t lo = (w << 4) & 0xF0F0F0F0u;   // bytes: k + {0, 4, 1, 5}
+                        uint32_t o[4];
+                        o[0] = pack_hi16(sbyte<0>(lo) - zf, sbyte<2>(lo) - zf);
+                        o[1] = pack_hi16(sbyte<0>(hi) - zf, sbyte<2>(hi) - zf);
+                        o[2] = pack_hi16(sbyte<1>(lo) - zf, sbyte<3>(lo) - zf);
+                        o[3] = pack_hi16(sbyte<1>(hi) - zf, sbyte<3>(hi) - zf);
+                        *(u32x4 *)(dst + 8 * q) = u32x4{o[0], o[1], o[2], o[3]};
                     }
                     ssc[bb][s] = sr[d][j];
                 }
@@ -385,7 +367,7 @@ void gemm_bf16(const PParams p) {
         compute(1);                    // step t0 + 1
         lds_barrier();
     };
-    if constexpr (kLean) {
+    if constexpr (kTwoForm) {
         const int t_full = n0 + BN <= p.Np ? kend / BK : 0;
         int t0 = t_begin;
         for (; t0 < t_stop && t0 + 4 < t_full; t0 += 2) iteration(t0, std::true_type{});
