@@ -127,3 +127,61 @@ def test_bf16_rows_across_tile_rules(backend, kind, K, N):
         torch.cuda.synchronize()
         err = O.parity_errors(y.cpu().numpy(), O.gemm_f64(xb.float().numpy(), W))
         assert err["gated"] <= GATE, (kind, K, N, M, err)
+
+
+EXTREME_CASES = [
+    ("int8", 8, 1),               # one output column, one 8-wide K piece
+    ("int8", 16, 3),
+    ("int8", 40, 7),
+    ("int8", 8192, 8),
+    ("int8", 32768, 16),          # long K: many chunks per lane
+    ("int4_nk_g32", 32, 1),
+    ("int4_nk_g32", 64, 5),
+    ("int4_nk_g32", 16384, 64),
+    ("int4_nk_g128", 32768, 9),
+    ("int4_kn_g32", 96, 32),      # runtime layout, a single N-block
+]
+
+
+@pytest.mark.parametrize("kind,K,N", EXTREME_CASES)
+def test_fp32_extreme_shapes(backend, kind, K, N):
+    qt, pq = _weight(kind, K, N, seed=3000 + K + N)
+    W = _oracle_weight(qt, pq.layout)
+    deq = backend.dequantize(pq)
+    np.testing.assert_array_equal(deq.view(np.uint32), W.view(np.uint32))
+    for M in (1, 2, 3, 5, 8, 13, 64, 300):
+        x = O.fill_normal(13 * K + M, M * K).reshape(M, K)
+        y = backend.matmulQuantized(x, pq)
+        err = O.parity_errors(y, O.gemm_f64(x, W))
+        assert err["gated"] <= GATE, (kind, K, N, M, err)
+
+
+@pytest.mark.parametrize("kind,K,N", [("int8", 8, 1), ("int8", 40, 7), ("int8", 8192, 8),
+                                      ("int4_nk_g32", 32, 1), ("int4_nk_g32", 16384, 64)])
+def test_bf16_extreme_shapes(backend, kind, K, N):
+    import torch
+
+    qt, pq = _weight(kind, K, N, seed=4000 + K + N)
+    W = _oracle_weight(qt, pq.layout)
+    w = backend.weight(pq)
+    for M in (64, 129, 300):
+        xb = torch.from_numpy(O.fill_normal(17 * K + M, M * K).reshape(M, K)).to(torch.bfloat16)
+        y = backend.matmul_bf16_device(xb.cuda(), w)
+        torch.cuda.synchronize()
+        err = O.parity_errors(y.cpu().numpy(), O.gemm_f64(xb.float().numpy(), W))
+        assert err["gated"] <= GATE, (kind, K, N, M, err)
+
+
+def test_long_k_without_an_mfma_route_is_unsupported(backend):
+    # K past the GEMV kernels' staged x: INT8 with zero points and the runtime
+    # INT4 layout have no MFMA route, and say so instead of failing a launch
+    from tinybrain_amd import _abi
+    from tinybrain_amd.backend import HIPBackendError
+
+    for kind, K, N in (("int8_zp", 16384, 16), ("int4_kn_g32", 16384, 32)):
+        qt, pq = _weight(kind, K, N, seed=5000 + K)
+        x = O.fill_normal(5, 2 * K).reshape(2, K)
+        with pytest.raises(HIPBackendError) as e:
+            backend.matmulQuantized(x, pq)
+        assert e.value.status == _abi.E_UNSUPPORTED, str(e.value)
+        assert "too long" in str(e.value)

@@ -778,7 +778,17 @@ static tbh_status matmul_enqueue(const tbh_weight *w, const float *x, int64_t M,
         return set_error(TBH_E_INVALID, "weight device arrays are inconsistent with its layout");
     const int mfma_forced = w->dev->mfma_min_rows.load(std::memory_order_relaxed);
     const int64_t mfma_min = mfma_forced > 0 ? mfma_forced : mfma_min_rows(*w);
-    if (M >= mfma_min && prefill_supported(*w) && !w->zp && w->K % 8 == 0 && ((uintptr_t)x & 15) == 0) {
+    // The GEMV kernels stage a whole row of x in LDS; past about 13 K (INT8)
+    // or 14.5 K (INT4) elements it does not fit, and every row count goes to
+    // the MFMA GEMM, which streams K through LDS in steps.
+    const bool gemv_fits = w->mfma_tiles || w->path == Path::Generic || gemv_max_rows(*w) > 0;
+    const bool mfma_ok = prefill_supported(*w) && !w->zp && w->K % 8 == 0 && ((uintptr_t)x & 15) == 0;
+    if (!gemv_fits && !mfma_ok)
+        return set_error(TBH_E_UNSUPPORTED,
+                         "K = " + std::to_string(w->K) + " is too long for the GEMV kernels' staged x, and this "
+                         "weight or x does not suit the MFMA GEMM (zero points, K % 8, a 16-byte aligned x, "
+                         "INT8 rows or INT4 K-groups only)");
+    if ((M >= mfma_min || !gemv_fits) && mfma_ok) {
         const hipError_t e = launch_prefill_f32(*w, x, w->K, M, y, w->N, s, scr);
         if (e == hipSuccess) return TBH_OK;
         if (e == hipErrorOutOfMemory && scr.is_fixed())
@@ -786,6 +796,7 @@ static tbh_status matmul_enqueue(const tbh_weight *w, const float *x, int64_t M,
                                                 " bytes of scratch; the no-allocation entry point holds " +
                                                 std::to_string(scr.fixed_bytes));
         if (e != hipErrorInvalidValue) return hip_error(e, "matmul kernel launch");
+        if (!gemv_fits) return set_error(TBH_E_UNSUPPORTED, "K too long for the GEMV kernels, shape refused by the MFMA GEMM");
         // shapes the GEMM does not take run on the GEMV kernels below
     }
     // 2..8 rows of x per launch on the matrix cores when the weight allows
