@@ -169,12 +169,13 @@ tbh_status tbh_weight_get_info(const tbh_weight *w, tbh_weight_info *info);
  * Calls on one device are serialised.  Like the Metal kernels, one call
  * covers any M (MetalBackend.swift:949-956): a few rows run on the GEMV
  * kernels; from a per-weight row count (8..64, TBH_OPT_MFMA_MIN_ROWS) INT8
- * rows and INT4 K-group weights without zero points run on the bf16 MFMA
- * GEMM with every fp32 x row split exactly into three bf16 pieces.  The GEMV
- * kernels stage a row of x in LDS, so a K past about 13 K (INT8) or 14.5 K
- * (INT4) elements runs on the MFMA GEMM at every M; such a weight that the
- * GEMM does not take (zero points, K % 8 != 0, the runtime INT4 layout)
- * returns TBH_E_UNSUPPORTED. */
+ * rows and INT4 K-group weights run on the bf16 MFMA GEMM with every fp32 x
+ * row split exactly into three bf16 pieces.  The GEMV kernels stage a row of
+ * x in LDS, so a K past about 13 K (INT8) or 14.5 K (INT4) elements runs on
+ * the MFMA GEMM at every M (runtime-layout INT4 of such a K keeps the
+ * reference's flat array and runs on the generic kernel); a long K that is
+ * not a multiple of 8, or an x that is not 16-byte aligned, returns
+ * TBH_E_UNSUPPORTED. */
 tbh_status tbh_matmul(tbh_device *dev, const float *x, int64_t M, int64_t K,
                       const tbh_weight *w, float *y);
 

@@ -140,6 +140,9 @@ EXTREME_CASES = [
     ("int4_nk_g32", 16384, 64),
     ("int4_nk_g128", 32768, 9),
     ("int4_kn_g32", 96, 32),      # runtime layout, a single N-block
+    ("int8_zp", 16384, 16),       # long K with zero points: the MFMA GEMM
+    ("int4_nk_g32_zp", 16384, 9),
+    ("int4_kn_g32", 16384, 32),   # long K, runtime layout: the generic kernel
 ]
 
 
@@ -173,15 +176,15 @@ def test_bf16_extreme_shapes(backend, kind, K, N):
 
 
 def test_long_k_without_an_mfma_route_is_unsupported(backend):
-    # K past the GEMV kernels' staged x: INT8 with zero points and the runtime
-    # INT4 layout have no MFMA route, and say so instead of failing a launch
+    # K past the GEMV kernels' staged x and not a multiple of 8 (which the MFMA
+    # GEMM needs): the call says so instead of failing a launch
     from tinybrain_amd import _abi
     from tinybrain_amd.backend import HIPBackendError
 
-    for kind, K, N in (("int8_zp", 16384, 16), ("int4_kn_g32", 16384, 32)):
-        qt, pq = _weight(kind, K, N, seed=5000 + K)
-        x = O.fill_normal(5, 2 * K).reshape(2, K)
-        with pytest.raises(HIPBackendError) as e:
-            backend.matmulQuantized(x, pq)
-        assert e.value.status == _abi.E_UNSUPPORTED, str(e.value)
-        assert "too long" in str(e.value)
+    K, N = 16388, 4
+    qt, pq = _weight("int8", K, N, seed=5000)
+    x = O.fill_normal(5, 2 * K).reshape(2, K)
+    with pytest.raises(HIPBackendError) as e:
+        backend.matmulQuantized(x, pq)
+    assert e.value.status == _abi.E_UNSUPPORTED, str(e.value)
+    assert "too long" in str(e.value)

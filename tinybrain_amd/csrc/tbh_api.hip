@@ -473,7 +473,10 @@ tbh_status tbh_weight_create(tbh_device *dev, const tbh_qtensor_desc *desc, tbh_
             if (K % gs == 0 && gs % kInt4ChunkElems == 0) { kgroup = true; seg = gs; }
             else if (gs % K == 0) { kgroup = true; seg = 0; }
         } else {
-            if (!has_zp) {
+            // The N-group kernels stage a row of x in LDS; with a longer K
+            // the weight keeps the reference's flat array (generic kernel).
+            const int64_t x_lds = round_up(K, kInt4ChunkElems) / kInt4ChunkElems * (kInt4ChunkElems + 4) * 4;
+            if (!has_zp && x_lds <= kMaxLdsBytes) {
                 if (N % gs == 0) { ngroup = true; rpn = gs; }
                 else if (gs % N == 0) { ngroup = true; rpn = 0; }
             }
@@ -782,12 +785,11 @@ static tbh_status matmul_enqueue(const tbh_weight *w, const float *x, int64_t M,
     // or 14.5 K (INT4) elements it does not fit, and every row count goes to
     // the MFMA GEMM, which streams K through LDS in steps.
     const bool gemv_fits = w->mfma_tiles || w->path == Path::Generic || gemv_max_rows(*w) > 0;
-    const bool mfma_ok = prefill_supported(*w) && !w->zp && w->K % 8 == 0 && ((uintptr_t)x & 15) == 0;
+    const bool mfma_ok = prefill_supported(*w) && w->K % 8 == 0 && ((uintptr_t)x & 15) == 0;
     if (!gemv_fits && !mfma_ok)
         return set_error(TBH_E_UNSUPPORTED,
-                         "K = " + std::to_string(w->K) + " is too long for the GEMV kernels' staged x, and this "
-                         "weight or x does not suit the MFMA GEMM (zero points, K % 8, a 16-byte aligned x, "
-                         "INT8 rows or INT4 K-groups only)");
+                         "K = " + std::to_string(w->K) + " is too long for the GEMV kernels' staged x, and the "
+                         "MFMA GEMM needs K % 8 == 0 and a 16-byte aligned x");
     if ((M >= mfma_min || !gemv_fits) && mfma_ok) {
         const hipError_t e = launch_prefill_f32(*w, x, w->K, M, y, w->N, s, scr);
         if (e == hipSuccess) return TBH_OK;

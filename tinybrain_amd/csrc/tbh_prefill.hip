@@ -483,10 +483,14 @@ hipError_t launch_tile(const PParams &p, int splits, hipStream_t s) {
     }();
     const dim3 grid((unsigned)((p.Np + BN - 1) / BN), (unsigned)((p.M + BM - 1) / BM), (unsigned)splits);
     const bool w8 = waves == 8 || (waves != 4 && BN == 128 && (p.M >= 256 || PREC == 4));
-    if (p.xf) {   // fp32 x (no zero points: the API routes those elsewhere)
-        if (p.zp) return hipErrorInvalidValue;
-        if (w8) hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, false, 8, BK, true>), grid, dim3(512), 0, s, p);
-        else hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, false, 4, BK, true>), grid, dim3(256), 0, s, p);
+    if (p.xf) {   // fp32 x
+        if (p.zp) {
+            if (w8) hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, true, 8, BK, true>), grid, dim3(512), 0, s, p);
+            else hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, true, 4, BK, true>), grid, dim3(256), 0, s, p);
+        } else {
+            if (w8) hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, false, 8, BK, true>), grid, dim3(512), 0, s, p);
+            else hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, false, 4, BK, true>), grid, dim3(256), 0, s, p);
+        }
     } else if (p.zp) {
         if (w8) hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, true, 8, BK, false>), grid, dim3(512), 0, s, p);
         else hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, true, 4, BK, false>), grid, dim3(256), 0, s, p);
@@ -634,7 +638,7 @@ static PParams prefill_params(const tbh_weight &w, int64_t ldx, float *y, int64_
 
 hipError_t launch_prefill_f32(const tbh_weight &w, const float *x, int64_t ldx, int64_t M, float *y,
                               int64_t ldy, hipStream_t s, const Scratch &scr) {
-    if (!prefill_supported(w) || w.zp || M < 1 || 4 * M > INT32_MAX || w.K % 8 != 0 || ldx % 4 != 0 ||
+    if (!prefill_supported(w) || M < 1 || 4 * M > INT32_MAX || w.K % 8 != 0 || ldx % 4 != 0 ||
         ((uintptr_t)x & 15) != 0)
         return hipErrorInvalidValue;
     PParams p = prefill_params(w, ldx, y, ldy);
