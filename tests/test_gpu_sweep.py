@@ -188,3 +188,26 @@ def test_long_k_without_an_mfma_route_is_unsupported(backend):
         backend.matmulQuantized(x, pq)
     assert e.value.status == _abi.E_UNSUPPORTED, str(e.value)
     assert "too long" in str(e.value)
+
+
+@pytest.mark.parametrize("kind,K,N", [("int8", 2048, 1003), ("int8_zp", 512, 333), ("int4_nk_g32", 2048, 1003),
+                                      ("int4_kn_g32", 512, 96)])
+def test_device_x_4_byte_aligned(backend, kind, K, N):
+    # tbh_matmul_device on an x that is a contiguous view 4 bytes into its
+    # buffer: the kernels that need 16-byte aligned rows are skipped, the
+    # rest read x element by element
+    import torch
+
+    qt, pq = _weight(kind, K, N, seed=6000 + K + N)
+    W = _oracle_weight(qt, pq.layout)
+    w = backend.weight(pq)
+    for M in (1, 2, 4, 5, 8, 12, 65):
+        x = O.fill_normal(19 * K + M, M * K).reshape(M, K)
+        buf = torch.zeros(M * K + 4, dtype=torch.float32, device="cuda")
+        xv = buf[1:1 + M * K].view(M, K)
+        xv.copy_(torch.from_numpy(x))
+        assert xv.data_ptr() % 16 == 4
+        y = backend.matmul_device(xv, w)
+        torch.cuda.synchronize()
+        err = O.parity_errors(y.cpu().numpy(), O.gemm_f64(x, W))
+        assert err["gated"] <= GATE, (kind, K, N, M, err)
