@@ -129,6 +129,9 @@ const char *tbh_status_string(tbh_status status);
  * and MetalBackend.isAvailable: opens HIP device `ordinal` (must be gfx950)
  * with one internal stream.  TBH_E_NODEVICE when absent. */
 tbh_status tbh_device_open(int32_t ordinal, tbh_device **out);
+/* Waits for the device's work and frees what the library allocated on it.
+ * Destroy the device's weights and decoders first: their destroy calls read
+ * the device handle. */
 tbh_status tbh_device_close(tbh_device *dev);
 /* HIP device ordinal and compute-unit count of an open device. */
 tbh_status tbh_device_get_info(const tbh_device *dev, int32_t *ordinal, int32_t *cu_count);

@@ -275,6 +275,26 @@ def test_empty_input(backend):
     assert y.shape == (0, 8)
 
 
+def test_backend_close_closes_its_weights_and_decoders_first():
+    # tbh_weight_destroy and tbh_decoder_destroy read their device handle, so
+    # HIPBackend.close() destroys every weight and decoder made on it (cached
+    # or not) before it closes the device; their own close is then a no-op
+    b = T.HIPBackend(0)
+    qt = _int8_pc(97, 64, 32)
+    direct = T.DeviceWeight(b, _product(qt, (64, 32)))
+    cached = b.weight(_product(qt, (64, 32)))
+    H, V = 64, 128
+    cfg = T.DecoderConfig(num_layers=1, hidden=H, num_heads=4, num_kv_heads=2, intermediate=128, vocab=V,
+                          max_seq=8)
+    lm = O.quantize_per_channel(O.fill_normal(98, H * V, std=0.02).reshape(H, V))
+    dec = T.Decoder(b, cfg, O.fill_normal(99, V * H).reshape(V, H), np.ones(H, np.float32), _product(lm, (H, V)))
+    b.close()
+    assert not direct.handle.value and not cached.handle.value and not dec._h.value
+    direct.close()
+    dec.close()
+    del direct, cached, dec
+
+
 def test_weight_cached_by_identifier_and_deterministic(backend):
     qt = _int4_nk(9, 512, 64, 32)
     pq = _product(qt, (512, 64), T.Layout.NK_FLAT)

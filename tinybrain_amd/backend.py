@@ -30,6 +30,7 @@ from __future__ import annotations
 import ctypes
 import threading
 import uuid
+import weakref
 from typing import Dict, Optional
 
 import numpy as np
@@ -60,6 +61,7 @@ class DeviceWeight:
         desc = quantized.desc()
         _check(self._lib.tbh_weight_create(backend._dev, ctypes.byref(desc), ctypes.byref(self._h)))
         self.backend = backend
+        backend._own(self)
         self.K, self.N = quantized.shape
         info = _abi.WeightInfo()
         _check(self._lib.tbh_weight_get_info(self._h, ctypes.byref(info)))
@@ -97,6 +99,15 @@ class HIPBackend:
         self.cu_count = cus.value
         self._cache: Dict[uuid.UUID, DeviceWeight] = {}
         self._lock = threading.Lock()
+        # every weight and decoder made on this device: closed before the
+        # device, whose handle their own teardown reads.  A lock of its own:
+        # weight() holds _lock while it builds the DeviceWeight that registers.
+        self._children = weakref.WeakSet()
+        self._children_lock = threading.Lock()
+
+    def _own(self, child) -> None:
+        with self._children_lock:
+            self._children.add(child)
 
     def set_option(self, option: int, value: int) -> None:
         """tbh_device_set_option: a launch-rule override (e.g.
@@ -386,10 +397,13 @@ class HIPBackend:
 
     def close(self) -> None:
         with self._lock:
-            ws = list(self._cache.values())
+            cached = list(self._cache.values())
             self._cache.clear()
-        for w in ws:
-            w.close()
+        with self._children_lock:
+            children = list(self._children) + cached
+            self._children.clear()
+        for c in children:
+            c.close()
         if self._dev:
             self._lib.tbh_device_close(self._dev)
             self._dev = ctypes.c_void_p()

@@ -64,6 +64,7 @@ class Decoder:
         desc = lm_head.desc()
         _check(self._lib.tbh_decoder_create(backend._dev, ctypes.byref(cfg), emb.ctypes.data,
                                             fn.ctypes.data, ctypes.byref(desc), ctypes.byref(self._h)))
+        backend._own(self)
 
     @classmethod
     def _adopt(cls, backend: HIPBackend, config: DecoderConfig, handle: ctypes.c_void_p) -> "Decoder":
@@ -73,6 +74,7 @@ class Decoder:
         d.backend = backend
         d.config = config
         d._h = handle
+        backend._own(d)
         return d
 
     def set_layer(self, layer: int, input_norm: np.ndarray, post_attention_norm: np.ndarray,
