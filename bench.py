@@ -58,6 +58,8 @@ PREFILL = {}
 for _m in (64, 128, 512, 2048):
     PREFILL[f"prefill_int8_m{_m}"] = ("int8", 0, (5632, 2048), _m)
     PREFILL[f"prefill_int4_m{_m}"] = ("int4", 32, (2048, 5632), _m)
+    # the INT4 shape in the runtime layout Tensor.quantize(.int4) writes
+    PREFILL[f"prefill_int4kn_m{_m}"] = ("int4kn", 32, (2048, 5632), _m)
 # Decode (BASELINE configs[2] and [4]): one token of a LLaMA-shaped model on
 # the GPU decode step.  name: (precision, group, config kwargs, context)
 CFG_7B = dict(num_layers=32, hidden=4096, num_heads=32, num_kv_heads=32, intermediate=11008, vocab=32000)
@@ -352,7 +354,7 @@ def run_prefill(args, backend, T, torch):
                  "kernel_us": round(kern_us, 3), "alg_bytes_per_launch": byts,
                  "flops_per_launch": int(flops)})
     out = {
-        "metric": f"prefill dequant-GEMM TFLOP/s on bf16 MFMA ({prec.upper()}, M={M})",
+        "metric": f"prefill dequant-GEMM TFLOP/s on bf16 MFMA ({ {'int4kn': 'INT4 runtime layout'}.get(prec, prec.upper()) }, M={M})",
         "value": round(value, 2),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -366,8 +368,9 @@ def run_prefill(args, backend, T, torch):
         "data": "synthetic",
         "config": {
             "workload": args.workload,
-            "weights": "INT4 symmetric, group 32 along K (converter layout)" if prec == "int4"
-            else "INT8 symmetric per output channel",
+            "weights": {"int4": "INT4 symmetric, group 32 along K (converter layout)",
+                        "int4kn": "INT4 symmetric, group 32 along N (runtime layout, Tensor.quantize(.int4))",
+                        "int8": "INT8 symmetric per output channel"}[prec],
             "shape_NxK": f"{N}x{K}", "M": M,
             "x": "bf16 (rounded from fp32 N(0,1)), W fp32 N(0,0.02) quantized",
             "pool_sets": n_sets,

@@ -172,8 +172,11 @@ tbh_status tbh_weight_get_info(const tbh_weight *w, tbh_weight_info *info);
  * Calls on one device are serialised.  Like the Metal kernels, one call
  * covers any M (MetalBackend.swift:949-956): a few rows run on the GEMV
  * kernels; from a per-weight row count (8..64, TBH_OPT_MFMA_MIN_ROWS) INT8
- * rows and INT4 K-group weights run on the bf16 MFMA GEMM with every fp32 x
- * row split exactly into three bf16 pieces.  The GEMV kernels stage a row of
+ * rows, INT4 K-group weights and runtime-layout INT4 whose N-blocks tile 64
+ * outputs (16, 32 or a multiple of 64 rows, or one block) run on the bf16
+ * MFMA GEMM with every fp32 x row split exactly into three bf16 pieces (for
+ * the runtime layout, x times the N-block's per-k scale, one fp32 rounding,
+ * then split).  The GEMV kernels stage a row of
  * x in LDS, so a K past about 13 K (INT8) or 14.5 K (INT4) elements runs on
  * the MFMA GEMM at every M (runtime-layout INT4 of such a K keeps the
  * reference's flat array and runs on the generic kernel); a long K that is
@@ -215,12 +218,16 @@ tbh_status tbh_linear_device(const tbh_weight *w, const float *x, int64_t M,
  * fp32 activations by dequantize(w) with cblas_sgemm
  * (QuantizedTensor.swift:640-642, Tensor.swift:839-861), which is the
  * product computed here for x = the bf16 values widened to fp32: weight
- * operands are exact (INT8: q - zp, scaled after accumulation; INT4:
- * (q - zp) * scale rounded once in fp32, split into three bf16 pieces),
- * accumulation is fp32.  x is [M, K] row-major bf16 bits (16-byte aligned,
- * K % 8 == 0), y is [M, N] fp32, both device pointers; enqueued on `stream`.
- * TBH_E_UNSUPPORTED for weights outside the INT8 row / INT4 K-group paths
- * (tbh_weight_info.path) or for the MFMA tile layout. */
+ * operands are exact integers (INT8: q - zp, the row scale applied after
+ * accumulation; INT4 K-groups: 16 (q - zp), each 32-deep MFMA's partial
+ * product times its group scale; INT4 runtime layout: 16 q against x times
+ * the N-block's per-k scale, rounded once in fp32 and split exactly into
+ * three bf16 pieces), accumulation is fp32.  x is [M, K] row-major bf16 bits
+ * (16-byte aligned, K % 8 == 0), y is [M, N] fp32, both device pointers;
+ * enqueued on `stream`.  TBH_E_UNSUPPORTED for weights outside the INT8
+ * row / INT4 K-group / INT4 runtime-layout paths (tbh_weight_info.path), for
+ * runtime-layout N-blocks that do not tile 64 outputs, or for the MFMA tile
+ * layout. */
 tbh_status tbh_matmul_bf16_device(const tbh_weight *w, const uint16_t *x, int64_t M,
                                   int64_t K, float *y, void *stream);
 

@@ -810,11 +810,28 @@ def test_prefill_bf16_split_k_determinism_and_graphs(backend):
         del g
 
 
+@pytest.mark.parametrize("K,N,gs,M", [
+    (2048, 5632, 32, 512),   # configs[3] shape, Tensor.quantize(.int4): two N-blocks per 64-output tile
+    (5632, 2048, 32, 64),    # split along K
+    (1000, 384, 128, 129),   # N-blocks of 128 rows (one per tile), K off the 64-deep steps, ragged M
+    (512, 320, 64, 300),     # N-blocks of 64 rows
+    (256, 96, 16, 70),       # N-blocks of 16 rows (four per tile), last tile half past N
+    (1000, 40, 80, 65),      # a group spans two k rows: all outputs share each k-block's scale
+])
+def test_prefill_bf16_runtime_layout(backend, K, N, gs, M):
+    # INT4 with groups along N (one scale per (N-block, k)): the GEMM stages
+    # x times each N-block's scales, split into three bf16 pieces
+    qk = _int4_kn(149 + K + N + gs, K, N, gs)
+    pq = _product(qk, (K, N))
+    assert backend.weight(pq).path == "int4_ngroup"
+    _prefill_check(backend, pq, qk, M, seed=37 + M)
+
+
 def test_prefill_bf16_unsupported(backend):
     import torch
 
-    qk = _int4_kn(89, 256, 512, 32)                        # runtime layout: N-groups
-    pq = _product(qk, (256, 512))
+    qk = _int4_kn(89, 256, 96, 48)                         # runtime layout, N-blocks of 48 rows
+    pq = _product(qk, (256, 96))
     x = torch.zeros((64, 256), dtype=torch.bfloat16, device="cuda")
     with pytest.raises(T.HIPBackendError) as e:
         backend.matmul_bf16_device(x, backend.weight(pq))

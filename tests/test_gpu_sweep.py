@@ -5,7 +5,8 @@ threshold of tbh_matmul* (burst GEMV at 1, 2, 4 rows; the VALU GEMV at 3;
 the matrix-core GEMV from 2..5 rows up to 8 per launch; the exact-split
 MFMA GEMM from 8..64 rows) and of the prefill tile rules
 (tbh_matmul_bf16_device: 64 / 128 / 256 rows), with ragged N and K, every
-INT8 mode, zero points, and INT4 in both flat layouts.  Each result is held
+INT8 mode, zero points, and INT4 in both flat layouts (runtime-layout INT4
+with N-blocks of 16, 32, 48, 128 rows).  Each result is held
 to the same bars as the other parity tests: dequantize() bit-exact against
 the oracle (QuantizedTensor.swift:182-246 restated), and the product within
 GATE (floored max relative error) of a float64 oracle over the same
@@ -83,8 +84,11 @@ FP32_CASES = [
     ("int4_nk_g64", 1024, 100),
     ("int4_nk_g128", 4096, 77),
     ("int4_nk_g32_zp", 512, 90),
-    ("int4_kn_g32", 2048, 1024),  # runtime layout on the burst GEMV
+    ("int4_kn_g32", 2048, 1024),  # runtime layout on the burst GEMV / MFMA GEMM (two N-blocks per tile)
     ("int4_kn_g32", 512, 96),
+    ("int4_kn_g16", 256, 96),     # N-blocks of 16 rows: four per GEMM tile
+    ("int4_kn_g128", 1000, 384),  # one N-block per GEMM tile
+    ("int4_kn_g48", 256, 96),     # N-blocks the GEMM tiles cannot hold: GEMV kernels at every M
     ("int4_kn_g64", 256, 100),    # groups that do not tile N: generic kernel
 ]
 
@@ -111,6 +115,8 @@ BF16_CASES = [
     ("int4_nk_g32", 2048, 1003),
     ("int4_nk_g128", 4096, 300),
     ("int4_nk_g32_zp", 512, 90),
+    ("int4_kn_g32", 2048, 1003 // 32 * 32),   # runtime layout
+    ("int4_kn_g16", 512, 80),
 ]
 
 

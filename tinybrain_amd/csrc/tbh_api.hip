@@ -768,8 +768,14 @@ static int64_t sgemv_min_rows(const tbh_weight &w) {
 // 7.8 / 9.7); INT4 4096x11008 M = 32 61.0 / 44.6; INT4 11008x4096 M = 32
 // 56.5 / 49.9 (M = 24 42.2 / 49.1); INT4 32000x2048 M = 64 101.7 / 67.5
 // (M = 48 76.5 / 78.4).
+// Runtime-layout INT4 has no matrix-core GEMV, so its GEMV route is the VALU
+// kernel four rows per launch: GEMM from 8 rows (2048x5632 M = 8 21.9 /
+// 13.8, 11008x4096 42.4 / 38.5) or 12 on weights under 8 Mi elements and on
+// N >= 16384 (2048x2048 M = 8 8.5 / 9.3, M = 12 12.5 / 9.4; 32000x2048 M = 8
+// 35.0 / 40.0, M = 12 49.6 / 39.2).
 static int64_t mfma_min_rows(const tbh_weight &w) {
     const int64_t nk = w.N * w.K;
+    if (w.path == Path::Int4NGroup) return nk >= ((int64_t)8 << 20) && w.N < 16384 ? 8 : 12;
     if (w.precision == TBH_PREC_INT8) return nk >= ((int64_t)8 << 20) ? 8 : 12;
     if (nk <= ((int64_t)24 << 20)) return 12;
     return w.N >= 16384 ? 64 : 32;

@@ -182,14 +182,15 @@ hipError_t launch_mgemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s);
 hipError_t launch_generic(const tbh_weight &w, const GemvArgs &a, hipStream_t s);
 
 // Prefill dequant-GEMM on bf16 MFMA (tbh_prefill.hip): x [M][ldx] bf16
-// bits, y [M][ldy] fp32.  Needs prefill_supported(w), K % 8 == 0, ldx % 8
-// == 0 and a 16-byte aligned x.
+// bits, y [M][ldy] fp32.  Needs prefill_supported(w) (INT8 rows, INT4
+// K-groups, runtime-layout INT4 whose N-blocks tile 64 outputs), K % 8 == 0,
+// ldx % 8 == 0 and a 16-byte aligned x.
 bool prefill_supported(const tbh_weight &w);
 hipError_t launch_prefill(const tbh_weight &w, const uint16_t *x, int64_t ldx, int64_t M, float *y,
                           int64_t ldy, hipStream_t s, const Scratch &scr);
 
-// The same GEMM for fp32 x [M][ldx] (16-byte aligned rows, K % 8 == 0, no
-// zero points): each x row is split exactly into three bf16 pieces and a zero
+// The same GEMM for fp32 x [M][ldx] (16-byte aligned rows, K % 8 == 0):
+// each x row is split exactly into three bf16 pieces and a zero
 // row, the four rows go through the bf16 MFMAs, and the epilogue adds each
 // row's four results (tbh_prefill.hip).  hipErrorInvalidValue for weights or
 // shapes it does not take.

@@ -63,6 +63,8 @@ struct PParams {
     int32_t chunks;  // 16-byte chunks per row
     int32_t G;       // INT4 K-groups per row
     int32_t cpg;     // chunks per K-group
+    int32_t rpn;     // runtime-layout INT4: rows per N-block (scales: [nbk][chunks * 32])
+    int32_t nbk;     // runtime-layout INT4: N-blocks
 };
 
 __device__ __forceinline__ void lds_barrier() {
@@ -101,18 +103,29 @@ __device__ __forceinline__ float sbyte(uint32_t w) {
     return (float)(int8_t)(uint8_t)(w >> (8 * J));
 }
 
-// XF (fp32 x): product row r is piece r % 4 of x row r / 4 (split3; piece 3
-// is zero), so the four rows a lane holds in each 16 x 16 accumulator tile
-// are the pieces of one x row, and the epilogue adds them into that row's
-// output.
+// XF = 1 (fp32 x): product row r is piece r % 4 of x row r / 4 (split3;
+// piece 3 is zero), so the four rows a lane holds in each 16 x 16
+// accumulator tile are the pieces of one x row, and the epilogue adds them
+// into that row's output.  XF = 2: the same from bf16 x (widened exactly).
+//
+// NC > 0: INT4 in the runtime layout (groups along N: one scale per
+// (N-block of rpn rows, k)).  The scale varies along K inside an MFMA, so it
+// goes on the x side: the tile's NC N-blocks each get their own LDS copy of
+// x, copy c holding split3(fl(x[k] * s[nb0 + c][k])) (fp32 product, split
+// exactly into three bf16 pieces), and an MFMA of output columns in N-block
+// c reads copy c against the exact integers 16 q.  Each term differs from the
+// reference's x * fl(q * s) only in which fp32 product is rounded.
 //
 // Eight-wave blocks with K steps of 64 are held to four waves per SIMD, so
 // two blocks share a CU.  INT4 blocks with K steps of 128 (256 VGPRs) run
 // every K step in its masked form: with a second, unmasked loop form their
 // spilled registers went from 2 to 14-17.
-template <int PREC, int BM, int BN, bool ZP, int WV, int BK, bool XF>
+template <int PREC, int BM, int BN, bool ZP, int WV, int BK, int XF, int NC>
 __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(WV == 8 && BK == 64 ? 4 : 1)))
 void gemm_bf16(const PParams p) {
+    static_assert(NC == 0 || (PREC == 4 && XF != 0 && !ZP), "runtime-layout INT4 stages split x, no zero points");
+    static_assert(XF != 2 || NC > 0, "bf16 x is split only for runtime-layout scales");
+    constexpr int NCC = NC > 0 ? NC : 1;                    // copies of x in LDS
     constexpr bool kTwoForm = !(PREC == 4 && BK == 128);   // unmasked form for steps inside K
     constexpr int kLdsRow = BK + kRowPad;
     constexpr int NT = 64 * WV;                   // threads; waves as 2 x (WV / 2)
@@ -128,9 +141,9 @@ void gemm_bf16(const PParams p) {
     static_assert(XSEG % NT == 0 && TN >= 1, "tile too small for the waves");
 
     // two LDS buffers: step t + 1 is staged while step t's MFMAs read
-    __shared__ __attribute__((aligned(16))) uint16_t xs[2][BM * kLdsRow];
+    __shared__ __attribute__((aligned(16))) uint16_t xs[2][NCC][BM * kLdsRow];
     __shared__ __attribute__((aligned(16))) uint16_t ws[2][BN * kLdsRow];
-    __shared__ float ssc[2][PREC == 4 ? BN * CPR : 1];   // INT4: scale of each (row, K-slice)
+    __shared__ float ssc[2][PREC == 4 && NC == 0 ? BN * CPR : 1];   // INT4 K-groups: scale of each (row, K-slice)
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int wm = wave / WC, wn = wave % WC;
@@ -151,12 +164,15 @@ void gemm_bf16(const PParams p) {
 
     // ---- global -> registers for one step, into register stage d of kDepth:
     // the loads of steps t+1 .. t+kDepth-1 are in flight while step t runs
-    // fp32 x: a segment is 8 fp32 of one x row (two 16-byte loads), staged
-    // as the four product rows of its pieces
+    // split x: a segment is 8 elements of one x row (two 16-byte loads of
+    // fp32, one of bf16), staged as the four product rows of its pieces; with
+    // runtime-layout scales an item is a (segment, copy) pair and also loads
+    // the copy's 8 scales
     constexpr int XSEGF = (BM / 4) * (BK / 8);
-    constexpr int XPTF = XF ? (XSEGF + NT - 1) / NT : 1;
+    constexpr int XPTF = XF ? (XSEGF * NCC + NT - 1) / NT : 1;
     constexpr int XPTL = XF ? XPTF : XPT;
-    u32x4 xr[kDepth][XPTL][XF ? 2 : 1];
+    u32x4 xr[kDepth][XPTL][XF == 1 ? 2 : 1];
+    u32x4 xsc[kDepth][NC > 0 ? XPTL : 1][2];
     bool xin[kDepth][XPTL];   // segment within K, applied at the LDS store
     u32x4 wr[kDepth][WPT];
     float sr[kDepth][WPT];
@@ -173,13 +189,27 @@ void gemm_bf16(const PParams p) {
         if constexpr (XF) {
 #pragma unroll
             for (int j = 0; j < XPTF; ++j) {
-                const int s = min(tid + NT * j, XSEGF - 1);   // threads past the last segment repeat it
+                const int i = min(tid + NT * j, XSEGF * NCC - 1);   // threads past the last item repeat it
+                const int s = NCC == 1 ? i : i % XSEGF;
                 const int qrow = s / (BK / 8), kq = s % (BK / 8);
                 const int m = min(m0 / 4 + qrow, p.Mout - 1), k = k0 + 8 * kq;
+                const int kk = k < p.K ? k : 0;
                 xin[d][j] = k < kend;
-                const float *src = p.xf + (int64_t)m * p.ldx + (k < p.K ? k : 0);
-                xr[d][j][0] = *(const u32x4 *)src;
-                xr[d][j][XF ? 1 : 0] = *(const u32x4 *)(src + 4);
+                if constexpr (XF == 1) {
+                    const float *src = p.xf + (int64_t)m * p.ldx + kk;
+                    xr[d][j][0] = *(const u32x4 *)src;
+                    xr[d][j][1] = *(const u32x4 *)(src + 4);
+                } else {
+                    xr[d][j][0] = *(const u32x4 *)(p.x + (int64_t)m * p.ldx + kk);
+                }
+                if constexpr (NC > 0) {
+                    // copy i / XSEGF: N-block n0 / rpn + copy (clamped; tiles
+                    // past the last N-block store nothing)
+                    const int nb = min(n0 / p.rpn + i / XSEGF, p.nbk - 1);
+                    const float *sp = p.scales + (int64_t)nb * (p.chunks * CE) + kk;
+                    xsc[d][j][0] = *(const u32x4 *)sp;
+                    xsc[d][j][1] = *(const u32x4 *)(sp + 4);
+                }
             }
         } else {
 #pragma unroll
@@ -206,11 +236,11 @@ void gemm_bf16(const PParams p) {
             // stored and K padding meets x = 0, so the values do not matter.
             const int64_t nn = in ? n : 0, cc = in ? c : 0;
             wr[d][j] = __builtin_nontemporal_load((const u32x4 *)(p.data + nn * p.row_bytes + cc * 16));
-            if (PREC == 4) {
+            if constexpr (PREC == 4 && NC == 0) {
                 const int64_t gi = kgroup_index(nn, cc / p.cpg, p.G);
                 sr[d][j] = p.scales[gi];
                 if (ZP) zq[d][j] = p.zp[gi];
-            } else if (ZP) {
+            } else if constexpr (ZP) {
                 zq[d][j] = p.zp[nn];
             }
         }
@@ -220,19 +250,29 @@ void gemm_bf16(const PParams p) {
     auto store_step = [&](int d, int bb, auto full) {
         constexpr bool FULL = decltype(full)::value && !XF && kTwoForm;
         if constexpr (XF) {
-            // segment (quad row qrow, kq) -> product rows 4 qrow + piece
+            // segment (quad row qrow, kq) of copy i / XSEGF -> product rows
+            // 4 qrow + piece
 #pragma unroll
             for (int j = 0; j < XPTF; ++j) {
-                const int s = tid + NT * j;
-                if (s < XSEGF) {
+                const int i = tid + NT * j;
+                if (i < XSEGF * NCC) {
+                    const int s = NCC == 1 ? i : i % XSEGF;
                     const int qrow = s / (BK / 8), kq = s % (BK / 8);
                     float pc[8][3];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        split3(xin[d][j] ? as_f32(xr[d][j][0][e]) : 0.0f, pc[e]);
-                        split3(xin[d][j] ? as_f32(xr[d][j][XF ? 1 : 0][e]) : 0.0f, pc[4 + e]);
+                    for (int h = 0; h < 8; ++h) {
+                        const int e = 4 * (h % 2) + h / 2;   // 0, 4, 1, 5, ...: the two loads' elements alternate
+                        float v;
+                        if constexpr (XF == 1) {
+                            v = as_f32(xr[d][j][e / 4][e % 4]);
+                        } else {   // bf16 element e: low half of word e / 2 when e is even
+                            const uint32_t wv = xr[d][j][0][e / 2];
+                            v = as_f32(e % 2 ? wv & 0xFFFF0000u : wv << 16);
+                        }
+                        if constexpr (NC > 0) v *= as_f32(xsc[d][j][e / 4][e % 4]);
+                        split3(xin[d][j] ? v : 0.0f, pc[e]);
                     }
-                    uint16_t *dst = &xs[bb][(4 * qrow) * kLdsRow + 8 * kq];
+                    uint16_t *dst = &xs[bb][NCC == 1 ? 0 : i / XSEGF][(4 * qrow) * kLdsRow + 8 * kq];
 #pragma unroll
                     for (int piece = 0; piece < 3; ++piece) {
                         uint32_t o[4];
@@ -248,7 +288,7 @@ void gemm_bf16(const PParams p) {
             for (int j = 0; j < XPT; ++j) {
                 const int s = tid + NT * j;
                 const int row = s / (BK / 8), kq = s % (BK / 8);
-                *(u32x4 *)&xs[bb][row * kLdsRow + 8 * kq] = FULL || xin[d][j] ? xr[d][j][0] : u32x4{0, 0, 0, 0};
+                *(u32x4 *)&xs[bb][0][row * kLdsRow + 8 * kq] = FULL || xin[d][j] ? xr[d][j][0] : u32x4{0, 0, 0, 0};
             }
         }
 #pragma unroll
@@ -294,7 +334,7 @@ void gemm_bf16(const PParams p) {
                         o[3] = pack_hi16(sbyte<1>(hi) - zf, sbyte<3>(hi) - zf);
                         *(u32x4 *)(dst + 8 * q) = u32x4{o[0], o[1], o[2], o[3]};
                     }
-                    ssc[bb][s] = sr[d][j];
+                    if constexpr (NC == 0) ssc[bb][s] = sr[d][j];
                 }
             }
         }
@@ -306,19 +346,32 @@ void gemm_bf16(const PParams p) {
 #pragma unroll
         for (int b = 0; b < TN; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+    // runtime-layout scales: copy c serves the tile's columns [c, c + 1) * BN / NC
+    constexpr int kColsPerCopy = BN / NCC;
+    constexpr bool kWaveOneCopy = kColsPerCopy >= WN;   // all of a wave's columns in one copy
+    static_assert(kColsPerCopy % 16 == 0, "an MFMA's 16 columns lie in one N-block");
     auto compute = [&](int bb) {
 #pragma unroll
         for (int ks = 0; ks < BK / 32; ++ks) {
             const int kofs = ks * 32 + 8 * (lane >> 4);
             bf16x8 af[TM];
+            if constexpr (kWaveOneCopy) {
+                const int cw = NCC == 1 ? 0 : (wn * WN) / kColsPerCopy;
 #pragma unroll
-            for (int a = 0; a < TM; ++a)
-                af[a] = *(const bf16x8 *)&xs[bb][(wm * WM + a * 16 + (lane & 15)) * kLdsRow + kofs];
+                for (int a = 0; a < TM; ++a)
+                    af[a] = *(const bf16x8 *)&xs[bb][cw][(wm * WM + a * 16 + (lane & 15)) * kLdsRow + kofs];
+            }
 #pragma unroll
             for (int b = 0; b < TN; ++b) {
                 const int wrow = wn * WN + b * 16 + (lane & 15);
                 const bf16x8 bfr = *(const bf16x8 *)&ws[bb][wrow * kLdsRow + kofs];
-                if (PREC == 8) {
+                if constexpr (!kWaveOneCopy) {
+                    const int cb = (wn * WN + b * 16) / kColsPerCopy;
+#pragma unroll
+                    for (int a = 0; a < TM; ++a)
+                        af[a] = *(const bf16x8 *)&xs[bb][cb][(wm * WM + a * 16 + (lane & 15)) * kLdsRow + kofs];
+                }
+                if (PREC == 8 || NC > 0) {
 #pragma unroll
                     for (int a = 0; a < TM; ++a)
                         acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[a], bfr, acc[a][b], 0, 0, 0);
@@ -475,28 +528,33 @@ __global__ __launch_bounds__(256) void split_sum(const float *__restrict__ part,
     }
 }
 
-template <int PREC, int BM, int BN, int BK>
+template <int PREC, int BM, int BN, int BK, int NC>
 hipError_t launch_tile(const PParams &p, int splits, hipStream_t s) {
     static const int waves = [] {   // 4 or 8 forces the waves per block
         const char *v = std::getenv("TBH_PREFILL_WAVES");
         return v && *v ? std::atoi(v) : 0;
     }();
     const dim3 grid((unsigned)((p.Np + BN - 1) / BN), (unsigned)((p.M + BM - 1) / BM), (unsigned)splits);
-    const bool w8 = waves == 8 || (waves != 4 && BN == 128 && (p.M >= 256 || PREC == 4));
-    if (p.xf) {   // fp32 x
-        if (p.zp) {
-            if (w8) hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, true, 8, BK, true>), grid, dim3(512), 0, s, p);
-            else hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, true, 4, BK, true>), grid, dim3(256), 0, s, p);
-        } else {
-            if (w8) hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, false, 8, BK, true>), grid, dim3(512), 0, s, p);
-            else hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, false, 4, BK, true>), grid, dim3(256), 0, s, p);
-        }
-    } else if (p.zp) {
-        if (w8) hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, true, 8, BK, false>), grid, dim3(512), 0, s, p);
-        else hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, true, 4, BK, false>), grid, dim3(256), 0, s, p);
+    if constexpr (NC > 0) {   // runtime-layout INT4: split x (fp32, or bf16 widened), four waves
+        if (p.xf) hipLaunchKernelGGL((gemm_bf16<4, BM, BN, false, 4, BK, 1, NC>), grid, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL((gemm_bf16<4, BM, BN, false, 4, BK, 2, NC>), grid, dim3(256), 0, s, p);
     } else {
-        if (w8) hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, false, 8, BK, false>), grid, dim3(512), 0, s, p);
-        else hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, false, 4, BK, false>), grid, dim3(256), 0, s, p);
+        const bool w8 = waves == 8 || (waves != 4 && BN == 128 && (p.M >= 256 || PREC == 4));
+        if (p.xf) {   // fp32 x
+            if (p.zp) {
+                if (w8) hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, true, 8, BK, 1, 0>), grid, dim3(512), 0, s, p);
+                else hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, true, 4, BK, 1, 0>), grid, dim3(256), 0, s, p);
+            } else {
+                if (w8) hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, false, 8, BK, 1, 0>), grid, dim3(512), 0, s, p);
+                else hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, false, 4, BK, 1, 0>), grid, dim3(256), 0, s, p);
+            }
+        } else if (p.zp) {
+            if (w8) hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, true, 8, BK, 0, 0>), grid, dim3(512), 0, s, p);
+            else hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, true, 4, BK, 0, 0>), grid, dim3(256), 0, s, p);
+        } else {
+            if (w8) hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, false, 8, BK, 0, 0>), grid, dim3(512), 0, s, p);
+            else hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, false, 4, BK, 0, 0>), grid, dim3(256), 0, s, p);
+        }
     }
     return hipGetLastError();
 }
@@ -515,7 +573,7 @@ constexpr int kMinSplitK = 256;  // K a split keeps at least
 
 // K is split over blocks when there are fewer than bpc blocks per CU.  BK:
 // K per staged step (64 or 128).
-template <int PREC, int BM, int BN, int BK = kBK>
+template <int PREC, int BM, int BN, int BK = kBK, int NC = 0>
 hipError_t launch_split(const tbh_weight &w, PParams p, int64_t tiles, int bpc, hipStream_t s,
                         const Scratch &scr) {
     const int nsteps = (int)((p.chunks * (PREC == 8 ? kInt8ChunkElems : kInt4ChunkElems) + BK - 1) / BK);
@@ -544,7 +602,7 @@ hipError_t launch_split(const tbh_weight &w, PParams p, int64_t tiles, int bpc, 
         p.y = part;
         p.split_stride = n;
     }
-    hipError_t e = launch_tile<PREC, BM, BN, BK>(p, splits, s);
+    hipError_t e = launch_tile<PREC, BM, BN, BK, NC>(p, splits, s);
     if (e != hipSuccess || splits == 1) return e;
     const int64_t grid_cap = 4 * cus;
     if (n % 4 == 0 && ((uintptr_t)y & 15) == 0) {
@@ -611,10 +669,38 @@ hipError_t launch_prec(const tbh_weight &w, const PParams &p, hipStream_t s, con
     return launch_split<PREC, 64, 64>(w, p, t64, 2, s, scr);
 }
 
+// Copies of x a 64-column tile of a runtime-layout INT4 weight needs (its
+// N-blocks), or 0 when the N-blocks do not tile the 64 columns evenly.
+int ng_copies(const tbh_weight &w) {
+    const int64_t rpn = w.rows_per_nblock;
+    if (rpn >= w.Np || rpn % 64 == 0) return 1;
+    if (rpn == 32) return 2;
+    if (rpn == 16) return 4;
+    return 0;
+}
+
+// Runtime-layout INT4 (one scale per (N-block, k)) with x given as p.x (bf16)
+// or p.xf (fp32), p.M = 4 * x rows: 64 x 64 tiles (16 x rows by 64
+// outputs), four waves, split along K to two blocks per CU when the tiles
+// are fewer.
+hipError_t launch_ngroup(const tbh_weight &w, PParams p, hipStream_t s, const Scratch &scr) {
+    p.rpn = w.rows_per_nblock;
+    p.nbk = (int32_t)((w.Np + w.rows_per_nblock - 1) / w.rows_per_nblock);
+    const int64_t tiles = ((p.Np + 63) / 64) * ((p.M + 63) / 64);
+    switch (ng_copies(w)) {
+    case 1: return launch_split<4, 64, 64, kBK, 1>(w, p, tiles, 2, s, scr);
+    case 2: return launch_split<4, 64, 64, kBK, 2>(w, p, tiles, 2, s, scr);
+    case 4: return launch_split<4, 64, 64, kBK, 4>(w, p, tiles, 2, s, scr);
+    default: return hipErrorInvalidValue;
+    }
+}
+
 }  // namespace
 
 bool prefill_supported(const tbh_weight &w) {
-    return !w.mfma_tiles && (w.path == Path::Int8Row || w.path == Path::Int4KGroup);
+    if (w.mfma_tiles) return false;
+    if (w.path == Path::Int4NGroup) return !w.ng_pairs && !w.zp && ng_copies(w) > 0;
+    return w.path == Path::Int8Row || w.path == Path::Int4KGroup;
 }
 
 static PParams prefill_params(const tbh_weight &w, int64_t ldx, float *y, int64_t ldy) {
@@ -645,6 +731,7 @@ hipError_t launch_prefill_f32(const tbh_weight &w, const float *x, int64_t ldx, 
     p.xf = x;
     p.M = (int32_t)(4 * M);
     p.Mout = (int32_t)M;
+    if (w.path == Path::Int4NGroup) return launch_ngroup(w, p, s, scr);
     return w.precision == TBH_PREC_INT8 ? launch_prec<8>(w, p, s, scr) : launch_prec<4>(w, p, s, scr);
 }
 
@@ -653,6 +740,14 @@ hipError_t launch_prefill(const tbh_weight &w, const uint16_t *x, int64_t ldx, i
     if (!prefill_supported(w) || M < 1 || w.K % 8 != 0 || ldx % 8 != 0 ||
         ((uintptr_t)x & 15) != 0)
         return hipErrorInvalidValue;
+    if (w.path == Path::Int4NGroup) {   // x rows split into three bf16 pieces after the scale
+        if (4 * M > INT32_MAX) return hipErrorInvalidValue;
+        PParams p = prefill_params(w, ldx, y, ldy);
+        p.x = x;
+        p.M = (int32_t)(4 * M);
+        p.Mout = (int32_t)M;
+        return launch_ngroup(w, p, s, scr);
+    }
     PParams p{};
     p.x = x;
     p.ldx = ldx;
