@@ -470,7 +470,10 @@ def measure_decode(args, backend, T, torch, workload):
     Returns the result object (the bench line's fields)."""
     prec, gs, c, ctx = DECODE[workload]
     dev = torch.device("cuda", 0)
-    cfg = T.DecoderConfig(max_seq=ctx + args.warmup + args.steps + 8, **c)
+    need = ctx + args.warmup + args.steps + 8
+    if args.max_seq and args.max_seq < need:
+        raise SystemExit(f"--max-seq {args.max_seq} is below the {need} positions this run fills")
+    cfg = T.DecoderConfig(max_seq=args.max_seq or need, **c)
     layer, lm = decode_shapes(c)
     t_setup = time.perf_counter()
     # One random init per projection shape; every layer gets its own device
@@ -528,7 +531,7 @@ def measure_decode(args, backend, T, torch, workload):
         "dtype": "f32",
         "data": "synthetic",
         "config": {
-            "workload": workload, **c, "context": ctx,
+            "workload": workload, **c, "context": ctx, "max_seq": cfg.max_seq,
             "weights": ("INT8 symmetric per output channel" if prec == "int8" else
                         "INT4 symmetric, group 32 along K (converter layout)") +
                        "; one random init per projection shape, a device copy per layer",
@@ -821,6 +824,9 @@ def main():
                     choices=sorted(WORKLOADS) + sorted(PREFILL) + sorted(DECODE) + sorted(PROJ) + sorted(OPS))
     ap.add_argument("--pool-gib", type=float, default=2.2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--max-seq", type=int, default=0,
+                    help="decode workloads: the decoder's cache length (default: the context plus the "
+                         "steps replayed)")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-decode", action="store_true",
                     help="int4_g32_gemv_m1: leave out the 1.1B decode-step measurement")
