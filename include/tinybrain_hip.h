@@ -186,7 +186,13 @@ tbh_status tbh_matmul(tbh_device *dev, const float *x, int64_t M, int64_t K,
                       const tbh_weight *w, float *y);
 
 /* Same product on device pointers, enqueued on `stream` (a hipStream_t of the
- * weight's device; NULL = the null stream).  Returns after the launch. */
+ * weight's device; NULL = the null stream).  Returns after the launch.
+ * Launches that split K (matrix-core GEMV, MFMA GEMM) keep their partial sums
+ * in a workspace the library allocates per (device, stream) on first use and
+ * keeps, with every buffer it outgrew, until tbh_device_close (a graph
+ * captured on the stream may still hold them): a caller that creates many
+ * short-lived streams should reuse a few, or call
+ * tbh_matmul_device_noalloc. */
 tbh_status tbh_matmul_device(const tbh_weight *w, const float *x, int64_t M,
                              int64_t K, float *y, void *stream);
 
