@@ -870,6 +870,13 @@ bool burst_shape(const tbh_weight &w, const KParams &p, int M, int *I_out, int *
         if (4 * I <= 16 && w.Np / 4 >= 8 * cus) U = 4;
         else if (2 * I <= 16) U = 2;
     } else {
+        // two or four x rows: at least two rows per wave (the block stages its
+        // x rows once for 4 U weight rows; us per launch, U = 1 / 2, M = 2
+        // and 4: INT4 5632x2048 4.49 / 4.35, 6.69 / 5.61; INT8 5632x2048
+        // 4.69 / 4.42, 6.80 / 5.67; INT4 2048x2048 3.16 / 3.11, 4.08 / 3.78),
+        // more while that still leaves burst_wpc waves per CU (INT4
+        // 32000x2048 at M = 4: U = 4 16.8 us, U = 2 19.5)
+        if (2 * I <= 16) U = 2;
         while (2 * U * I <= 16 && 2 * U * M <= 32 && w.Np / (2 * U) >= burst_wpc * cus) U *= 2;
     }
     if (u_force > 0 && u_force * I <= 16 && u_force * M <= 32 && (u_force & (u_force - 1)) == 0) U = u_force;
