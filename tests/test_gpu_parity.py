@@ -176,6 +176,33 @@ def test_burst_shapes(backend, prec, K, N):
         backend.set_option(_abi.OPT_SGEMV_MIN_ROWS, 0)
 
 
+@pytest.mark.parametrize("kind,K,N", [
+    ("int8", 2048, 5632),     # INT8 under 16384 outputs: 8 rows on one burst launch, the GEMM from 9
+    ("int8", 2048, 1003),     # ragged N
+    ("int8", 1000, 64),       # K off the chunk multiple
+    ("int4", 2048, 2048),     # configs[1] shape the matrix-core GEMV never takes
+    ("int4", 4096, 520),      # two chunk iterations per row (the matrix-core GEMV switched off)
+    ("int4kn", 2048, 5632),   # runtime layout (groups along N)
+])
+def test_burst_eight_rows(backend, kind, K, N):
+    # eight x rows in one burst GEMV launch: each row's chunk unpacked once,
+    # the x rows taken one at a time; M = 9 and 16 add the tails
+    if kind == "int8":
+        oq = _int8_pc(0x8B + K + N, K, N)
+        pq = _product(oq, (K, N))
+    elif kind == "int4":
+        oq = _int4_nk(0x8C + K + N, K, N, 32)
+        pq = _product(oq, (K, N), T.Layout.NK_FLAT)
+    else:
+        oq = _int4_kn(0x8D + K + N, K, N, 32)
+        pq = _product(oq, (K, N))
+    backend.set_option(_abi.OPT_SGEMV_MIN_ROWS, 9)
+    try:
+        _check(backend, pq, oq, Ms=(8, 9, 16), cpu_path=False)
+    finally:
+        backend.set_option(_abi.OPT_SGEMV_MIN_ROWS, 0)
+
+
 @pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 11008), (11008, 4096), (4096, 32000)])
 def test_int4_7b_projection_shapes(backend, K, N):
     # the 7B projection set (q/k/v/o, gate/up, down, LM

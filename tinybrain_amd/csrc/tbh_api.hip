@@ -773,10 +773,17 @@ static int64_t sgemv_min_rows(const tbh_weight &w) {
 // 13.8, 11008x4096 42.4 / 38.5) or 12 on weights under 8 Mi elements and on
 // N >= 16384 (2048x2048 M = 8 8.5 / 9.3, M = 12 12.5 / 9.4; 32000x2048 M = 8
 // 35.0 / 40.0, M = 12 49.6 / 39.2).
-static int64_t mfma_min_rows(const tbh_weight &w) {
+//
+// burst8: the weight takes eight rows of this x in one burst GEMV launch
+// (gemv8_supported).  Below 16384 outputs that launch beats the GEMM at
+// exactly 8 rows (us per call, GEMM / one 8-row launch: INT8 5632x2048 11.2
+// / 9.2, 11264x2048 15.4 / 15.7; runtime-layout INT4 5632x2048 13.1 / 9.9;
+// INT8 32000x2048 27.4 / 32.4), so those weights start the GEMM at 9.
+static int64_t mfma_min_rows(const tbh_weight &w, bool burst8) {
     const int64_t nk = w.N * w.K;
-    if (w.path == Path::Int4NGroup) return nk >= ((int64_t)8 << 20) && w.N < 16384 ? 8 : 12;
-    if (w.precision == TBH_PREC_INT8) return nk >= ((int64_t)8 << 20) ? 8 : 12;
+    const bool big = nk >= ((int64_t)8 << 20);
+    if (w.path == Path::Int4NGroup) return big && w.N < 16384 ? (burst8 ? 9 : 8) : 12;
+    if (w.precision == TBH_PREC_INT8) return big ? (burst8 && w.N < 16384 ? 9 : 8) : 12;
     if (nk <= ((int64_t)24 << 20)) return 12;
     return w.N >= 16384 ? 64 : 32;
 }
@@ -786,7 +793,8 @@ static tbh_status matmul_enqueue(const tbh_weight *w, const float *x, int64_t M,
     if (!weight_arrays_ok(*w))
         return set_error(TBH_E_INVALID, "weight device arrays are inconsistent with its layout");
     const int mfma_forced = w->dev->mfma_min_rows.load(std::memory_order_relaxed);
-    const int64_t mfma_min = mfma_forced > 0 ? mfma_forced : mfma_min_rows(*w);
+    const bool burst8 = !w->mfma_tiles && gemv8_supported(*w, x, w->K);
+    const int64_t mfma_min = mfma_forced > 0 ? mfma_forced : mfma_min_rows(*w, burst8);
     // The GEMV kernels stage a whole row of x in LDS; past about 13 K (INT8)
     // or 14.5 K (INT4) elements it does not fit, and every row count goes to
     // the MFMA GEMM, which streams K through LDS in steps.
@@ -814,13 +822,18 @@ static tbh_status matmul_enqueue(const tbh_weight *w, const float *x, int64_t M,
     const int forced = w->dev->sgemv_min_rows.load(std::memory_order_relaxed);
     const int64_t sg_min = forced > 0 ? std::max(2, forced) : sgemv_min_rows(*w);
     const bool sg = M >= sg_min && sgemv_supported(*w);
-    const int64_t rows = w->mfma_tiles || sg ? 8 : gemv_max_rows(*w);
+    // eight rows at a time on the burst GEMV when the weight and x allow it
+    // and the matrix-core GEMV does not take them (INT4 2048x2048 at M = 8:
+    // 6.9 us as two 4-row launches, 4.8 us as one)
+    const bool b8 = burst8 && M >= 8;
+    const int64_t rows = w->mfma_tiles || sg || b8 ? 8 : gemv_max_rows(*w);
     for (int64_t m0 = 0; m0 < M;) {
         int64_t mc = rows > 0 ? std::min(rows, M - m0) : M - m0;
         GemvArgs a{x + m0 * w->K, w->K, y + m0 * w->N, w->N, mc};
         hipError_t e = hipErrorInvalidValue;
         if (w->mfma_tiles) e = launch_mgemv(*w, a, s);
-        else if (sg && mc >= sg_min) e = launch_sgemv(*w, a, s, scr);
+        else if (b8 && mc == 8 && !sg) e = launch_gemv(*w, a, s);
+        if (e == hipErrorInvalidValue && !w->mfma_tiles && sg && mc >= sg_min) e = launch_sgemv(*w, a, s, scr);
         if (e == hipErrorOutOfMemory && scr.is_fixed())
             return set_error(TBH_E_INVALID, "this call needs " + std::to_string(scr.shortfall) +
                                                 " bytes of scratch; the no-allocation entry point holds " +

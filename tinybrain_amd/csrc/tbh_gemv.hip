@@ -603,7 +603,69 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
 #pragma unroll
     for (int i = 0; i < I; ++i) {
         const int c = lane + 64 * i;
-        if (i < I - 1 || c < p.chunks) {
+        if constexpr (M >= 8) {
+            // eight x rows: each row's chunk is unpacked once into f16
+            // pairs, then the x rows are taken one at a time (all eight
+            // rows' x chunks at once would not fit the registers)
+            if (i < I - 1 || c < p.chunks) {
+                constexpr int XQ = CE / 4;
+                constexpr int NPAIR = CE / 2;   // f16 pairs per chunk
+                h2 ph[U][NPAIR];
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        const uint32_t wv = w[i][u][d];
+                        if (PREC == 8) {
+                            const h2 c8 = splat(-1152.0f);
+                            ph[u][2 * d] = as_h2(and_or(wv, kLo, kMagic)) + c8;
+                            ph[u][2 * d + 1] = as_h2(and_or(wv >> 8, kLo, kMagic)) + c8;
+                        } else {
+                            const h2 c1 = splat(-1032.0f), c16 = splat(-1152.0f);
+                            const uint32_t w8 = wv >> 8;
+                            ph[u][4 * d] = as_h2(and_or(wv, kLo, kMagic)) + c1;
+                            ph[u][4 * d + 1] = as_h2(and_or(wv, kHi, kMagic)) + c16;
+                            ph[u][4 * d + 2] = as_h2(and_or(w8, kLo, kMagic)) + c1;
+                            ph[u][4 * d + 3] = as_h2(and_or(w8, kHi, kMagic)) + c16;
+                        }
+                    }
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    float4 xq[XQ];
+#pragma unroll
+                    for (int q = 0; q < XQ; ++q) xq[q] = xs4[(m * lds_row + c * CS + 4 * q) >> 2];
+#pragma unroll
+                    for (int u = 0; u < U; ++u) {
+                        float a0 = PREC == 8 ? acc[m][u] : 0.0f, a1 = 0.0f;
+#pragma unroll
+                        for (int d = 0; d < 4; ++d) {
+                            if (PREC == 8) {
+                                const h2 p0 = ph[u][2 * d], p1 = ph[u][2 * d + 1];
+                                a0 = fmix(p0.x, xq[d].x, a0);
+                                a1 = fmix(p1.x, xq[d].z, a1);
+                                a0 = fmix(p0.y, xq[d].y, a0);
+                                a1 = fmix(p1.y, xq[d].w, a1);
+                            } else {
+                                const h2 p0 = ph[u][4 * d], p1 = ph[u][4 * d + 1];
+                                const h2 p2 = ph[u][4 * d + 2], p3 = ph[u][4 * d + 3];
+                                const float4 xa = xq[2 * d], xb = xq[2 * d + 1];
+                                a0 = fmix(p0.x, xa.x, a0);
+                                a1 = fmix(p2.x, xb.x, a1);
+                                a0 = fmix(p0.y, xa.y, a0);
+                                a1 = fmix(p2.y, xb.y, a1);
+                                a0 = fmix(p1.x, xa.z, a0);
+                                a1 = fmix(p3.x, xb.z, a1);
+                                a0 = fmix(p1.y, xa.w, a0);
+                                a1 = fmix(p3.y, xb.w, a1);
+                            }
+                        }
+                        if (PREC == 8) acc[m][u] = a0 + a1;
+                        else acc[m][u] = NG > 0 ? acc[m][u] + (a0 + a1)
+                                                : __builtin_fmaf(s[i][u], a0 + a1, acc[m][u]);
+                    }
+                }
+            }
+        } else if (i < I - 1 || c < p.chunks) {
             constexpr int XQ = CE / 4;  // float4 of x per chunk and x row
             float4 xq[XC][XQ];
 #pragma unroll
@@ -733,13 +795,16 @@ int env_int(const char *name, int dflt) {
 }
 
 // Burst-kernel shapes: chunk iterations per row I <= kBurstMaxI, rows per
-// wave U a power of two with U * I <= 16.
+// wave U a power of two with U * I <= 16.  Eight x rows take rows of at most
+// 2 x 64 chunks (K <= 2048 INT8 or 4096 INT4) and up to 80 KB of LDS (two
+// blocks per CU).
 constexpr int kBurstMaxI = 6;
+constexpr int64_t kBurst8LdsBytes = 80 * 1024;
 
 template <int PREC, int M, int U, int I, int PRO, int EPI, int NG>
 hipError_t launch_burst_one(const KParams &p, size_t lds, hipStream_t s) {
     if constexpr (U * I > 16 || M * U > 32 || (EPI == EPI_SILU_PAIR && (U < 2 || M != 1)) ||
-                  (NG > 0 && PREC != 4) || (NG == 2 && (M != 1 || U % 2 != 0))) {
+                  (NG > 0 && PREC != 4) || (NG == 2 && (M != 1 || U % 2 != 0)) || (M == 8 && I > 2)) {
         return hipErrorInvalidValue;
     } else {
         const int64_t waves = (p.Np + U - 1) / U;
@@ -780,6 +845,7 @@ hipError_t burst_m(int M, int I, int U, const KParams &p, size_t lds, hipStream_
     case 1: return burst_i<PREC, 1, PRO_NONE, EPI_STORE, NG>(I, U, p, lds, s);
     case 2: return burst_i<PREC, 2, PRO_NONE, EPI_STORE, NG>(I, U, p, lds, s);
     case 4: return burst_i<PREC, 4, PRO_NONE, EPI_STORE, NG>(I, U, p, lds, s);
+    case 8: return burst_i<PREC, 8, PRO_NONE, EPI_STORE, NG>(I, U, p, lds, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -853,8 +919,8 @@ bool burst_shape(const tbh_weight &w, const KParams &p, int M, int *I_out, int *
     const bool ng = w.path == Path::Int4NGroup;
     const int copies = w.ng_pairs ? 2 : M;   // x copies the block stages in LDS
     const int64_t blds = (int64_t)copies * 64 * I * (ce + 4) * (int64_t)sizeof(float);
-    if (kernel_sel || !(M == 1 || M == 2 || M == 4) || w.zp != nullptr || I > kBurstMaxI || !p.x_vec4 ||
-        blds > kMaxLdsBytes || !(w.path == Path::Int8Row || w.path == Path::Int4KGroup || ng) ||
+    if (kernel_sel || !(M == 1 || M == 2 || M == 4 || M == 8) || w.zp != nullptr || I > kBurstMaxI ||
+        !p.x_vec4 || blds > (M == 8 ? kBurst8LdsBytes : kMaxLdsBytes) || (M == 8 && I > 2) || !(w.path == Path::Int8Row || w.path == Path::Int4KGroup || ng) ||
         (w.path == Path::Int4KGroup && p.cpg_shift < 0) || w.mfma_tiles || (w.ng_pairs && M != 1) ||
         (ng && (p.rpn <= 0 || p.Kp % 4 != 0)))
         return false;
@@ -901,6 +967,15 @@ bool burst_shape(const tbh_weight &w, const KParams &p, int M, int *I_out, int *
 
 }  // namespace
 
+bool gemv8_supported(const tbh_weight &w, const float *x, int64_t ldx) {
+    if (w.ng_pairs) return false;
+    GemvArgs a{x, ldx, nullptr, w.N, 8};
+    KParams p = make_params(w, a);
+    int I, U;
+    int64_t lds;
+    return burst_shape(w, p, 8, &I, &U, &lds);
+}
+
 bool gemv_fused_supported(const tbh_weight &w) {
     GemvArgs a{nullptr, w.K, nullptr, w.N, 1};
     KParams p = make_params(w, a);
@@ -935,6 +1010,15 @@ hipError_t launch_gemv_fused(const tbh_weight &w, const FusedGemvArgs &f, hipStr
 
 hipError_t launch_gemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s) {
     const int M = (int)a.M;
+    if (M == 8 && !w.ng_pairs) {   // the burst kernel only
+        KParams p = make_params(w, a);
+        int I, U;
+        int64_t blds;
+        if (!burst_shape(w, p, 8, &I, &U, &blds)) return hipErrorInvalidValue;
+        if (w.path == Path::Int8Row) return burst_m<8>(8, I, U, p, (size_t)blds, s);
+        return w.path == Path::Int4NGroup ? burst_m<4, 1>(8, I, U, p, (size_t)blds, s)
+                                          : burst_m<4>(8, I, U, p, (size_t)blds, s);
+    }
     if (M < 1 || M > 4 || w.ng_pairs) return hipErrorInvalidValue;
     const int64_t lds = lds_bytes_for(w, M);
     if (lds > kMaxLdsBytes) return hipErrorInvalidValue;
