@@ -344,19 +344,36 @@ __device__ __forceinline__ float act(float x, float s2p) {
     return 0.5f * x * (1.0f + tanhf(inner));
 }
 
-template <int A, bool VEC>
+// Elementwise.  Vector form: each thread takes UN 16-byte pieces per pass,
+// their loads issued before any compute (us per call on 2048 x 5632, UN / grid
+// cap in blocks per CU: SiLU 1 / 8 19.1, 2 / 16 18.6, 4 / 8 20.0; GELU 19.6,
+// 18.6, 19.9).
+template <int A, bool VEC, int UN>
 __global__ __launch_bounds__(256) void activation(const float *__restrict__ x, float *__restrict__ y, int64_t n,
                                                   float s2p) {
-    const int64_t stride = (int64_t)gridDim.x * 256;
-    const int64_t i0 = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (VEC) {
-        for (int64_t i = i0; i < n / 4; i += stride) {
-            const float4 v = ((const float4 *)x)[i];
-            ((float4 *)y)[i] = float4{act<A>(v.x, s2p), act<A>(v.y, s2p), act<A>(v.z, s2p), act<A>(v.w, s2p)};
+        const int64_t n4 = n / 4;
+        const int64_t stride = (int64_t)gridDim.x * 256 * UN;
+        for (int64_t i = (int64_t)blockIdx.x * 256 * UN + threadIdx.x; i < n4; i += stride) {
+            float4 v[UN];
+#pragma unroll
+            for (int j = 0; j < UN; ++j) {
+                const int64_t e = i + 256 * j;
+                v[j] = ((const float4 *)x)[e < n4 ? e : i];   // past the end: re-read a valid piece
+            }
+#pragma unroll
+            for (int j = 0; j < UN; ++j) {
+                const int64_t e = i + 256 * j;
+                if (e < n4)
+                    ((float4 *)y)[e] = float4{act<A>(v[j].x, s2p), act<A>(v[j].y, s2p), act<A>(v[j].z, s2p),
+                                              act<A>(v[j].w, s2p)};
+            }
         }
-        for (int64_t i = (n / 4) * 4 + i0; i < n; i += stride) y[i] = act<A>(x[i], s2p);
+        const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+        if (t < n - n4 * 4) y[n4 * 4 + t] = act<A>(x[n4 * 4 + t], s2p);
     } else {
-        for (int64_t i = i0; i < n; i += stride) y[i] = act<A>(x[i], s2p);
+        const int64_t stride = (int64_t)gridDim.x * 256;
+        for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) y[i] = act<A>(x[i], s2p);
     }
 }
 
@@ -854,9 +871,15 @@ float gelu_s2p() { return std::sqrt(2.0f / 3.14159265358979f); }
 template <int A>
 hipError_t launch_act(const tbh_device *dev, const float *x, int64_t n, float *y, hipStream_t s) {
     const bool vec = aligned16(x) && aligned16(y);
-    const unsigned grid = grid_for(((vec ? n / 4 : n) + 255) / 256, dev);
-    if (vec) hipLaunchKernelGGL((activation<A, true>), dim3(grid), dim3(256), 0, s, x, y, n, gelu_s2p());
-    else hipLaunchKernelGGL((activation<A, false>), dim3(grid), dim3(256), 0, s, x, y, n, gelu_s2p());
+    constexpr int UN = 2;
+    const int64_t cus = std::max(1, dev->cu_count);
+    const unsigned grid = vec ? (unsigned)std::max<int64_t>(1, std::min((n / 4 + 256 * UN - 1) / (256 * UN), 16 * cus))
+                              : grid_for((n + 255) / 256, dev);
+    if (vec) {
+        hipLaunchKernelGGL((activation<A, true, UN>), dim3(grid), dim3(256), 0, s, x, y, n, gelu_s2p());
+    } else {
+        hipLaunchKernelGGL((activation<A, false, 1>), dim3(grid), dim3(256), 0, s, x, y, n, gelu_s2p());
+    }
     return hipGetLastError();
 }
 
