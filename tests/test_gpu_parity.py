@@ -186,7 +186,9 @@ def test_burst_shapes(backend, prec, K, N):
 ])
 def test_burst_eight_rows(backend, kind, K, N):
     # eight x rows in one burst GEMV launch: each row's chunk unpacked once,
-    # the x rows taken one at a time; M = 9 and 16 add the tails
+    # the x rows taken one at a time; five to seven rows on the same launch
+    # and three on the four-row one, the rows past M masked; M = 9 and 16
+    # add the tails
     if kind == "int8":
         oq = _int8_pc(0x8B + K + N, K, N)
         pq = _product(oq, (K, N))
@@ -198,7 +200,7 @@ def test_burst_eight_rows(backend, kind, K, N):
         pq = _product(oq, (K, N))
     backend.set_option(_abi.OPT_SGEMV_MIN_ROWS, 9)
     try:
-        _check(backend, pq, oq, Ms=(8, 9, 16), cpu_path=False)
+        _check(backend, pq, oq, Ms=(3, 5, 6, 7, 8, 9, 11, 16), cpu_path=False)
     finally:
         backend.set_option(_abi.OPT_SGEMV_MIN_ROWS, 0)
 

@@ -827,7 +827,10 @@ static tbh_status matmul_enqueue(const tbh_weight *w, const float *x, int64_t M,
     // 6.9 us as two 4-row launches, 4.8 us as one), or takes them on a weight
     // of at most 12 Mi elements (INT4 5632x2048: 9.0 us there, 8.6-8.9 us as
     // one burst launch; 8192x2048: 9.2-9.4 against 10.5-11.0)
-    const bool b8 = burst8 && M >= 8;
+    // (five to seven rows: the same launch with the rows past M masked;
+    // INT4 2048x2048 at M = 5 / 7: 6.3 / 8.2 us as 4 + 1 / 4 + 3 rows, 5.0 /
+    // 5.0 us as one launch)
+    const bool b8 = burst8 && M >= 5;
     const bool b8_over_sg = w->N * w->K <= ((int64_t)12 << 20);
     const int64_t rows = w->mfma_tiles || sg || b8 ? 8 : gemv_max_rows(*w);
     for (int64_t m0 = 0; m0 < M;) {
@@ -835,7 +838,7 @@ static tbh_status matmul_enqueue(const tbh_weight *w, const float *x, int64_t M,
         GemvArgs a{x + m0 * w->K, w->K, y + m0 * w->N, w->N, mc};
         hipError_t e = hipErrorInvalidValue;
         if (w->mfma_tiles) e = launch_mgemv(*w, a, s);
-        else if (b8 && mc == 8 && (!sg || b8_over_sg)) e = launch_gemv(*w, a, s);
+        else if (b8 && mc >= 5 && (!(sg && mc >= sg_min) || (mc == 8 && b8_over_sg))) e = launch_gemv(*w, a, s);
         if (e == hipErrorInvalidValue && !w->mfma_tiles && sg && mc >= sg_min) e = launch_sgemv(*w, a, s, scr);
         if (e == hipErrorOutOfMemory && scr.is_fixed())
             return set_error(TBH_E_INVALID, "this call needs " + std::to_string(scr.shortfall) +

@@ -60,6 +60,8 @@ struct KParams {
     int32_t rpn;     // rows per N-block (INT4 runtime layout)
     int32_t nb_half; // INT4 runtime layout, gate|up rows interleaved: N-blocks of the first part
     int32_t x_vec4;  // x rows are 16-byte aligned and K % 4 == 0
+    int32_t m_act;   // x rows present (the burst kernel's M may round it up: rows
+                     // from m_act on re-read row m_act - 1 and are not stored)
     // fused decode prologue / epilogue (gemv_burst with M = 1 only)
     const float *g;    // PRO_RMSNORM: norm weight [K]
     float eps;         // PRO_RMSNORM: epsilon
@@ -455,7 +457,7 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
     float4 xv[M][XR];
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-        const float *xr = p.x + (int64_t)m * p.ldx;
+        const float *xr = p.x + (int64_t)(M == 1 ? 0 : min(m, p.m_act - 1)) * p.ldx;
 #pragma unroll
         for (int r = 0; r < XR; ++r) {
             const int k = 4 * (tid + 256 * r);
@@ -750,7 +752,7 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
     } else if ((lane & (64 / V - 1)) == 0) {
         const int m = ridx / U, n = r0 + ridx % U;
         const float v = PREC == 8 ? tot * rs : tot;
-        if (n < p.N) p.y[(int64_t)m * p.ldy + n] = EPI == EPI_ACCUMULATE ? yin + v : v;
+        if (n < p.N && (M == 1 || m < p.m_act)) p.y[(int64_t)m * p.ldy + n] = EPI == EPI_ACCUMULATE ? yin + v : v;
     }
 }
 
@@ -899,6 +901,7 @@ KParams make_params(const tbh_weight &w, const GemvArgs &a) {
     p.rpn = w.rows_per_nblock;
     p.nb_half = w.nb_half;
     p.x_vec4 = (w.K % 4 == 0 && a.ldx % 4 == 0 && ((uintptr_t)a.x & 15) == 0) ? 1 : 0;
+    p.m_act = (int32_t)a.M;
     p.g = a.x;
     p.eps = 0.0f;
     return p;
@@ -1010,7 +1013,7 @@ hipError_t launch_gemv_fused(const tbh_weight &w, const FusedGemvArgs &f, hipStr
 
 hipError_t launch_gemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s) {
     const int M = (int)a.M;
-    if (M == 8 && !w.ng_pairs) {   // the burst kernel only
+    if (M >= 5 && M <= 8 && !w.ng_pairs) {   // the eight-row burst kernel only (rows past M masked)
         KParams p = make_params(w, a);
         int I, U;
         int64_t blds;
@@ -1025,12 +1028,16 @@ hipError_t launch_gemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s) {
     KParams p = make_params(w, a);
     const int64_t cus = std::max(1, w.dev->cu_count);
     {
+        // three rows on the four-row burst kernel, the fourth masked
+        // (us per launch, VALU kernel at M = 3 / burst at M = 4: INT4
+        // 2048x2048 4.48 / 3.61-3.78, 5632x2048 6.16 / 5.59)
+        const int Mb = M == 3 ? 4 : M;
         int I, U;
         int64_t blds;
-        if (burst_shape(w, p, M, &I, &U, &blds)) {
-            if (w.path == Path::Int8Row) return burst_m<8>(M, I, U, p, (size_t)blds, s);
-            return w.path == Path::Int4NGroup ? burst_m<4, 1>(M, I, U, p, (size_t)blds, s)
-                                              : burst_m<4>(M, I, U, p, (size_t)blds, s);
+        if (burst_shape(w, p, Mb, &I, &U, &blds)) {
+            if (w.path == Path::Int8Row) return burst_m<8>(Mb, I, U, p, (size_t)blds, s);
+            return w.path == Path::Int4NGroup ? burst_m<4, 1>(Mb, I, U, p, (size_t)blds, s)
+                                              : burst_m<4>(Mb, I, U, p, (size_t)blds, s);
         }
     }
 
