@@ -1,0 +1,84 @@
+"""Seeded random parity cases over the whole routing of the matmul path.
+
+Each case draws a weight kind (every INT8 mode, zero points, INT4 in the
+converter layout with groups along K and in the runtime layout with groups
+along N, group sizes that do and do not tile the layouts), a shape (ragged K
+and N, K not a multiple of 8 included) and a row count (1..9, the masked-row
+counts, the GEMM thresholds and a few prefill sizes), then checks
+dequantize() bit-exactly against the oracle (QuantizedTensor.swift:182-286
+restated) and the fp32 product (tbh_matmul_device) and, where the weight
+takes it, the bf16 prefill product (tbh_matmul_bf16_device) within GATE of a
+float64 product over the same dequantized weights.  The cases are fixed by
+their seeds, so a failure names a reproducible case.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+import tinybrain_amd as T
+from tinybrain_amd import _abi
+from test_gpu_sweep import _oracle_weight, _weight
+
+pytestmark = pytest.mark.gpu
+
+GATE = 1e-3
+
+KINDS = ["int8", "int8_zp", "int8_sym", "int8_asym", "int4_nk_g32", "int4_nk_g64", "int4_nk_g128",
+         "int4_nk_g32_zp", "int4_kn_g16", "int4_kn_g32", "int4_kn_g64", "int4_kn_g48"]
+MS = [1, 2, 3, 4, 5, 6, 7, 8, 9, 11, 13, 16, 24, 33, 64, 65, 130]
+
+
+def _case(seed):
+    r = np.random.RandomState(seed)
+    kind = KINDS[r.randint(len(KINDS))]
+    gs = int(kind.split("_g")[1].split("_")[0]) if "_g" in kind else 0
+    if kind.startswith("int4_nk"):
+        K = gs * r.randint(1, 6000 // gs + 1) if r.rand() < 0.8 else 8 * r.randint(1, 700)
+        N = r.randint(1, 2500)
+    elif kind.startswith("int4_kn"):
+        K = 8 * r.randint(1, 700)
+        N = gs * r.randint(1, 2500 // gs + 1) if r.rand() < 0.8 else r.randint(1, 2500)
+    else:
+        K = 8 * r.randint(1, 700) if r.rand() < 0.85 else r.randint(8, 5600)
+        N = r.randint(1, 3000)
+    while K * N > 6_000_000:
+        N = max(1, N // 2)
+    M = MS[r.randint(len(MS))]
+    return kind, int(K), int(N), int(M)
+
+
+SEEDS = list(range(0xF0, 0xF0 + 160))
+
+
+@pytest.fixture(scope="module")
+def backend():
+    b = T.HIPBackend(0)
+    yield b
+    b.close()
+
+
+@pytest.mark.parametrize("seed", SEEDS)
+def test_random_case(backend, seed):
+    import torch
+
+    kind, K, N, M = _case(seed)
+    qt, pq = _weight(kind, K, N, seed=seed)
+    W = _oracle_weight(qt, pq.layout)
+    deq = backend.dequantize(pq)
+    np.testing.assert_array_equal(deq.view(np.uint32), W.view(np.uint32), err_msg=str((kind, K, N)))
+    x = O.fill_normal(seed * 31 + M, M * K).reshape(M, K)
+    y = backend.matmulQuantized(x, pq)
+    err = O.parity_errors(y, O.gemm_f64(x, W))
+    assert err["gated"] <= GATE, (kind, K, N, M, err)
+
+    # bf16 prefill entry: weights and shapes it takes; the rest say so
+    w = backend.weight(pq)
+    xb = torch.from_numpy(x).to(torch.bfloat16)
+    try:
+        yb = backend.matmul_bf16_device(xb.cuda(), w)
+    except T.HIPBackendError as e:
+        assert e.status == _abi.E_UNSUPPORTED, (kind, K, N, M, str(e))
+        return
+    torch.cuda.synchronize()
+    errb = O.parity_errors(yb.cpu().numpy(), O.gemm_f64(xb.float().numpy(), W))
+    assert errb["gated"] <= GATE, (kind, K, N, M, "bf16", errb)

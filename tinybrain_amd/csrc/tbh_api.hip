@@ -954,8 +954,8 @@ tbh_status tbh_matmul_bf16_device(const tbh_weight *w, const uint16_t *x, int64_
     if (!x || !y) return set_error(TBH_E_INVALID, "tbh_matmul_bf16_device: x or y is NULL");
     if (!prefill_supported(*w))
         return set_error(TBH_E_UNSUPPORTED,
-                         "tbh_matmul_bf16_device: needs an INT8 row or INT4 K-group weight in the "
-                         "row layout");
+                         "tbh_matmul_bf16_device: needs an INT8 row, INT4 K-group or runtime-layout INT4 "
+                         "weight (N-blocks of 16, 32 or a multiple of 64 rows) in the row layout");
     if (K % 8 != 0 || ((uintptr_t)x & 15) != 0)
         return set_error(TBH_E_UNSUPPORTED,
                          "tbh_matmul_bf16_device: needs K % 8 == 0 and a 16-byte aligned x");
