@@ -822,14 +822,14 @@ static tbh_status matmul_enqueue(const tbh_weight *w, const float *x, int64_t M,
     const int forced = w->dev->sgemv_min_rows.load(std::memory_order_relaxed);
     const int64_t sg_min = forced > 0 ? std::max(2, forced) : sgemv_min_rows(*w);
     const bool sg = M >= sg_min && sgemv_supported(*w);
-    // eight rows at a time on the burst GEMV when the weight and x allow it
+    // Eight rows at a time on the burst GEMV when the weight and x allow it
     // and the matrix-core GEMV does not take them (INT4 2048x2048 at M = 8:
     // 6.9 us as two 4-row launches, 4.8 us as one), or takes them on a weight
     // of at most 12 Mi elements (INT4 5632x2048: 9.0 us there, 8.6-8.9 us as
-    // one burst launch; 8192x2048: 9.2-9.4 against 10.5-11.0)
-    // (five to seven rows: the same launch with the rows past M masked;
-    // INT4 2048x2048 at M = 5 / 7: 6.3 / 8.2 us as 4 + 1 / 4 + 3 rows, 5.0 /
-    // 5.0 us as one launch)
+    // one burst launch; 8192x2048: 9.2-9.4 against 10.5-11.0).  Five to seven
+    // rows take the same launch with the rows past M masked (INT4 2048x2048
+    // at M = 5 / 7: 6.3 / 8.2 us as 4 + 1 / 4 + 3 rows, 5.0 / 5.0 us as one
+    // launch).
     const bool b8 = burst8 && M >= 5;
     const bool b8_over_sg = w->N * w->K <= ((int64_t)12 << 20);
     const int64_t rows = w->mfma_tiles || sg || b8 ? 8 : gemv_max_rows(*w);
