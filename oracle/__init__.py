@@ -25,7 +25,9 @@ from typing import Optional
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "_build", "libtbh_oracle.so")
+# ORACLE_LIB: another build of the same source (the sanitizer build of
+# `make -C oracle asan`)
+_LIB_PATH = os.environ.get("ORACLE_LIB") or os.path.join(_HERE, "_build", "libtbh_oracle.so")
 
 # QuantizationMode (QuantizedTensor.swift:31-37) and precision codes
 MODE_SYMMETRIC, MODE_ASYMMETRIC, MODE_PER_CHANNEL, MODE_INT4, MODE_INT4_PER_CHANNEL = range(5)
