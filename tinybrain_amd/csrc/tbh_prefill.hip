@@ -535,9 +535,10 @@ hipError_t launch_tile(const PParams &p, int splits, hipStream_t s) {
         return v && *v ? std::atoi(v) : 0;
     }();
     const dim3 grid((unsigned)((p.Np + BN - 1) / BN), (unsigned)((p.M + BM - 1) / BM), (unsigned)splits);
-    if constexpr (NC > 0) {   // runtime-layout INT4: split x (fp32, or bf16 widened), four waves
-        if (p.xf) hipLaunchKernelGGL((gemm_bf16<4, BM, BN, false, 4, BK, 1, NC>), grid, dim3(256), 0, s, p);
-        else hipLaunchKernelGGL((gemm_bf16<4, BM, BN, false, 4, BK, 2, NC>), grid, dim3(256), 0, s, p);
+    if constexpr (NC > 0) {   // runtime-layout INT4: split x (fp32, or bf16 widened)
+        constexpr int WVN = BM == 128 ? 8 : 4;
+        if (p.xf) hipLaunchKernelGGL((gemm_bf16<4, BM, BN, false, WVN, BK, 1, NC>), grid, dim3(64 * WVN), 0, s, p);
+        else hipLaunchKernelGGL((gemm_bf16<4, BM, BN, false, WVN, BK, 2, NC>), grid, dim3(64 * WVN), 0, s, p);
     } else {
         const bool w8 = waves == 8 || (waves != 4 && BN == 128 && (p.M >= 256 || PREC == 4));
         if (p.xf) {   // fp32 x
@@ -680,13 +681,26 @@ int ng_copies(const tbh_weight &w) {
 }
 
 // Runtime-layout INT4 (one scale per (N-block, k)) with x given as p.x (bf16)
-// or p.xf (fp32), p.M = 4 * x rows: 64 x 64 tiles (16 x rows by 64
-// outputs), four waves, split along K to two blocks per CU when the tiles
-// are fewer.
+// or p.xf (fp32), p.M = 4 * x rows: 64 x 64 tiles (16 x rows by 64 outputs,
+// four waves) or 128 x 64 tiles (32 x rows, eight waves), split along K when
+// the tiles are fewer than the CUs.
 hipError_t launch_ngroup(const tbh_weight &w, PParams p, hipStream_t s, const Scratch &scr) {
     p.rpn = w.rows_per_nblock;
     p.nbk = (int32_t)((w.Np + w.rows_per_nblock - 1) / w.rows_per_nblock);
     const int64_t tiles = ((p.Np + 63) / 64) * ((p.M + 63) / 64);
+    // past 16 x rows (64 product rows): 128 x 64 tiles as 8-wave blocks,
+    // which re-read the weights half as often (2048x5632, N-blocks of 32, us
+    // per call 64 / 128 product rows: M = 64 28.1 / 24.6, M = 128 49.2 /
+    // 41.0, M = 512 160.1 / 133.9, M = 2048 598 / 508); with four copies of
+    // x the 128-row tile does not fit the LDS
+    if (p.M > 64) {
+        const int64_t t128 = ((p.Np + 63) / 64) * ((p.M + 127) / 128);
+        switch (ng_copies(w)) {
+        case 1: return launch_split<4, 128, 64, kBK, 1>(w, p, t128, 1, s, scr);
+        case 2: return launch_split<4, 128, 64, kBK, 2>(w, p, t128, 1, s, scr);
+        default: break;
+        }
+    }
     switch (ng_copies(w)) {
     case 1: return launch_split<4, 64, 64, kBK, 1>(w, p, tiles, 2, s, scr);
     case 2: return launch_split<4, 64, 64, kBK, 2>(w, p, tiles, 2, s, scr);
