@@ -664,6 +664,10 @@ hipError_t launch_prec(const tbh_weight &w, const PParams &p, hipStream_t s, con
     // does little work per K step, so one per CU leaves its latency exposed;
     // 8-wave 64 x 128 tiles measured the same at M = 64 and 4 % slower at
     // M = 128).
+    // fp32 x at 32..63 rows (128..252 product rows): 128 x 128 tiles split
+    // along K (2048x5632 at 32 rows 16.6 -> 14.8 us; bf16 x at M = 128 is
+    // slower that way, 18.1 -> 20.4 us)
+    if (PREC == 4 && p.xf && p.M >= 128) return launch_split<PREC, 128, 128>(w, p, t128, 1, s, scr);
     if (PREC == 4) return launch_split<PREC, 64, 128>(w, p, t64x128, 1, s, scr);
     if (t128 >= cus) return launch_split<PREC, 128, 128>(w, p, t128, 1, s, scr);
     if (t64x128 >= cus) return launch_split<PREC, 64, 128>(w, p, t64x128, 1, s, scr);
