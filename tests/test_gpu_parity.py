@@ -205,6 +205,66 @@ def test_burst_eight_rows(backend, kind, K, N):
         backend.set_option(_abi.OPT_SGEMV_MIN_ROWS, 0)
 
 
+def _extreme_rows(seed, K):
+    """Eight x rows of unusual ranges: huge, tiny, a third zero, all zero,
+    one huge 32-element chunk, one tiny chunk, all positive (as after a
+    ReLU or SiLU) and all positive with a large common offset."""
+    x = O.fill_normal(seed, 8 * K).reshape(8, K)
+    x[0] *= 1e6
+    x[1] *= 1e-7
+    x[2, ::3] = 0.0
+    x[3, :] = 0.0
+    x[4, :32] *= 1e20
+    x[5, 32:64] *= 1e-20
+    x[6] = np.abs(x[6])
+    x[7] = 100.0 + np.abs(x[7])
+    return x
+
+
+@pytest.mark.parametrize("kind,K,N", [
+    ("int8", 2048, 1000),
+    ("int8_zp", 1000, 300),
+    ("int4", 2048, 1000),
+    ("int4", 5632, 300),     # three chunk iterations per row
+    ("int4kn", 2048, 1024),  # runtime layout: x times the N-block's scale row in LDS
+])
+def test_burst_x_range_extremes(backend, kind, K, N):
+    # the burst GEMV keeps x in fp32 and the weights exact in f16, so huge,
+    # tiny and all-positive activations (no cancellation to hide rounding)
+    # stay within the gate, one row at a time and on the 2-, 4- and 8-row
+    # launches; an all-zero row gives exactly zero
+    if kind.startswith("int8"):
+        oq = _int8_pc(0xE1 + K, K, N)
+        if kind == "int8_zp":
+            oq.zero_points = ((np.arange(N) % 9) - 4).astype(np.int8)
+        pq = _product(oq, (K, N))
+    elif kind == "int4":
+        oq = _int4_nk(0xE2 + K, K, N, 32)
+        pq = _product(oq, (K, N), T.Layout.NK_FLAT)
+    else:
+        oq = _int4_kn(0xE3 + K, K, N, 32)
+        pq = _product(oq, (K, N))
+    W = _oracle_weight(oq, pq.layout)
+    x = _extreme_rows(0xE4 + K + N, K)
+    y64 = O.gemm_f64(x, W)
+    backend.set_option(_abi.OPT_SGEMV_MIN_ROWS, 9)
+    try:
+        outs = [backend.matmulQuantized(x[m:m + 1], pq) for m in range(8)]
+        outs.append(backend.matmulQuantized(x[:2], pq))
+        outs.append(backend.matmulQuantized(x[4:], pq))
+        outs.append(backend.matmulQuantized(x, pq))
+    finally:
+        backend.set_option(_abi.OPT_SGEMV_MIN_ROWS, 0)
+    rows = [[m] for m in range(8)] + [[0, 1], [4, 5, 6, 7], list(range(8))]
+    for y, ms in zip(outs, rows):
+        for i, m in enumerate(ms):
+            if m == 3:
+                assert np.all(y[i] == 0.0), (kind, len(ms))
+            else:
+                err = O.parity_errors(y[i:i + 1], y64[m:m + 1])
+                assert err["gated"] <= GATE, (kind, m, len(ms), err)
+
+
 @pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 11008), (11008, 4096), (4096, 32000)])
 def test_int4_7b_projection_shapes(backend, K, N):
     # BASELINE config 4: the 7B projection set (q/k/v/o, gate/up, down, LM
@@ -854,6 +914,43 @@ def test_prefill_bf16_runtime_layout(backend, K, N, gs, M):
     pq = _product(qk, (K, N))
     assert backend.weight(pq).path == "int4_ngroup"
     _prefill_check(backend, pq, qk, M, seed=37 + M)
+
+
+@pytest.mark.parametrize("kind,K,N,M", [
+    ("int8", 2048, 1024, 64),      # split along K
+    ("int8", 2048, 5632, 512),     # one block per tile, no split
+    ("int4", 5632, 2048, 64),
+    ("int4", 2048, 5632, 2048),    # 128 x 128 tiles, K steps of 128
+    ("int4kn", 2048, 1024, 128),   # runtime layout: three pieces of fl(x * s)
+])
+def test_prefill_bf16_x_range_extremes(backend, kind, K, N, M):
+    # the eight extreme rows (huge, tiny, zeros, one huge or tiny chunk, all
+    # positive) repeated over M rows, each copy rescaled by a power of two
+    import torch
+
+    if kind == "int8":
+        oq = _int8_pc(0xE5 + K, K, N)
+        pq = _product(oq, (K, N))
+    elif kind == "int4":
+        oq = _int4_nk(0xE6 + K, K, N, 32)
+        pq = _product(oq, (K, N), T.Layout.NK_FLAT)
+    else:
+        oq = _int4_kn(0xE7 + K, K, N, 32)
+        pq = _product(oq, (K, N))
+    W = _oracle_weight(oq, pq.layout)
+    base = _extreme_rows(0xE8 + K + M, K)
+    x = np.concatenate([base * np.float32(2.0 ** ((r % 9) - 4)) for r in range(M // 8)])
+    xb = torch.from_numpy(x).to(torch.bfloat16)
+    y = backend.matmul_bf16_device(xb.cuda(), backend.weight(pq))
+    torch.cuda.synchronize()
+    y = y.cpu().numpy()
+    y64 = O.gemm_f64(xb.float().numpy(), W)
+    for m in range(M):
+        if m % 8 == 3:
+            assert np.all(y[m] == 0.0), (kind, m)
+        else:
+            err = O.parity_errors(y[m:m + 1], y64[m:m + 1])
+            assert err["gated"] <= GATE, (kind, m, err)
 
 
 def test_prefill_bf16_unsupported(backend):
