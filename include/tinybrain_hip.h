@@ -157,7 +157,8 @@ tbh_status tbh_device_set_option(tbh_device *dev, int32_t option, int64_t value)
 /* Replaces the weight upload of MetalBackend.cachedQuantizedBuffers
  * (MetalBackend.swift:1282-1308) and cachedINT4Buffers (:1322-1359): copies
  * the descriptor's arrays and repacks them ONCE into the gfx950 layout; the
- * caller may free its arrays on return.  Thread-safe. */
+ * caller may free its arrays on return.  Thread-safe.  K or N above 2^30
+ * returns TBH_E_UNSUPPORTED (the caller's CPU fallback takes it). */
 tbh_status tbh_weight_create(tbh_device *dev, const tbh_qtensor_desc *desc,
                              tbh_weight **out);
 tbh_status tbh_weight_destroy(tbh_weight *w);

@@ -358,6 +358,48 @@ def test_int4_per_channel_is_unsupported(backend):
     assert e.value.status == _abi.E_UNSUPPORTED
 
 
+def test_dimension_above_limit_is_unsupported(backend):
+    # K or N above 2^30 is refused before any array is read (the kernels hold
+    # row and column indices in 32-bit integers); the caller's CPU path takes it
+    one = np.zeros(16, np.uint8)
+    s = np.ones(1, np.float32)
+    for K, N in (((1 << 30) + 1, 1), (1, (1 << 30) + 1)):
+        d = _abi.QTensorDesc(K=K, N=N, precision=_abi.PREC_INT8, mode=_abi.MODE_SYMMETRIC,
+                             layout=_abi.LAYOUT_KN_FLAT, group_size=0, data=one.ctypes.data,
+                             data_bytes=K * N, scales=s.ctypes.data, n_scales=1)
+        h = ctypes.c_void_p()
+        st = _abi.lib().tbh_weight_create(backend._dev, ctypes.byref(d), ctypes.byref(h))
+        assert st == _abi.E_UNSUPPORTED and not h.value, (K, N)
+
+
+@pytest.mark.parametrize("kind", ["int8", "int4", "int4kn"])
+def test_rows_beyond_one_gemm_launch(backend, kind):
+    # 2^18 + 37 rows: the GEMM takes x in chunks of 2^18 rows, one launch
+    # after the other, through the fp32 entry and the bf16 entry
+    import torch
+
+    K, N, M = 64, 32, (1 << 18) + 37
+    if kind == "int8":
+        oq = _int8_pc(0xB1, K, N)
+        pq = _product(oq, (K, N))
+    elif kind == "int4":
+        oq = _int4_nk(0xB2, K, N, 32)
+        pq = _product(oq, (K, N), T.Layout.NK_FLAT)
+    else:
+        oq = _int4_kn(0xB3, K, N, 16)      # N-blocks of 16 rows
+        pq = _product(oq, (K, N))
+    W = _oracle_weight(oq, pq.layout)
+    x = O.fill_normal(0xB4, M * K).reshape(M, K)
+    y = backend.matmulQuantized(x, pq)
+    err = O.parity_errors(y, O.gemm_f64(x, W))
+    assert err["gated"] <= GATE, (kind, err)
+    xb = torch.from_numpy(x).to(torch.bfloat16)
+    yb = backend.matmul_bf16_device(xb.cuda(), backend.weight(pq))
+    torch.cuda.synchronize()
+    errb = O.parity_errors(yb.cpu().numpy(), O.gemm_f64(xb.float().numpy(), W))
+    assert errb["gated"] <= GATE, (kind, "bf16", errb)
+
+
 def test_empty_input(backend):
     qt = _int8_pc(8, 32, 8)
     y = backend.matmulQuantized(np.zeros((0, 32), np.float32), _product(qt, (32, 8)))

@@ -189,6 +189,9 @@ static tbh_status validate_desc(const tbh_qtensor_desc *d) {
     if (d->layout != TBH_LAYOUT_KN_FLAT && d->layout != TBH_LAYOUT_NK_FLAT)
         return set_error(TBH_E_INVALID, "unknown layout");
     if (d->group_size < 0) return set_error(TBH_E_INVALID, "group_size < 0");
+    if (d->K > kMaxDim || d->N > kMaxDim)
+        return set_error(TBH_E_UNSUPPORTED, "K and N must each be at most 2^30 (the kernels index rows and "
+                                            "columns of a weight with 32-bit integers)");
     const int64_t count = d->K * d->N;
     if (d->precision == TBH_PREC_INT8) {
         if (d->data_bytes != count)

@@ -27,6 +27,10 @@ __host__ __device__ __forceinline__ int64_t kgroup_index(int64_t n, int64_t g, i
     return ((n >> 2) * G + g) * 4 + (n & 3);
 }
 
+// Largest K or N of a weight: the kernels hold row and column indices (and
+// their padded forms) in 32-bit integers.
+constexpr int64_t kMaxDim = (int64_t)1 << 30;
+
 // Largest x tile (M * Kp fp32) the VALU GEMV keeps in LDS.
 constexpr int64_t kMaxLdsBytes = 64 * 1024;
 

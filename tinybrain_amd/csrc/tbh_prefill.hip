@@ -740,51 +740,50 @@ static PParams prefill_params(const tbh_weight &w, int64_t ldx, float *y, int64_
     return p;
 }
 
-hipError_t launch_prefill_f32(const tbh_weight &w, const float *x, int64_t ldx, int64_t M, float *y,
-                              int64_t ldy, hipStream_t s, const Scratch &scr) {
-    if (!prefill_supported(w) || M < 1 || 4 * M > INT32_MAX || w.K % 8 != 0 || ldx % 4 != 0 ||
-        ((uintptr_t)x & 15) != 0)
-        return hipErrorInvalidValue;
-    PParams p = prefill_params(w, ldx, y, ldy);
-    p.xf = x;
-    p.M = (int32_t)(4 * M);
-    p.Mout = (int32_t)M;
+// Rows of x per GEMM launch.  The grid's second dimension counts row tiles,
+// and the fp32 and runtime-layout forms run four product rows per x row in
+// 32-bit row indices; longer x is taken in chunks of this many rows, one
+// launch (and split sum) after the other on the caller's stream.
+constexpr int64_t kGemmRowsPerLaunch = (int64_t)1 << 18;
+
+static hipError_t launch_rows(const tbh_weight &w, PParams &p, hipStream_t s, const Scratch &scr) {
     if (w.path == Path::Int4NGroup) return launch_ngroup(w, p, s, scr);
     return w.precision == TBH_PREC_INT8 ? launch_prec<8>(w, p, s, scr) : launch_prec<4>(w, p, s, scr);
 }
 
+hipError_t launch_prefill_f32(const tbh_weight &w, const float *x, int64_t ldx, int64_t M, float *y,
+                              int64_t ldy, hipStream_t s, const Scratch &scr) {
+    if (!prefill_supported(w) || M < 1 || w.K % 8 != 0 || ldx % 4 != 0 || ((uintptr_t)x & 15) != 0)
+        return hipErrorInvalidValue;
+    for (int64_t m0 = 0; m0 < M; m0 += kGemmRowsPerLaunch) {
+        const int64_t mc = std::min(kGemmRowsPerLaunch, M - m0);
+        PParams p = prefill_params(w, ldx, y + m0 * ldy, ldy);
+        p.xf = x + m0 * ldx;
+        p.M = (int32_t)(4 * mc);    // three bf16 pieces and a zero row per x row
+        p.Mout = (int32_t)mc;
+        const hipError_t e = launch_rows(w, p, s, scr);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
 hipError_t launch_prefill(const tbh_weight &w, const uint16_t *x, int64_t ldx, int64_t M, float *y,
                           int64_t ldy, hipStream_t s, const Scratch &scr) {
-    if (!prefill_supported(w) || M < 1 || w.K % 8 != 0 || ldx % 8 != 0 ||
-        ((uintptr_t)x & 15) != 0)
+    if (!prefill_supported(w) || M < 1 || w.K % 8 != 0 || ldx % 8 != 0 || ((uintptr_t)x & 15) != 0)
         return hipErrorInvalidValue;
-    if (w.path == Path::Int4NGroup) {   // x rows split into three bf16 pieces after the scale
-        if (4 * M > INT32_MAX) return hipErrorInvalidValue;
-        PParams p = prefill_params(w, ldx, y, ldy);
-        p.x = x;
-        p.M = (int32_t)(4 * M);
-        p.Mout = (int32_t)M;
-        return launch_ngroup(w, p, s, scr);
+    // runtime-layout INT4: every x row becomes the three bf16 pieces of
+    // fl(x * s) and a zero row, as in the fp32 form
+    const int64_t pieces = w.path == Path::Int4NGroup ? 4 : 1;
+    for (int64_t m0 = 0; m0 < M; m0 += kGemmRowsPerLaunch) {
+        const int64_t mc = std::min(kGemmRowsPerLaunch, M - m0);
+        PParams p = prefill_params(w, ldx, y + m0 * ldy, ldy);
+        p.x = x + m0 * ldx;
+        p.M = (int32_t)(pieces * mc);
+        p.Mout = (int32_t)mc;
+        const hipError_t e = launch_rows(w, p, s, scr);
+        if (e != hipSuccess) return e;
     }
-    PParams p{};
-    p.x = x;
-    p.ldx = ldx;
-    p.y = y;
-    p.ldy = ldy;
-    p.data = w.data;
-    p.row_bytes = w.row_bytes;
-    p.scales = w.scales;
-    p.zp = w.zp;
-    p.M = (int32_t)M;
-    p.Mout = (int32_t)M;
-    p.K = (int32_t)w.K;
-    p.N = (int32_t)w.N;
-    p.Np = (int32_t)w.Np;
-    const bool int8 = w.precision == TBH_PREC_INT8;
-    p.chunks = (int32_t)(w.Kp / (int8 ? kInt8ChunkElems : kInt4ChunkElems));
-    p.G = (int32_t)w.groups_per_row;
-    p.cpg = w.chunks_per_group;
-    return int8 ? launch_prec<8>(w, p, s, scr) : launch_prec<4>(w, p, s, scr);
+    return hipSuccess;
 }
 
 }  // namespace tbh
