@@ -11,6 +11,8 @@ takes it, the bf16 prefill product (tbh_matmul_bf16_device) within GATE of a
 float64 product over the same dequantized weights.  The cases are fixed by
 their seeds, so a failure names a reproducible case.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -47,7 +49,10 @@ def _case(seed):
     return kind, int(K), int(N), int(M)
 
 
-SEEDS = list(range(0xF0, 0xF0 + 160))
+# TBH_FUZZ_SEEDS=first:count runs another range of seeds (a longer sweep)
+_range = os.environ.get("TBH_FUZZ_SEEDS")
+SEEDS = (list(range(int(_range.split(":")[0]), int(_range.split(":")[0]) + int(_range.split(":")[1])))
+         if _range else list(range(0xF0, 0xF0 + 160)))
 
 
 @pytest.fixture(scope="module")
