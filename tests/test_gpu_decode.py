@@ -191,6 +191,29 @@ def test_decode_long_context(backend, heads):
     dec.close()
 
 
+@pytest.mark.parametrize("hd,nh,nkv,prec", [
+    (48, 4, 2, "int8"), (48, 4, 2, "int4"),
+    (80, 2, 1, "int8"), (80, 2, 1, "int4"),
+    (96, 8, 2, "int8"), (96, 8, 2, "int4"),
+    (112, 4, 4, "int8"), (112, 4, 4, "int4"),
+])
+def test_decode_head_dims_off_powers_of_two(backend, hd, nh, nkv, prec):
+    # head_dim / 4 not a power of two: attention scores one position per
+    # lane with whole key rows, and the value pieces and the merge use
+    # 64 / (head_dim / 4) lane groups with the lanes past them idle; 70
+    # steps cross a 64-position range
+    H = hd * nh
+    cfg = T.DecoderConfig(num_layers=2, hidden=H, num_heads=nh, num_kv_heads=nkv, intermediate=2 * H,
+                          vocab=500, max_seq=72)
+    dec, ref = _model(backend, cfg, prec, seed=83 + hd + nh)
+    rng = np.random.default_rng(hd * 5 + nkv)
+    for i, tok in enumerate(rng.integers(0, cfg.vocab, size=70)):
+        y = dec.step(int(tok))
+        r = ref.step(int(tok))
+        assert _gated(y, r) <= GATE, (i, _gated(y, r))
+    dec.close()
+
+
 def test_decode_merge_beyond_one_load_round(backend):
     # head_dim 128: the merge kernel loads 16 ranges (1024 positions) per
     # head in its first round and loops over the rest; 1100 steps reach 18
