@@ -359,3 +359,45 @@ def test_decode_from_converter_tbf_file(backend, fname):
             y, r = dec.step(tok), ref.step(tok)
             assert _gated(y, r) <= GATE, (fname, i, _gated(y, r))
         dec.close()
+
+
+def _decode_case(seed):
+    """A random decoder the library takes: head_dim a multiple of 16 up to
+    128, 1..8 query heads per KV head, INT8, converter INT4 or runtime INT4
+    (whose output widths are then multiples of 32)."""
+    r = np.random.RandomState(seed)
+    prec = ["int8", "int4", "int4kn"][r.randint(3)]
+    while True:
+        hd = 16 * r.randint(1, 9)
+        rep = [1, 2, 4, 8][r.randint(4)]
+        nkv = [1, 2, 4][r.randint(3)]
+        H = hd * rep * nkv
+        if rep * hd > 1024 or H > 2048:
+            continue
+        if prec != "int8" and H % 32:
+            continue
+        if prec == "int4kn" and (nkv * hd) % 32:
+            continue
+        break
+    mult = 4 if prec == "int8" else 32
+    inter = mult * r.randint(max(1, H // mult), 2 * H // mult + 2)
+    vocab = 32 * r.randint(4, 64) if prec == "int4kn" else r.randint(100, 2000)
+    steps = int(r.randint(3, 140))
+    layers = int(r.randint(1, 3))
+    return prec, dict(num_layers=layers, hidden=H, num_heads=rep * nkv, num_kv_heads=nkv, intermediate=int(inter),
+                      vocab=int(vocab), max_seq=steps + int(r.randint(0, 9))), steps
+
+
+@pytest.mark.parametrize("seed", list(range(0xDE0, 0xDE0 + 24)))
+def test_decode_random_configs(backend, seed):
+    # seeded random model shapes through the whole step; logits at every step
+    # within the gate of the float64 restatement
+    prec, kw, steps = _decode_case(seed)
+    cfg = T.DecoderConfig(**kw)
+    dec, ref = _model(backend, cfg, prec, seed=seed)
+    rng = np.random.default_rng(seed)
+    for i, tok in enumerate(rng.integers(0, cfg.vocab, size=steps)):
+        y = dec.step(int(tok))
+        r = ref.step(int(tok))
+        assert _gated(y, r) <= GATE, (prec, kw, i, _gated(y, r))
+    dec.close()
