@@ -176,6 +176,41 @@ def make_weight(prec: str, gs: int, N: int, K: int, seed: int):
     return T.quantize(np.ascontiguousarray(w_nk.T), T.QuantizationMode.perChannel)
 
 
+def host_entry(backend, pool, shapes, M: int, prec: str, gs: int, reps: int = 200) -> dict:
+    """tbh_matmul as the Swift drop-in calls it: x and y in pageable host
+    memory, the copy of x in, the copy of y out and the synchronisation
+    inside every call (MetalBackend.matmulQuantized's commit-and-wait,
+    MetalBackend.swift:894-974).  Weights rotate through the same >= 2 GiB
+    pool, so every call streams its weight from HBM.  Median over `reps`
+    calls per shape, after 10 untimed ones."""
+    from tinybrain_amd import _abi
+
+    lib = _abi.lib()
+    rng = np.random.default_rng(3)
+    per, total_us, total_b = {}, 0.0, 0
+    for j, (N, K) in enumerate(shapes):
+        x = rng.standard_normal((M, K), dtype=np.float32)
+        y = np.empty((M, N), np.float32)
+        ts = []
+        for i in range(reps + 10):
+            w = pool[i % len(pool)][j]
+            t0 = time.perf_counter()
+            st = lib.tbh_matmul(backend._dev, x.ctypes.data, M, K, w.handle, y.ctypes.data)
+            t1 = time.perf_counter()
+            if st != 0:
+                raise RuntimeError(f"tbh_matmul: status {st}")
+            if i >= 10:
+                ts.append(t1 - t0)
+        us = float(np.median(ts)) * 1e6
+        b = alg_bytes(prec, gs, N, K, M)
+        per[f"{N}x{K}"] = {"us": round(us, 2), "GB_s": round(b / us / 1e3, 1)}
+        total_us += us
+        total_b += b
+    return {"entry": "tbh_matmul: host x and y (pageable), copies and synchronisation included",
+            "per_shape": per, "us_per_step": round(total_us, 2), "GB_s": round(total_b / total_us / 1e3, 1),
+            "calls_per_shape": reps}
+
+
 def cpu_baseline(qts, shapes, M: int, budget_s: float = 15.0):
     """Reference CPU path (QuantizedTensor.swift:640-642) restated in the
     oracle: single-threaded dequantize() into a fresh fp32 [K, N] buffer, then
@@ -828,6 +863,8 @@ def main():
                     help="decode workloads: the decoder's cache length (default: the context plus the "
                          "steps replayed)")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--no-host-entry", action="store_true",
+                    help="GEMV workloads: leave out the host-pointer (tbh_matmul) timing")
     ap.add_argument("--no-decode", action="store_true",
                     help="int4_g32_gemv_m1: leave out the 1.1B decode-step measurement")
     ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
@@ -1023,6 +1060,8 @@ def main():
         "per_shape": per_shape,
         "setup_s": round(setup_s, 1),
     }
+    if not args.no_host_entry:
+        out["host_entry"] = host_entry(backend, pool, shapes, M, prec, gs)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(bases, shapes, M, args.cpu_budget)
     del pool

@@ -31,6 +31,10 @@ __host__ __device__ __forceinline__ int64_t kgroup_index(int64_t n, int64_t g, i
 // their padded forms) in 32-bit integers.
 constexpr int64_t kMaxDim = (int64_t)1 << 30;
 
+// Largest x plus y (bytes) that tbh_matmul passes through its page-locked
+// host staging; larger calls copy straight from the caller's arrays.
+constexpr size_t kPinnedStageBytes = (size_t)64 << 20;
+
 // Largest x tile (M * Kp fp32) the VALU GEMV keeps in LDS.
 constexpr int64_t kMaxLdsBytes = 64 * 1024;
 
@@ -59,6 +63,8 @@ struct tbh_device {
     std::atomic<int> mfma_min_rows{0};    // TBH_OPT_MFMA_MIN_ROWS; 0 = per-weight rule
     void *stage = nullptr;       // device staging for the host-pointer calls
     size_t stage_bytes = 0;
+    void *pin = nullptr;         // page-locked host staging for the host-pointer calls
+    size_t pin_bytes = 0;
     void *noalloc_scratch = nullptr;   // this GPU's scratch array (tbh_matmul_device_noalloc)
     std::atomic<int64_t> noalloc_limit{0};   // TBH_OPT_NOALLOC_SCRATCH_BYTES; 0 = the whole array
 
