@@ -2,6 +2,8 @@
 (oracle/decode_ref.py, ModelRunner.step restated in float64) on the same
 dequantized weights.  Gate: max|logit - ref| / max(|ref|, 1e-3 * max|ref|)
 <= 1e-3 at every step."""
+import os
+
 import numpy as np
 import pytest
 
@@ -388,7 +390,13 @@ def _decode_case(seed):
                       vocab=int(vocab), max_seq=steps + int(r.randint(0, 9))), steps
 
 
-@pytest.mark.parametrize("seed", list(range(0xDE0, 0xDE0 + 24)))
+# TBH_DECODE_FUZZ_SEEDS=first:count runs another range of seeds
+_range = os.environ.get("TBH_DECODE_FUZZ_SEEDS")
+DECODE_SEEDS = (list(range(int(_range.split(":")[0]), int(_range.split(":")[0]) + int(_range.split(":")[1])))
+                if _range else list(range(0xDE0, 0xDE0 + 24)))
+
+
+@pytest.mark.parametrize("seed", DECODE_SEEDS)
 def test_decode_random_configs(backend, seed):
     # seeded random model shapes through the whole step; logits at every step
     # within the gate of the float64 restatement
