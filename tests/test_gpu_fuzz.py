@@ -76,8 +76,21 @@ def test_random_case(backend, seed):
     err = O.parity_errors(y, O.gemm_f64(x, W))
     assert err["gated"] <= GATE, (kind, K, N, M, err)
 
-    # bf16 prefill entry: weights and shapes it takes; the rest say so
+    # device entry: the same bits as the host entry; the allocation-free
+    # entry: the same bits again, or refused when its scratch is too small
     w = backend.weight(pq)
+    xd = torch.from_numpy(x).cuda()
+    yd = backend.matmul_device(xd, w)
+    out = torch.empty_like(yd)
+    try:
+        backend.matmul_device_noalloc(xd, w, out=out)
+        torch.cuda.synchronize()
+        assert torch.equal(out, yd), (kind, K, N, M, "noalloc")
+    except T.HIPBackendError as e:
+        assert e.status == _abi.E_INVALID and "scratch" in str(e), (kind, K, N, M, str(e))
+    np.testing.assert_array_equal(yd.cpu().numpy(), y, err_msg=str((kind, K, N, M, "device entry")))
+
+    # bf16 prefill entry: weights and shapes it takes; the rest say so
     xb = torch.from_numpy(x).to(torch.bfloat16)
     try:
         yb = backend.matmul_bf16_device(xb.cuda(), w)
