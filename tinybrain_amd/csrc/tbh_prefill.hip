@@ -120,8 +120,15 @@ __device__ __forceinline__ float sbyte(uint32_t w) {
 // two blocks share a CU.  INT4 blocks with K steps of 128 (256 VGPRs) run
 // every K step in its masked form: with a second, unmasked loop form their
 // spilled registers went from 2 to 14-17.
+// Eight-wave blocks with K steps of 64 are held to four waves per SIMD
+// (two blocks per CU) where that fits: not the INT4 128 x 128 tiles (about
+// 180 VGPRs) nor runtime-layout tiles holding two or more x copies (their
+// LDS allows one block per CU).
+template <int PREC, int BM, int BN, int WV, int BK, int NC>
+constexpr bool kFourWavesPerSimd = WV == 8 && BK == 64 && NC <= 1 && !(PREC == 4 && BM == 128 && BN == 128);
+
 template <int PREC, int BM, int BN, bool ZP, int WV, int BK, int XF, int NC>
-__global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(WV == 8 && BK == 64 ? 4 : 1)))
+__global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(kFourWavesPerSimd<PREC, BM, BN, WV, BK, NC> ? 4 : 1)))
 void gemm_bf16(const PParams p) {
     static_assert(NC == 0 || (PREC == 4 && XF != 0 && !ZP), "runtime-layout INT4 stages split x, no zero points");
     static_assert(XF != 2 || NC > 0, "bf16 x is split only for runtime-layout scales");
