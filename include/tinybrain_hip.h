@@ -193,7 +193,11 @@ tbh_status tbh_matmul(tbh_device *dev, const float *x, int64_t M, int64_t K,
  * keeps, with every buffer it outgrew, until tbh_device_close (a graph
  * captured on the stream may still hold them): a caller that creates many
  * short-lived streams should reuse a few, or call
- * tbh_matmul_device_noalloc. */
+ * tbh_matmul_device_noalloc.  A graph captured on a stream holds that
+ * stream's current workspace, which later eager calls on the same stream
+ * reuse: such a graph must not be replayed (on any stream) while eager
+ * calls on its capture stream are in flight, or both write the same partial
+ * sums. */
 tbh_status tbh_matmul_device(const tbh_weight *w, const float *x, int64_t M,
                              int64_t K, float *y, void *stream);
 
@@ -202,9 +206,13 @@ tbh_status tbh_matmul_device(const tbh_weight *w, const float *x, int64_t M,
  * harnesses that forbid hipMalloc.  Same product, same kernels, same
  * arguments; the split-K partial sums (matrix-core small-M GEMV, MFMA GEMM)
  * go to a fixed 16 MiB scratch array per GPU (held until the process ends)
- * instead of a per-stream workspace, and the call makes no allocation.  A call whose
- * launch would need more than 16 MiB of scratch returns TBH_E_INVALID before
- * enqueueing anything (decode shapes need at most a few MiB).  Every call on
+ * instead of a per-stream workspace, and the call makes no allocation.  A
+ * call one of whose launches would need more than the scratch holds (16 MiB,
+ * or TBH_OPT_NOALLOC_SCRATCH_BYTES) returns TBH_E_INVALID before that launch
+ * is enqueued; rows of x that an earlier launch of the same call took on a
+ * route without scratch (x runs in pieces of up to 8 rows, and pieces can
+ * take different routes) may already have been written, so y is then
+ * unspecified (decode shapes need at most a few MiB).  Every call on
  * one GPU shares that GPU's array: calls that overlap on one GPU (different
  * streams, or graphs replayed concurrently) race and must be serialised by
  * the caller. */

@@ -73,7 +73,9 @@ class RefDecoder:
             out[o + i + 1] = x0 * s + x1 * c
         return out
 
-    def step(self, token: int) -> np.ndarray:
+    def step(self, token: int, logits: bool = True):
+        """One ModelRunner.step; with logits=False the LM head is skipped
+        (the caches and position advance the same) and None is returned."""
         self.ctx_trace = []                    # attention context of each layer
         h = self.emb[token].copy()
         for li, lw in enumerate(self.layers):
@@ -103,6 +105,5 @@ class RefDecoder:
             g = x @ wg
             u = x @ wu
             h = h + ((g / (1.0 + np.exp(-g))) * u) @ wd
-        logits = self._rms(h, self.final_norm) @ self.lm
         self.pos += 1
-        return logits
+        return self._rms(h, self.final_norm) @ self.lm if logits else None

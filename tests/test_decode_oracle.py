@@ -90,3 +90,53 @@ def test_softmax_weights_and_reset():
     b = [d.step(t) for t in (1, 2, 3)]
     for x, y in zip(a, b):
         np.testing.assert_array_equal(x, y)
+
+
+def test_swiglu_ffn_closed_form():
+    # ModelRunner.swift:445-452: h <- h + (silu(x Wg) * (x Wu)) Wd with
+    # x = rmsNorm(h, post_norm).  Attention projections are zero, so h after
+    # attention is the embedding row.  Gate and up are diagonal maps chosen
+    # so that x Wg = g and x Wu = u for known vectors g, u; down sends entry
+    # j to output column perm[j] times c[j]; the LM head is the identity, so
+    # the logits are rmsNorm(h_out, final_norm).  The expectation goes
+    # through torch's rms_norm and silu, not through the oracle's helpers.
+    import torch
+    import torch.nn.functional as F
+
+    H, inter = 8, 4
+    d = _tiny(nh=2, nkv=1, hd=4, inter=inter, vocab=H, zero=True, seed=9)
+    rng = np.random.default_rng(19)
+    tok = 3
+    h = d.emb[tok].copy()
+    post = d.layers[0].post_norm
+    x = F.rms_norm(torch.tensor(h), (H,), weight=torch.tensor(post), eps=1e-5).numpy()
+    g = np.array([1.5, -2.0, 0.7, 3.0])
+    u = np.array([-0.5, 1.2, 2.0, -1.0])
+    perm = np.array([5, 0, 7, 2])
+    c = rng.normal(0, 1, inter)
+    wg = np.zeros((H, inter))
+    wu = np.zeros((H, inter))
+    wd = np.zeros((inter, H))
+    for j in range(inter):
+        wg[j, j] = g[j] / x[j]
+        wu[j, j] = u[j] / x[j]
+        wd[j, perm[j]] = c[j]
+    w = list(d.layers[0].weights)
+    w[4], w[5], w[6] = wg, wu, wd
+    d.layers[0].weights = w
+    d.lm = np.eye(H)
+    silu = F.silu(torch.tensor(g)).numpy()
+    h_out = h.copy()
+    h_out[perm] += silu * u * c
+    want = F.rms_norm(torch.tensor(h_out), (H,), weight=torch.tensor(d.final_norm), eps=1e-5).numpy()
+    logits = d.step(tok)
+    np.testing.assert_allclose(logits, want, rtol=1e-10, atol=1e-12)
+    # the plausible slips give a different answer: gate and up swapped
+    # (silu(u) * g), or the residual dropped
+    swapped = h.copy()
+    swapped[perm] += F.silu(torch.tensor(u)).numpy() * g * c
+    no_res = np.zeros(H)
+    no_res[perm] = silu * u * c
+    for bad in (swapped, no_res):
+        b = F.rms_norm(torch.tensor(bad), (H,), weight=torch.tensor(d.final_norm), eps=1e-5).numpy()
+        assert np.max(np.abs(b - logits)) > 1e-3

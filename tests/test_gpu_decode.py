@@ -149,6 +149,28 @@ def test_decode_tinyllama_full_depth(backend):
     dec.close()
 
 
+def test_decode_tinyllama_context_520(backend):
+    # BASELINE configs[2]'s head layout at its own context: hidden 2048, 32
+    # query heads over 4 KV heads (8 per KV head), head_dim 64, FFN 5632,
+    # vocab 32000, INT8 per-channel, 2 layers, 520 steps.  Positions 511..519
+    # run eight and nine 64-position attention ranges through the merge, as
+    # the 1.1B bench step at context 512 does.  The caches and positions
+    # advance at every step on both sides; logits are gated at the range
+    # edges (the oracle skips its LM head elsewhere).
+    cfg = T.DecoderConfig(num_layers=2, hidden=2048, num_heads=32, num_kv_heads=4, intermediate=5632,
+                          vocab=32000, max_seq=528)
+    dec, ref = _model(backend, cfg, "int8", seed=29)
+    gates = (0, 63, 64, 127, 128, 511, 512, 519)
+    rng = np.random.default_rng(29)
+    for i, tok in enumerate(rng.integers(0, cfg.vocab, size=520)):
+        y = dec.step(int(tok))
+        r = ref.step(int(tok), logits=i in gates)
+        if i in gates:
+            assert _gated(y, r) <= GATE, (i, _gated(y, r))
+    assert dec.position == 520 and ref.pos == 520
+    dec.close()
+
+
 def test_decode_tinyllama_width_runtime_int4(backend):
     # TinyLlama-1.1B layer shapes, 2 layers, INT4 in the runtime layout that
     # Tensor.quantize(.int4) and the perplexity harness write (groups of 32

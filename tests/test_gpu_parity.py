@@ -181,7 +181,8 @@ def test_burst_shapes(backend, prec, K, N):
     ("int8", 2048, 1003),     # ragged N
     ("int8", 1000, 64),       # K off the chunk multiple
     ("int4", 2048, 2048),     # configs[1] shape the matrix-core GEMV never takes
-    ("int4", 4096, 520),      # two chunk iterations per row (the matrix-core GEMV switched off)
+    ("int4", 4096, 520),      # two chunk iterations per row: eight staged x rows would need 144 KB
+                              # of LDS, so 8 rows run as two 4-row launches (matrix-core GEMV off)
     ("int4kn", 2048, 5632),   # runtime layout (groups along N)
 ])
 def test_burst_eight_rows(backend, kind, K, N):

@@ -328,6 +328,86 @@ def test_int4_per_channel_uses_dim0_and_traps():
     np.testing.assert_array_equal(out, (vals * qt2.scales[:2, None]).astype(np.float32))
 
 
+# --------------------------------------------------------------------------
+# quantizeINT4PerChannel (QuantizedTensor.swift:563-606): one scale per
+# column (dim 1, out_features), q = clamp(round(w / s[col]), -7, 7) with
+# Swift's half-away-from-zero round, packed even flat index -> high nibble.
+# --------------------------------------------------------------------------
+def _nibbles_by_shift(packed: np.ndarray, n: int) -> np.ndarray:
+    """Signed nibbles of a packed array by int8 arithmetic shifts (high
+    nibble = byte >> 4, low = (byte << 4) >> 4): a decode independent of
+    the oracle's raw > 7 ? raw - 16 : raw rule."""
+    b = packed.view(np.int8).astype(np.int8)
+    hi = (b >> np.int8(4)).astype(np.int64)
+    lo = (np.left_shift(b.view(np.uint8), np.uint8(4)).view(np.int8) >> np.int8(4)).astype(np.int64)
+    return np.stack([hi, lo], 1).reshape(-1)[:n]
+
+
+def test_int4_per_channel_known_bytes():
+    # Every column's abs-max is exactly 7, so every scale is exactly 1.0 and
+    # q = round(w): [[7, -3], [2.5, -7]] -> flat [7, -3, 3, -7] (2.5 -> 3,
+    # half away from zero) -> bytes 0x7D, 0x39 (even index in the high nibble)
+    w = np.array([[7.0, -3.0], [2.5, -7.0]], np.float32)
+    qt = O.quantize_int4_per_channel(w)
+    assert qt.scales.tolist() == [1.0, 1.0]
+    assert qt.zero_points is None and qt.mode == O.MODE_INT4_PER_CHANNEL
+    assert qt.data.view(np.uint8).tolist() == [0x7D, 0x39]
+
+
+def test_int4_per_channel_scale_is_column_absmax_over_7():
+    # 5 x 3 (rows != cols, so a per-row scale would differ in count and
+    # value): s[c] = max_r |w[r, c]| / 7 in fp32, one per column
+    w = np.array([[0.1, -2.0, 0.0],
+                  [0.3, 1.0, 0.0],
+                  [-0.7, 0.5, 0.0],
+                  [0.2, -1.5, 0.0],
+                  [0.0, 0.25, 0.0]], np.float32)
+    qt = O.quantize_int4_per_channel(w)
+    assert qt.scales.size == 3
+    assert qt.scales[0] == np.float32(0.7) / np.float32(7)
+    assert qt.scales[1] == np.float32(2.0) / np.float32(7)
+    assert qt.scales[2] == np.float32(1.0)          # all-zero column: scale 1.0
+    q = _nibbles_by_shift(qt.data, w.size).reshape(5, 3)
+    # the abs-max element of each non-zero column maps to +-7 with its sign
+    assert q[2, 0] == -7 and q[0, 1] == -7
+    assert not q[:, 2].any()                        # zero column stays zero
+    assert qt.data.size == (15 + 1) // 2 and qt.data.view(np.uint8)[-1] & 0x0F == 0
+
+
+def test_int4_per_channel_ties_round_half_away_from_zero():
+    # One column with abs-max 7 (scale exactly 1.0): ties go away from zero,
+    # where numpy's half-to-even would give 2, -2, 0, 0, 4 for the first five
+    col = np.array([2.5, -2.5, 0.5, -0.5, 3.5, 7.0, -6.5, 8.0 / 8.0], np.float32).reshape(-1, 1)
+    qt = O.quantize_int4_per_channel(col)
+    assert qt.scales[0] == np.float32(1.0)
+    assert _nibbles_by_shift(qt.data, 8).tolist() == [3, -3, 1, -1, 4, 7, -7, 1]
+    ne = O.quantize_int4_per_channel(col, O.ROUND_NUMPY)
+    assert _nibbles_by_shift(ne.data, 8).tolist() == [2, -2, 0, 0, 4, 7, -6, 1]
+
+
+def test_int4_per_channel_random_invariants():
+    # 37 x 29 N(0, 0.3): the error of every element is at most half its
+    # column's scale (no element reaches the clamp, since |w| <= absMax),
+    # every column's abs-max element gives +-7, and the packed order is the
+    # flat [row, col] order (element i in byte i / 2, high nibble when even)
+    w = O.fill_normal(91, 37 * 29, std=0.3).reshape(37, 29)
+    qt = O.quantize_int4_per_channel(w)
+    s = qt.scales.astype(np.float64)
+    np.testing.assert_array_equal(qt.scales, (np.abs(w).max(0) / np.float32(7)).astype(np.float32))
+    q = _nibbles_by_shift(qt.data, w.size).reshape(37, 29)
+    assert np.abs(q).max() <= 7
+    err = np.abs(q * s[None, :] - w.astype(np.float64))
+    assert np.all(err <= 0.5 * s[None, :] * (1 + 1e-6))
+    am = np.abs(w).argmax(0)
+    np.testing.assert_array_equal(q[am, np.arange(29)], 7 * np.sign(w[am, np.arange(29)]).astype(int))
+    # the same values quantized by the per-group quantizer with one group per
+    # column (columns laid out contiguously) give the same nibbles
+    for c in range(29):
+        g = O.quantize_int4(np.ascontiguousarray(w[:, c]), 37)
+        assert g.scales[0] == qt.scales[c]
+        np.testing.assert_array_equal(_nibbles_by_shift(g.data, 37), q[:, c])
+
+
 def test_validate_preconditions():
     good = O.quantize_per_channel(np.ones((4, 6), np.float32))
     assert O.validate(good) == O.OK

@@ -145,3 +145,42 @@ def test_noalloc_rejects_scratch_beyond_the_limit(backend):
         backend.set_option(_abi.OPT_NOALLOC_SCRATCH_BYTES, 0)
     with pytest.raises(T.HIPBackendError):
         backend.set_option(_abi.OPT_NOALLOC_SCRATCH_BYTES, (16 << 20) + 1)
+
+
+def test_noalloc_rejects_a_later_piece_beyond_the_limit(backend):
+    # x runs in pieces of up to 8 rows, and the pieces of one call can take
+    # different routes: with the matrix-core GEMV forced from 2 rows, 10 rows
+    # on INT4 [2048 -> 1024] run 8 rows on the burst GEMV (no scratch), then
+    # the last 2 on the matrix-core GEMV split along K (32 KB of scratch).
+    # With the limit at 4 KB the second launch is refused: the call returns
+    # TBH_E_INVALID (y unspecified), and with the limit restored the same
+    # call equals tbh_matmul_device bit for bit.
+    import torch
+
+    pq, W = _int4_nk(931, 2048, 1024)
+    w = backend.weight(pq)
+    xh = O.fill_normal(932, 10 * 2048).reshape(10, 2048)
+    x = torch.from_numpy(xh).cuda()
+    y = torch.empty((10, 1024), dtype=torch.float32, device="cuda")
+    y_ref = torch.empty_like(y)
+    s = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    backend.set_option(_abi.OPT_SGEMV_MIN_ROWS, 2)
+    try:
+        backend.set_option(_abi.OPT_NOALLOC_SCRATCH_BYTES, 4096)
+        try:
+            st = _noalloc(w, x, y, s)
+            torch.cuda.synchronize()
+            assert st == _abi.E_INVALID
+            assert "scratch" in _abi.last_error()
+        finally:
+            backend.set_option(_abi.OPT_NOALLOC_SCRATCH_BYTES, 0)
+        with torch.cuda.stream(s):
+            backend.matmul_device(x, w, out=y_ref, stream=s)
+            assert _noalloc(w, x, y, s) == _abi.OK, _abi.last_error()
+        torch.cuda.synchronize()
+    finally:
+        backend.set_option(_abi.OPT_SGEMV_MIN_ROWS, 0)
+    got = y.cpu().numpy()
+    np.testing.assert_array_equal(got.view(np.uint32), y_ref.cpu().numpy().view(np.uint32))
+    assert O.parity_errors(got, O.gemm_f64(xh, W))["gated"] <= GATE

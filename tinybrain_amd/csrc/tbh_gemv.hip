@@ -798,8 +798,9 @@ int env_int(const char *name, int dflt) {
 
 // Burst-kernel shapes: chunk iterations per row I <= kBurstMaxI, rows per
 // wave U a power of two with U * I <= 16.  Eight x rows take rows of at most
-// 2 x 64 chunks (K <= 2048 INT8 or 4096 INT4) and up to 80 KB of LDS (two
-// blocks per CU).
+// 2 x 64 chunks and up to 80 KB of LDS (two blocks per CU): eight staged x
+// copies of 64 x I x (32 + 4) floats fit that for INT8 at I <= 2 (K <= 2048)
+// but INT4 only at I = 1 (K <= 2048; I = 2 would need 144 KB).
 constexpr int kBurstMaxI = 6;
 constexpr int64_t kBurst8LdsBytes = 80 * 1024;
 

@@ -153,7 +153,7 @@ hipError_t launch_gemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s);
 // (0 when the fast path cannot take it).
 int64_t gemv_max_rows(const tbh_weight &w);
 // Whether launch_gemv takes eight rows of this x in one launch (the burst
-// kernel; K up to 2048 INT8 or 4096 INT4, no zero points, 16-byte aligned x).
+// kernel; K up to 2048 INT8 or INT4, no zero points, 16-byte aligned x).
 bool gemv8_supported(const tbh_weight &w, const float *x, int64_t ldx);
 
 // Fused decode GEMV (M = 1, tbh_gemv.hip): y = W . pro(x) (+ y).

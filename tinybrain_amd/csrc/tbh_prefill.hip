@@ -116,10 +116,6 @@ __device__ __forceinline__ float sbyte(uint32_t w) {
 // c reads copy c against the exact integers 16 q.  Each term differs from the
 // reference's x * fl(q * s) only in which fp32 product is rounded.
 //
-// Eight-wave blocks with K steps of 64 are held to four waves per SIMD, so
-// two blocks share a CU.  INT4 blocks with K steps of 128 (256 VGPRs) run
-// every K step in its masked form: with a second, unmasked loop form their
-// spilled registers went from 2 to 14-17.
 // Eight-wave blocks with K steps of 64 are held to four waves per SIMD
 // (two blocks per CU) where that fits: not the INT4 128 x 128 tiles (about
 // 180 VGPRs) nor runtime-layout tiles holding two or more x copies (their
@@ -133,7 +129,10 @@ void gemm_bf16(const PParams p) {
     static_assert(NC == 0 || (PREC == 4 && XF != 0 && !ZP), "runtime-layout INT4 stages split x, no zero points");
     static_assert(XF != 2 || NC > 0, "bf16 x is split only for runtime-layout scales");
     constexpr int NCC = NC > 0 ? NC : 1;                    // copies of x in LDS
-    constexpr bool kTwoForm = !(PREC == 4 && BK == 128);   // unmasked form for steps inside K
+    // Steps wholly inside K and the N tile run an unmasked loop form, except
+    // in INT4 blocks with K steps of 128 (256 VGPRs), which run every step
+    // masked: with the second form their spilled registers went from 2 to 14-17.
+    constexpr bool kTwoForm = !(PREC == 4 && BK == 128);
     constexpr int kLdsRow = BK + kRowPad;
     constexpr int NT = 64 * WV;                   // threads; waves as 2 x (WV / 2)
     constexpr int WC = WV / 2;
