@@ -23,7 +23,11 @@ times the restated reference CPU path (dequantize() single-threaded, then
 sgemm on every host CPU this process may use, capped by the CPU share
 OMP_NUM_THREADS grants) on a bounded sample of the same workload.  The
 default line also carries "decode_1p1b_int8": tokens/s of the 1.1B-shaped
-INT8 decode step (the headline metric's second half), same step counts.
+INT8 decode step (the headline metric's second half), same step counts,
+and one key per remaining BASELINE row (TABLE below: INT8 configs[0],
+INT4 configs[1] at M=8, configs[3] prefill INT8 M=2048 and INT4 M=512,
+configs[4] 7B projection set at M=8), each with its own roofline and a
+bounded CPU baseline sample (a third of --cpu-budget); --no-table skips them.
 """
 from __future__ import annotations
 
@@ -88,6 +92,19 @@ OPS = {
 }
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 RIDGE_FLOP_PER_BYTE = MFMA_BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
+
+# The rest of the BASELINE table, measured after the headline workload and
+# the 1.1B decode step in the default run, each as a key of the default line
+# with its own roofline and a bounded CPU baseline sample.
+TABLE = ["int8_pc_gemv_m1", "int4_g32_gemv_m8", "prefill_int8_m2048", "prefill_int4_m512", "proj_7b_int4_m8"]
+
+# What roofline.frac is computed from.
+FRAC_BASIS_KERNEL = ("events: HIP events on the replay stream around graphs of back-to-back launches of "
+                     "this kernel alone, so the per-launch time includes the gap between launches; the "
+                     "rocprofv3 kernel trace under profiles/ (dispatch start to end) reads a few percent less")
+FRAC_BASIS_CALL = ("events: HIP events around graphs of back-to-back calls, each call's launches (the "
+                   "split-K sum included) and the gaps between them")
+FRAC_BASIS_STEP = "events: HIP events around graph replays of whole steps, every launch and gap included"
 
 
 def alg_bytes(prec: str, gs: int, N: int, K: int, M: int) -> int:
@@ -315,8 +332,11 @@ def cpu_baseline_prefill(qt, N, K, M, budget_s: float = 15.0):
     }
 
 
-def run_prefill(args, backend, T, torch):
-    prec, gs, (N, K), M = PREFILL[args.workload]
+def measure_prefill(args, backend, T, torch, workload, cpu_budget):
+    """Prefill TFLOP/s of one PREFILL workload: graphs of back-to-back
+    tbh_matmul_bf16_device calls over a >= 2 GiB weight pool.  Returns the
+    result object (the bench line's fields)."""
+    prec, gs, (N, K), M = PREFILL[workload]
     dev = torch.device("cuda", 0)
     t_setup = time.perf_counter()
     base = make_weight(prec, gs, N, K, seed=0x7B1A0030)
@@ -336,10 +356,8 @@ def run_prefill(args, backend, T, torch):
         for i in range(20):
             backend.matmul_bf16_device(x, pool[i % n_sets], out=y, stream=cap)
         torch.cuda.synchronize()
-        print(json.dumps({"pmc_pass": True, "copy_bytes": src.numel() * 4, "workload": args.workload,
-                          "alg_bytes_per_launch": prefill_bytes(prec, gs, N, K, M)}), flush=True)
-        backend.close()
-        return
+        return {"pmc_pass": True, "copy_bytes": src.numel() * 4, "workload": workload,
+                "alg_bytes_per_launch": prefill_bytes(prec, gs, N, K, M)}
     for i in range(n_sets):
         backend.matmul_bf16_device(x, pool[i], out=y, stream=cap)
     torch.cuda.synchronize()
@@ -387,7 +405,7 @@ def run_prefill(args, backend, T, torch):
     roof.update({"traffic": profiled_traffic(prec, N, K, M, "prefill"),
                  "kernel": f"gemm_bf16 {N}x{K} M={M} ({pool[0].path})",
                  "kernel_us": round(kern_us, 3), "alg_bytes_per_launch": byts,
-                 "flops_per_launch": int(flops)})
+                 "flops_per_launch": int(flops), "frac_basis": FRAC_BASIS_CALL})
     out = {
         "metric": f"prefill dequant-GEMM TFLOP/s on bf16 MFMA ({ {'int4kn': 'INT4 runtime layout'}.get(prec, prec.upper()) }, M={M})",
         "value": round(value, 2),
@@ -402,7 +420,7 @@ def run_prefill(args, backend, T, torch):
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": args.workload,
+            "workload": workload,
             "weights": {"int4": "INT4 symmetric, group 32 along K (converter layout)",
                         "int4kn": "INT4 symmetric, group 32 along N (runtime layout, Tensor.quantize(.int4))",
                         "int8": "INT8 symmetric per output channel"}[prec],
@@ -414,8 +432,12 @@ def run_prefill(args, backend, T, torch):
         "setup_s": round(setup_s, 1),
     }
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline_prefill(base, N, K, M, args.cpu_budget)
-    print(json.dumps(out), flush=True)
+        out["cpu_baseline"] = cpu_baseline_prefill(base, N, K, M, cpu_budget)
+    return out
+
+
+def run_prefill(args, backend, T, torch):
+    print(json.dumps(measure_prefill(args, backend, T, torch, args.workload, args.cpu_budget)), flush=True)
     backend.close()
 
 
@@ -499,7 +521,7 @@ def cpu_baseline_decode(prec, gs, c, qts, budget_s: float = 15.0, M: int = 1):
     }
 
 
-def measure_decode(args, backend, T, torch, workload):
+def measure_decode(args, backend, T, torch, workload, cpu_budget=None):
     """Decode tokens/s of one DECODE workload: a HIP graph of one step,
     replayed exactly args.warmup times untimed and args.steps times timed.
     Returns the result object (the bench line's fields)."""
@@ -576,12 +598,13 @@ def measure_decode(args, backend, T, torch, workload):
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
             "kernel": "decode step (graph of all launches)", "kernel_us": round(step_us, 2),
-            "alg_bytes_per_launch": int(byts),
+            "alg_bytes_per_launch": int(byts), "frac_basis": FRAC_BASIS_STEP,
         },
         "setup_s": round(setup_s, 1),
     }
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline_decode(prec, gs, c, qts, args.cpu_budget)
+        out["cpu_baseline"] = cpu_baseline_decode(prec, gs, c, qts,
+                                                  args.cpu_budget if cpu_budget is None else cpu_budget)
     dec.close()
     return out
 
@@ -593,12 +616,13 @@ def run_decode(args, backend, T, torch):
     backend.close()
 
 
-def run_proj(args, backend, T, torch):
+def measure_proj(args, backend, T, torch, workload, cpu_budget):
     """The 7B projection set at M rows: num_layers x (q, k, v, o, gate, up,
     down) + the LM head through tbh_matmul_device, captured in one HIP
     graph.  Every layer has its own device copy of its seven weights (one
-    random init per shape), so a step streams the whole model from HBM."""
-    prec, gs, c, M = PROJ[args.workload]
+    random init per shape), so a step streams the whole model from HBM.
+    Returns the result object (the bench line's fields)."""
+    prec, gs, c, M = PROJ[workload]
     dev = torch.device("cuda", 0)
     layer, lm = decode_shapes(c)
     t_setup = time.perf_counter()
@@ -664,7 +688,7 @@ def run_proj(args, backend, T, torch):
         "dtype": "f32",
         "data": "synthetic",
         "config": {
-            "workload": args.workload, **c, "M": M,
+            "workload": workload, **c, "M": M,
             "weights": "INT4 symmetric, group 32 along K (converter layout); one random init per "
                        "projection shape, a device copy per layer",
             "step": "q, k, v, o, gate, up, down of every layer + LM head (no attention or norms)",
@@ -674,13 +698,18 @@ def run_proj(args, backend, T, torch):
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
             "kernel": "projection step (graph of all launches)", "kernel_us": round(step_us, 2),
-            "alg_bytes_per_launch": int(byts),
+            "alg_bytes_per_launch": int(byts), "frac_basis": FRAC_BASIS_STEP,
         },
         "setup_s": round(setup_s, 1),
     }
+    del graph, weights, head
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline_decode(prec, gs, c, qts, args.cpu_budget, M=M)
-    print(json.dumps(out), flush=True)
+        out["cpu_baseline"] = cpu_baseline_decode(prec, gs, c, qts, cpu_budget, M=M)
+    return out
+
+
+def run_proj(args, backend, T, torch):
+    print(json.dumps(measure_proj(args, backend, T, torch, args.workload, args.cpu_budget)), flush=True)
     backend.close()
 
 
@@ -867,6 +896,8 @@ def main():
                     help="GEMV workloads: leave out the host-pointer (tbh_matmul) timing")
     ap.add_argument("--no-decode", action="store_true",
                     help="int4_g32_gemv_m1: leave out the 1.1B decode-step measurement")
+    ap.add_argument("--no-table", action="store_true",
+                    help="int4_g32_gemv_m1: leave out the other BASELINE rows (" + ", ".join(TABLE) + ")")
     ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
                     help="summarise a rocprofv3 --kernel-trace CSV (no GPU work): per-kernel averages over "
                          "all dispatches and over the last --last dispatches of kernels matching --kernel")
@@ -882,7 +913,8 @@ def main():
         return trace_summary(args.trace_summary, args.kernel, args.last)
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; the GEMV would shard along N "
-                                   "(see DESIGN.md) but no multi-GPU path is built", "n_gpus": args.gpus}))
+                                   "(each GPU a share of the output rows, outputs all-gathered), but no "
+                                   "multi-GPU path is built", "n_gpus": args.gpus}))
         sys.exit(2)
 
     import torch
@@ -898,7 +930,44 @@ def main():
         return run_proj(args, backend, T, torch)
     if args.workload in OPS:
         return run_op(args, backend, T, torch)
-    prec, gs, shapes, M = WORKLOADS[args.workload]
+    out = measure_gemv(args, backend, T, torch, args.workload, args.cpu_budget, with_host_entry=not args.no_host_entry)
+    if args.workload == "int4_g32_gemv_m1" and not args.pmc_pass:
+        if not args.no_decode:
+            # the second half of the headline metric: decode tokens/s at the
+            # 1.1B shape, same --steps / --warmup
+            _release(torch)
+            out["decode_1p1b_int8"] = measure_decode(args, backend, T, torch, "decode_1p1b_int8")
+        if not args.no_table:
+            # the rest of the BASELINE table, each row with its roofline and a
+            # bounded sample of the reference CPU path
+            budget = args.cpu_budget / 3
+            for name in TABLE:
+                _release(torch)
+                if name in WORKLOADS:
+                    r = measure_gemv(args, backend, T, torch, name, budget, with_host_entry=False)
+                elif name in PREFILL:
+                    r = measure_prefill(args, backend, T, torch, name, budget)
+                else:
+                    r = measure_proj(args, backend, T, torch, name, budget)
+                out[name] = r
+    print(json.dumps(out), flush=True)
+    backend.close()
+
+
+def _release(torch):
+    """Let the previous measurement's pool go before the next one allocates."""
+    import gc
+
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+
+def measure_gemv(args, backend, T, torch, workload, cpu_budget, with_host_entry=True):
+    """GB/s of one WORKLOADS entry: one GEMV of each shape per step, graphs of
+    back-to-back tbh_matmul_device calls over a >= 2 GiB weight pool.
+    Returns the result object (the bench line's fields)."""
+    prec, gs, shapes, M = WORKLOADS[workload]
 
     # ---- weights: one quantized base per shape, copied into a >= 2 GiB pool
     t_setup = time.perf_counter()
@@ -925,10 +994,8 @@ def main():
         for i in range(20):
             backend.matmul_device(xs[Kd], pool[i % n_sets][jd], out=ys[jd], stream=stream)
         torch.cuda.synchronize()
-        print(json.dumps({"pmc_pass": True, "copy_bytes": src.numel() * 4, "kernel": f"{Nd}x{Kd}",
-                          "alg_bytes_per_launch": alg_bytes(prec, gs, Nd, Kd, M)}), flush=True)
-        backend.close()
-        return
+        return {"pmc_pass": True, "copy_bytes": src.numel() * 4, "kernel": f"{Nd}x{Kd}",
+                "alg_bytes_per_launch": alg_bytes(prec, gs, Nd, Kd, M)}
 
     # Launches are captured into HIP graphs, so the timed region measures the
     # GPU, not Python/ctypes launch overhead.  Step i runs one GEMV of each
@@ -1033,7 +1100,7 @@ def main():
         "dtype": "f32",
         "data": "synthetic",
         "config": {
-            "workload": args.workload,
+            "workload": workload,
             "weights": {"int4": "INT4 symmetric, group 32 along K (converter layout)",
                         "int4kn": "INT4 symmetric, group 32 along N (runtime layout, Tensor.quantize(.int4))",
                         "int8": "INT8 symmetric per output channel"}[prec],
@@ -1056,23 +1123,17 @@ def main():
             "kernel_us": round(kern_us, 3),
             "alg_bytes_per_launch": kbytes,
             "timed_dispatches": shape_n[jd],
+            "frac_basis": FRAC_BASIS_KERNEL,
         },
         "per_shape": per_shape,
         "setup_s": round(setup_s, 1),
     }
-    if not args.no_host_entry:
+    if with_host_entry:
         out["host_entry"] = host_entry(backend, pool, shapes, M, prec, gs)
-    if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(bases, shapes, M, args.cpu_budget)
     del pool
-    if args.workload == "int4_g32_gemv_m1" and not args.no_decode:
-        # the second half of the headline metric: decode tokens/s at the
-        # 1.1B shape, same --steps / --warmup
-        torch.cuda.synchronize()
-        torch.cuda.empty_cache()
-        out["decode_1p1b_int8"] = measure_decode(args, backend, T, torch, "decode_1p1b_int8")
-    print(json.dumps(out), flush=True)
-    backend.close()
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(bases, shapes, M, cpu_budget)
+    return out
 
 
 if __name__ == "__main__":
