@@ -170,6 +170,9 @@ tbh_status tbh_weight_get_info(const tbh_weight *w, tbh_weight_info *info);
  * MetalBackend.matmulQuantized / matmulINT4 (MetalBackend.swift:894-1048):
  * y[M,N] = x[M,K] . dequantize(w)[K,N] with fp32 accumulation.
  * Host pointers; synchronous (the reference commits and waits, :959-960).
+ * Up to 8 rows of x, the kernels read x from and write y to page-locked
+ * host staging, and the calling thread polls a completion word there for up
+ * to 200 us before it blocks on the stream; more rows move by DMA.
  * Calls on one device are serialised.  Like the Metal kernels, one call
  * covers any M (MetalBackend.swift:949-956): a few rows run on the GEMV
  * kernels; from a per-weight row count (8..64, TBH_OPT_MFMA_MIN_ROWS) INT8

@@ -1,6 +1,7 @@
 // tbh_api.hip -- C ABI of libtinybrain_hip: devices, weight upload + repack,
 // matmul dispatch.  Kernels live in tbh_gemv.hip and tbh_ref_kernels.hip.
 #include <algorithm>
+#include <chrono>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -140,6 +141,7 @@ tbh_status tbh_device_close(tbh_device *dev) {
     (void)hipDeviceSynchronize();
     if (dev->stage) (void)hipFree(dev->stage);
     if (dev->pin) (void)hipHostFree(dev->pin);
+    if (dev->done_flag) (void)hipHostFree(dev->done_flag);
     for (auto &ws : dev->workspaces) (void)hipFree(ws.ptr);
     for (void *p : dev->retired) (void)hipFree(p);
     if (dev->stream) (void)hipStreamDestroy(dev->stream);
@@ -912,6 +914,90 @@ tbh_status tbh_linear_device(const tbh_weight *w, const float *x, int64_t M, int
     return TBH_OK;
 }
 
+// x from page-locked host memory into the device staging buffer: one
+// 16-byte load and store per thread (src and dst 16-byte aligned).
+static __global__ __launch_bounds__(256) void stage_x(const float *__restrict__ src, float *__restrict__ dst,
+                                                       int64_t n) {
+    const int64_t n4 = n / 4, stride = (int64_t)gridDim.x * 256;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride)
+        reinterpret_cast<float4 *>(dst)[i] = reinterpret_cast<const float4 *>(src)[i];
+    for (int64_t i = 4 * n4 + (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) dst[i] = src[i];
+}
+
+// Completion word for the host-pointer calls: one thread stores the call's
+// sequence number into coherent host memory once every earlier launch on the
+// stream has finished (stream order), so the host sees completion by reading
+// its own memory instead of waiting for the stream's completion signal.
+static __global__ __launch_bounds__(64) void mark_done(uint32_t *flag, uint32_t seq) {
+    if (threadIdx.x == 0) __hip_atomic_store(flag, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// How tbh_matmul waits when the kernels write y into locked host memory
+// (TBH_HOST_WAIT, read once): 1 (default) = a mark_done launch after the
+// call's kernels, the host polling the word for up to kHostSpinUs before
+// falling back to hipStreamSynchronize; 0 = hipStreamSynchronize.  INT4 g32
+// at M = 1, us per call, synchronize / poll: 2048x2048 18.2 / 14.8,
+// 32000x2048 28.6 / 26.2; at M = 8 2048x2048 24.5 / 20.7.  With the DMA
+// copies (TBH_HOST_ENTRY = 0) polling did not pay (M = 8 step 205 / 259 us)
+// and the stream is synchronised.
+static int host_wait_mode() {
+    static const int mode = [] {
+        const char *v = std::getenv("TBH_HOST_WAIT");
+        return v && *v ? std::atoi(v) : 1;
+    }();
+    return mode;
+}
+constexpr double kHostSpinUs = 200.0;
+
+// Waits for the work enqueued so far on dev->stream.  With TBH_HOST_WAIT = 1
+// and a completion word, enqueues mark_done and polls the word (bounded),
+// then falls back to (or finishes with) hipStreamSynchronize's status.
+static hipError_t host_wait(tbh_device *dev) {
+    if (host_wait_mode() == 1) {
+        if (!dev->done_flag) {
+            void *p = nullptr;
+            if (hipHostMalloc(&p, 64, hipHostMallocMapped | hipHostMallocCoherent) == hipSuccess) {
+                dev->done_flag = (uint32_t *)p;
+                __atomic_store_n(dev->done_flag, 0u, __ATOMIC_RELEASE);
+            }
+        }
+        uint32_t *dflag = nullptr;
+        if (dev->done_flag && hipHostGetDevicePointer((void **)&dflag, dev->done_flag, 0) == hipSuccess) {
+            const uint32_t seq = ++dev->done_seq;
+            hipLaunchKernelGGL(mark_done, dim3(1), dim3(64), 0, dev->stream, dflag, seq);
+            hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            const auto t0 = std::chrono::steady_clock::now();
+            while (__atomic_load_n(dev->done_flag, __ATOMIC_ACQUIRE) != seq) {
+                const double us =
+                    std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count();
+                if (us > kHostSpinUs) return hipStreamSynchronize(dev->stream);
+            }
+            return hipSuccess;
+        }
+    }
+    return hipStreamSynchronize(dev->stream);
+}
+
+// How tbh_matmul moves x and y when they fit the page-locked staging buffer
+// (TBH_HOST_ENTRY, read once): 0 = DMA copies to and from device staging;
+// 1 = a copy kernel reads x from the locked buffer into device staging and
+// the matmul kernels write y straight into the locked buffer; 2 (default) =
+// as 1, except that one row of x is read by the matmul kernels straight from
+// the locked buffer (no copy launch).  INT4 g32, us per call with the polled
+// wait, modes 1 / 2: M = 1 2048x2048 14.8 / 12.9, 5632x2048 16.9 / 14.0,
+// 32000x2048 26.2 / 23.1 (DMA copies: 19.7, 28.6, 38.0); at M = 8, where
+// every block reading eight rows over the bus lost (2048x2048 20.7 against
+// 24.7), the copy launch stays.
+static int host_entry_mode() {
+    static const int mode = [] {
+        const char *v = std::getenv("TBH_HOST_ENTRY");
+        const int m = v && *v ? std::atoi(v) : 2;
+        return m >= 0 && m <= 2 ? m : 2;
+    }();
+    return mode;
+}
+
 tbh_status tbh_matmul(tbh_device *dev, const float *x, int64_t M, int64_t K, const tbh_weight *w,
                       float *y) {
     if (!dev || !w) return set_error(TBH_E_INVALID, "tbh_matmul: NULL device or weight");
@@ -934,12 +1020,13 @@ tbh_status tbh_matmul(tbh_device *dev, const float *x, int64_t M, int64_t K, con
     }
     float *dx = (float *)dev->stage;
     float *dy = (float *)((char *)dev->stage + ((xb + 255) & ~size_t(255)));
-    // Page-locked host staging: the CPU copies x into it and y out of it, so
-    // both transfers are plain DMA from locked pages instead of going through
-    // the runtime's staging of pageable memory (INT4 g32 at M = 1, us per
-    // call: 2048x2048 33.9 -> 19.7, 2048x5632 33.7 -> 27.1; 5632x2048 and
-    // 32000x2048 unchanged at 30 and 39).  Calls above kPinnedStageBytes, or
-    // when no locked memory can be had, copy from the caller's arrays.
+    // Page-locked host staging: the CPU copies x into it and y out of it.  Up
+    // to 8 rows of x the kernels read x from it and write y into it
+    // themselves (host_entry_mode); more rows move by DMA from and to device
+    // staging, which already beat the runtime's staging of pageable memory
+    // (INT4 g32 at M = 1, us per call: 2048x2048 33.9 -> 19.7, 2048x5632
+    // 33.7 -> 27.1).  Calls above kPinnedStageBytes, or when no locked memory
+    // can be had, copy from the caller's arrays.
     bool pinned = need <= kPinnedStageBytes;
     if (pinned && dev->pin_bytes < need) {
         if (dev->pin) (void)hipHostFree(dev->pin);   // every earlier call has synchronised
@@ -947,15 +1034,43 @@ tbh_status tbh_matmul(tbh_device *dev, const float *x, int64_t M, int64_t K, con
         dev->pin_bytes = 0;
         size_t grown = (size_t)1 << 20;
         while (grown < need) grown *= 2;
-        if (hipHostMalloc(&dev->pin, grown, hipHostMallocDefault) == hipSuccess) dev->pin_bytes = grown;
+        // coherent: kernels that read x from it or write y into it (TBH_HOST_ENTRY
+        // 1, 2) see the host's latest bytes, and the host sees theirs once the
+        // stream has synchronised, whatever the caches held from earlier calls
+        if (hipHostMalloc(&dev->pin, grown, hipHostMallocMapped | hipHostMallocCoherent) == hipSuccess)
+            dev->pin_bytes = grown;
         else dev->pin = nullptr, pinned = false;
     }
     float *px = pinned ? (float *)dev->pin : nullptr;
     float *py = pinned ? (float *)((char *)dev->pin + ((xb + 255) & ~size_t(255))) : nullptr;
-    if (pinned) std::memcpy(px, x, xb);
-    TBH_HIP(hipMemcpyAsync(dx, pinned ? px : x, xb, hipMemcpyHostToDevice, dev->stream), "tbh_matmul: copy x");
     Scratch scr;
     scr.dev = dev;
+    const int mode = pinned && M <= 8 ? host_entry_mode() : 0;
+    if (mode > 0) {
+        // the kernels address the locked buffer directly (device view of it)
+        float *dpx = nullptr;
+        TBH_HIP(hipHostGetDevicePointer((void **)&dpx, dev->pin, 0), "tbh_matmul: locked buffer address");
+        float *dpy = (float *)((char *)dpx + ((xb + 255) & ~size_t(255)));
+        std::memcpy(px, x, xb);
+        const float *xin = dpx;
+        if (mode == 1 || M > 1) {
+            const int64_t n = M * K;
+            const unsigned blocks = (unsigned)std::max<int64_t>(1, std::min<int64_t>(256, (n / 4 + 255) / 256));
+            hipLaunchKernelGGL(stage_x, dim3(blocks), dim3(256), 0, dev->stream, (const float *)dpx, dx, n);
+            TBH_HIP(hipGetLastError(), "tbh_matmul: stage x");
+            xin = dx;
+        }
+        st = matmul_enqueue(w, xin, M, dpy, dev->stream, scr);
+        if (st != TBH_OK) {
+            (void)hipStreamSynchronize(dev->stream);
+            return st;
+        }
+        TBH_HIP(host_wait(dev), "tbh_matmul: synchronize");
+        std::memcpy(y, py, yb);
+        return TBH_OK;
+    }
+    if (pinned) std::memcpy(px, x, xb);
+    TBH_HIP(hipMemcpyAsync(dx, pinned ? px : x, xb, hipMemcpyHostToDevice, dev->stream), "tbh_matmul: copy x");
     st = matmul_enqueue(w, dx, M, dy, dev->stream, scr);
     if (st != TBH_OK) {
         // the copy of the caller's x may still be queued: wait for it before
