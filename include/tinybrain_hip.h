@@ -149,8 +149,22 @@ tbh_status tbh_device_get_info(const tbh_device *dev, int32_t *ordinal, int32_t 
  *     default) is the whole 16 MiB array.  A call needing more is rejected.
  *   TBH_OPT_MFMA_MIN_ROWS: fewest rows of fp32 x that tbh_matmul* send to the
  *     MFMA GEMM (x split exactly into bf16 pieces) for every weight; 0
- *     restores the per-weight rule. */
-enum { TBH_OPT_SGEMV_MIN_ROWS = 1, TBH_OPT_NOALLOC_SCRATCH_BYTES = 2, TBH_OPT_MFMA_MIN_ROWS = 3 };
+ *     restores the per-weight rule.
+ *   TBH_OPT_HOST_ENTRY: how tbh_matmul moves x and y for up to 8 rows of x:
+ *     0 = DMA copies through device staging; 1 = a copy launch brings x from
+ *     page-locked staging and the kernels write y into it; 2 (default) = as
+ *     1, with one row of x read by the kernels in place.  Initially the
+ *     environment variable TBH_HOST_ENTRY when set.
+ *   TBH_OPT_HOST_WAIT: how tbh_matmul waits in modes 1 and 2: 1 (default) =
+ *     poll a completion word in page-locked memory for up to 200 us, then
+ *     block; 0 = block on the stream.  Initially TBH_HOST_WAIT when set. */
+enum {
+    TBH_OPT_SGEMV_MIN_ROWS = 1,
+    TBH_OPT_NOALLOC_SCRATCH_BYTES = 2,
+    TBH_OPT_MFMA_MIN_ROWS = 3,
+    TBH_OPT_HOST_ENTRY = 4,
+    TBH_OPT_HOST_WAIT = 5
+};
 tbh_status tbh_device_set_option(tbh_device *dev, int32_t option, int64_t value);
 
 /* ---- weights ----------------------------------------------------------- */

@@ -19,7 +19,7 @@ LAYOUT_KN_FLAT, LAYOUT_NK_FLAT = 0, 1
 PATH_INT8_ROW, PATH_INT4_KGROUP, PATH_INT4_NGROUP, PATH_GENERIC = range(4)
 PATH_NAMES = {0: "int8_row", 1: "int4_kgroup", 2: "int4_ngroup", 3: "generic"}
 # device options (tbh_device_set_option)
-OPT_SGEMV_MIN_ROWS, OPT_NOALLOC_SCRATCH_BYTES, OPT_MFMA_MIN_ROWS = 1, 2, 3
+OPT_SGEMV_MIN_ROWS, OPT_NOALLOC_SCRATCH_BYTES, OPT_MFMA_MIN_ROWS, OPT_HOST_ENTRY, OPT_HOST_WAIT = 1, 2, 3, 4, 5
 
 # every symbol the header declares
 EXPORTS = [

@@ -127,6 +127,14 @@ tbh_status tbh_device_open(int32_t ordinal, tbh_device **out) {
         const int r = std::atoi(v);
         dev->sgemv_min_rows.store(r == 0 ? 0 : std::min(9, std::max(2, r)), std::memory_order_relaxed);
     }
+    if (const char *v = std::getenv("TBH_HOST_ENTRY"); v && *v) {   // initial TBH_OPT_HOST_ENTRY
+        const int m = std::atoi(v);
+        if (m >= 0 && m <= 2) dev->host_entry.store(m, std::memory_order_relaxed);
+    }
+    if (const char *v = std::getenv("TBH_HOST_WAIT"); v && *v) {    // initial TBH_OPT_HOST_WAIT
+        const int m = std::atoi(v);
+        if (m == 0 || m == 1) dev->host_wait.store(m, std::memory_order_relaxed);
+    }
     TBH_HIP(hipStreamCreateWithFlags(&dev->stream, hipStreamNonBlocking), "hipStreamCreate");
     *out = dev.release();
     return TBH_OK;
@@ -156,6 +164,17 @@ tbh_status tbh_device_set_option(tbh_device *dev, int32_t option, int64_t value)
         if (value != 0 && (value < 2 || value > 9))
             return set_error(TBH_E_INVALID, "TBH_OPT_SGEMV_MIN_ROWS takes 0 (per-weight rule) or 2..9");
         dev->sgemv_min_rows.store((int)value, std::memory_order_relaxed);
+        return TBH_OK;
+    case TBH_OPT_HOST_ENTRY:
+        if (value < 0 || value > 2)
+            return set_error(TBH_E_INVALID, "TBH_OPT_HOST_ENTRY takes 0 (DMA copies), 1 (copy launch, y to host "
+                                            "memory) or 2 (one row of x read in place)");
+        dev->host_entry.store((int)value, std::memory_order_relaxed);
+        return TBH_OK;
+    case TBH_OPT_HOST_WAIT:
+        if (value != 0 && value != 1)
+            return set_error(TBH_E_INVALID, "TBH_OPT_HOST_WAIT takes 0 (stream synchronise) or 1 (polled word)");
+        dev->host_wait.store((int)value, std::memory_order_relaxed);
         return TBH_OK;
     case TBH_OPT_MFMA_MIN_ROWS:
         if (value < 0 || value > INT32_MAX)
@@ -933,27 +952,20 @@ static __global__ __launch_bounds__(64) void mark_done(uint32_t *flag, uint32_t 
 }
 
 // How tbh_matmul waits when the kernels write y into locked host memory
-// (TBH_HOST_WAIT, read once): 1 (default) = a mark_done launch after the
-// call's kernels, the host polling the word for up to kHostSpinUs before
-// falling back to hipStreamSynchronize; 0 = hipStreamSynchronize.  INT4 g32
-// at M = 1, us per call, synchronize / poll: 2048x2048 18.2 / 14.8,
-// 32000x2048 28.6 / 26.2; at M = 8 2048x2048 24.5 / 20.7.  With the DMA
-// copies (TBH_HOST_ENTRY = 0) polling did not pay (M = 8 step 205 / 259 us)
-// and the stream is synchronised.
-static int host_wait_mode() {
-    static const int mode = [] {
-        const char *v = std::getenv("TBH_HOST_WAIT");
-        return v && *v ? std::atoi(v) : 1;
-    }();
-    return mode;
-}
+// (TBH_OPT_HOST_WAIT, initially TBH_HOST_WAIT): 1 (default) = a mark_done
+// launch after the call's kernels, the host polling the word for up to
+// kHostSpinUs before falling back to hipStreamSynchronize; 0 =
+// hipStreamSynchronize.  INT4 g32 at M = 1, us per call, synchronize /
+// poll: 2048x2048 18.2 / 14.8, 32000x2048 28.6 / 26.2; at M = 8 2048x2048
+// 24.5 / 20.7.  With the DMA copies (TBH_OPT_HOST_ENTRY = 0) polling did not
+// pay (M = 8 step 205 / 259 us) and the stream is synchronised.
 constexpr double kHostSpinUs = 200.0;
 
 // Waits for the work enqueued so far on dev->stream.  With TBH_HOST_WAIT = 1
 // and a completion word, enqueues mark_done and polls the word (bounded),
 // then falls back to (or finishes with) hipStreamSynchronize's status.
 static hipError_t host_wait(tbh_device *dev) {
-    if (host_wait_mode() == 1) {
+    if (dev->host_wait.load(std::memory_order_relaxed) == 1) {
         if (!dev->done_flag) {
             void *p = nullptr;
             if (hipHostMalloc(&p, 64, hipHostMallocMapped | hipHostMallocCoherent) == hipSuccess) {
@@ -980,23 +992,15 @@ static hipError_t host_wait(tbh_device *dev) {
 }
 
 // How tbh_matmul moves x and y when they fit the page-locked staging buffer
-// (TBH_HOST_ENTRY, read once): 0 = DMA copies to and from device staging;
-// 1 = a copy kernel reads x from the locked buffer into device staging and
-// the matmul kernels write y straight into the locked buffer; 2 (default) =
-// as 1, except that one row of x is read by the matmul kernels straight from
-// the locked buffer (no copy launch).  INT4 g32, us per call with the polled
-// wait, modes 1 / 2: M = 1 2048x2048 14.8 / 12.9, 5632x2048 16.9 / 14.0,
-// 32000x2048 26.2 / 23.1 (DMA copies: 19.7, 28.6, 38.0); at M = 8, where
-// every block reading eight rows over the bus lost (2048x2048 20.7 against
-// 24.7), the copy launch stays.
-static int host_entry_mode() {
-    static const int mode = [] {
-        const char *v = std::getenv("TBH_HOST_ENTRY");
-        const int m = v && *v ? std::atoi(v) : 2;
-        return m >= 0 && m <= 2 ? m : 2;
-    }();
-    return mode;
-}
+// (TBH_OPT_HOST_ENTRY, initially TBH_HOST_ENTRY): 0 = DMA copies to and from
+// device staging; 1 = a copy kernel reads x from the locked buffer into
+// device staging and the matmul kernels write y straight into the locked
+// buffer; 2 (default) = as 1, except that one row of x is read by the matmul
+// kernels straight from the locked buffer (no copy launch).  INT4 g32, us per
+// call with the polled wait, modes 1 / 2: M = 1 2048x2048 14.8 / 12.9,
+// 5632x2048 16.9 / 14.0, 32000x2048 26.2 / 23.1 (DMA copies: 19.7, 28.6,
+// 38.0); at M = 8, where every block reading eight rows over the bus lost
+// (2048x2048 20.7 against 24.7), the copy launch stays.
 
 tbh_status tbh_matmul(tbh_device *dev, const float *x, int64_t M, int64_t K, const tbh_weight *w,
                       float *y) {
@@ -1022,7 +1026,7 @@ tbh_status tbh_matmul(tbh_device *dev, const float *x, int64_t M, int64_t K, con
     float *dy = (float *)((char *)dev->stage + ((xb + 255) & ~size_t(255)));
     // Page-locked host staging: the CPU copies x into it and y out of it.  Up
     // to 8 rows of x the kernels read x from it and write y into it
-    // themselves (host_entry_mode); more rows move by DMA from and to device
+    // themselves (TBH_OPT_HOST_ENTRY); more rows move by DMA from and to device
     // staging, which already beat the runtime's staging of pageable memory
     // (INT4 g32 at M = 1, us per call: 2048x2048 33.9 -> 19.7, 2048x5632
     // 33.7 -> 27.1).  Calls above kPinnedStageBytes, or when no locked memory
@@ -1045,7 +1049,7 @@ tbh_status tbh_matmul(tbh_device *dev, const float *x, int64_t M, int64_t K, con
     float *py = pinned ? (float *)((char *)dev->pin + ((xb + 255) & ~size_t(255))) : nullptr;
     Scratch scr;
     scr.dev = dev;
-    const int mode = pinned && M <= 8 ? host_entry_mode() : 0;
+    const int mode = pinned && M <= 8 ? dev->host_entry.load(std::memory_order_relaxed) : 0;
     if (mode > 0) {
         // the kernels address the locked buffer directly (device view of it)
         float *dpx = nullptr;

@@ -67,6 +67,8 @@ struct tbh_device {
     size_t pin_bytes = 0;
     uint32_t *done_flag = nullptr;   // coherent host word a host-pointer call's last launch writes
     uint32_t done_seq = 0;           // value the next call waits for (under mu)
+    std::atomic<int> host_entry{2};  // TBH_OPT_HOST_ENTRY: how tbh_matmul moves x and y
+    std::atomic<int> host_wait{1};   // TBH_OPT_HOST_WAIT: how tbh_matmul waits
     void *noalloc_scratch = nullptr;   // this GPU's scratch array (tbh_matmul_device_noalloc)
     std::atomic<int64_t> noalloc_limit{0};   // TBH_OPT_NOALLOC_SCRATCH_BYTES; 0 = the whole array
 
