@@ -80,6 +80,9 @@ PROJ = {
     "proj_7b_int4_m1": ("int4", 32, CFG_7B, 1),
     "proj_7b_int4_m8": ("int4", 32, CFG_7B, 8),
 }
+# The same sets with every projection its own launch (7 per layer) instead
+# of q|k|v and gate|up concatenated at repack (4 per layer).
+PROJ_SEP = {name + "_sep": cfg for name, cfg in PROJ.items()}
 # The other backend protocols (softmax, RMSNorm, SiLU/GELU, attention) at the
 # shapes either side of the GEMV in a 1.1B-shaped model: one launch per step
 # over a >= 2 GiB rotating pool of inputs.  name: (op, shape kwargs)
@@ -622,16 +625,27 @@ def measure_proj(args, backend, T, torch, workload, cpu_budget):
     graph.  Every layer has its own device copy of its seven weights (one
     random init per shape), so a step streams the whole model from HBM.
     Returns the result object (the bench line's fields)."""
-    prec, gs, c, M = PROJ[workload]
+    separate = workload in PROJ_SEP
+    prec, gs, c, M = PROJ_SEP[workload] if separate else PROJ[workload]
     dev = torch.device("cuda", 0)
     layer, lm = decode_shapes(c)
     t_setup = time.perf_counter()
     qts = [make_weight(prec, gs, N, K, seed=0x7B1A0040 + j) for j, (K, N) in enumerate(layer)]
     qts.append(make_weight(prec, gs, lm[1], lm[0], seed=0x7B1A0050))
-    weights = [[T.DeviceWeight(backend, q) for q in qts[:7]] for _ in range(c["num_layers"])]
+    # launches of a layer: (K, N, parts); the parts of one launch read the
+    # same x (q, k, v; gate, up) and are concatenated at repack unless the
+    # workload runs every projection on its own
+    groups = [[j] for j in range(7)] if separate else [[0, 1, 2], [3], [4, 5], [6]]
+    launches = [(layer[g[0]][0], sum(layer[j][1] for j in g), g) for g in groups]
+
+    def device_weight(g):
+        return T.DeviceWeight(backend, qts[g[0]]) if len(g) == 1 else \
+            T.DeviceWeight.concat(backend, [qts[j] for j in g])
+
+    weights = [[device_weight(g) for _, _, g in launches] for _ in range(c["num_layers"])]
     head = T.DeviceWeight(backend, qts[7])
     setup_s = time.perf_counter() - t_setup
-    shapes = layer + [lm]
+    shapes = [(K, N) for K, N, _ in launches] + [lm]
     gen = torch.Generator(device=dev).manual_seed(3)
     xs = {K: torch.randn((M, K), generator=gen, device=dev, dtype=torch.float32) for K, _ in shapes}
     ys = {N: torch.empty((M, N), device=dev, dtype=torch.float32) for _, N in shapes}
@@ -640,7 +654,7 @@ def measure_proj(args, backend, T, torch, workload, cpu_budget):
 
     def step():
         for ws in weights:
-            for (K, N), w in zip(layer, ws):
+            for (K, N, _), w in zip(launches, ws):
                 backend.matmul_device(xs[K], w, out=ys[N], stream=cap)
         backend.matmul_device(xs[lm[0]], head, out=ys[lm[1]], stream=cap)
 
@@ -671,7 +685,7 @@ def measure_proj(args, backend, T, torch, workload, cpu_budget):
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
     step_us = e0.elapsed_time(e1) * 1e3 / args.steps
-    byts = c["num_layers"] * sum(alg_bytes(prec, gs, N, K, M) for K, N in layer) + \
+    byts = c["num_layers"] * sum(alg_bytes(prec, gs, N, K, M) for K, N, _ in launches) + \
         alg_bytes(prec, gs, lm[1], lm[0], M)
     achieved = byts / step_us / 1e3
     out = {
@@ -691,8 +705,10 @@ def measure_proj(args, backend, T, torch, workload, cpu_budget):
             "workload": workload, **c, "M": M,
             "weights": "INT4 symmetric, group 32 along K (converter layout); one random init per "
                        "projection shape, a device copy per layer",
-            "step": "q, k, v, o, gate, up, down of every layer + LM head (no attention or norms)",
-            "launches_per_step": 7 * c["num_layers"] + 1,
+            "step": "q, k, v, o, gate, up, down of every layer + LM head (no attention or norms)" +
+                    ("; every projection its own launch" if separate else
+                     "; q|k|v and gate|up concatenated at repack (one launch each, as the decode step)"),
+            "launches_per_step": len(launches) * c["num_layers"] + 1,
         },
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -885,7 +901,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="int4_g32_gemv_m1",
-                    choices=sorted(WORKLOADS) + sorted(PREFILL) + sorted(DECODE) + sorted(PROJ) + sorted(OPS))
+                    choices=sorted(WORKLOADS) + sorted(PREFILL) + sorted(DECODE) + sorted(PROJ) + sorted(PROJ_SEP) +
+                    sorted(OPS))
     ap.add_argument("--pool-gib", type=float, default=2.2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--max-seq", type=int, default=0,
@@ -926,7 +943,7 @@ def main():
         return run_prefill(args, backend, T, torch)
     if args.workload in DECODE:
         return run_decode(args, backend, T, torch)
-    if args.workload in PROJ:
+    if args.workload in PROJ or args.workload in PROJ_SEP:
         return run_proj(args, backend, T, torch)
     if args.workload in OPS:
         return run_op(args, backend, T, torch)

@@ -175,6 +175,23 @@ tbh_status tbh_device_set_option(tbh_device *dev, int32_t option, int64_t value)
  * returns TBH_E_UNSUPPORTED (the caller's CPU fallback takes it). */
 tbh_status tbh_weight_create(tbh_device *dev, const tbh_qtensor_desc *desc,
                              tbh_weight **out);
+/* One weight that computes the outputs of n weights reading the same input,
+ * side by side: y[M, N_0 + ... + N_{n-1}] = x . [dequantize(W_0) | ... ],
+ * repacked once, so that the projections of a layer that read one x (q, k
+ * and v; gate and up: ModelRunner.swift:418-452, where each is its own
+ * apply(toRow:) call, ModelWeights.swift:47-68) run as one launch.  No
+ * single reference counterpart: it is a one-time repack of
+ * TransformerLayerWeights' quantized projections.  The parts must share K
+ * and precision and be concatenable without re-quantizing: INT8 in the
+ * [K][N] layout (per-channel, or a per-tensor scale repeated per column),
+ * INT4 in the converter layout (groups along K), or runtime-layout INT4 whose
+ * groups tile every part's N; zero points on all parts or none.  Otherwise
+ * TBH_E_UNSUPPORTED (or TBH_E_INVALID for inconsistent descriptors).
+ * Results are within the matmul tolerance of the parts' products (the
+ * kernels chosen for the wider weight may sum in another order). */
+tbh_status tbh_weight_create_concat(tbh_device *dev, int32_t n,
+                                    const tbh_qtensor_desc *const *parts,
+                                    tbh_weight **out);
 tbh_status tbh_weight_destroy(tbh_weight *w);
 tbh_status tbh_weight_get_info(const tbh_weight *w, tbh_weight_info *info);
 

@@ -25,7 +25,7 @@ OPT_SGEMV_MIN_ROWS, OPT_NOALLOC_SCRATCH_BYTES, OPT_MFMA_MIN_ROWS, OPT_HOST_ENTRY
 EXPORTS = [
     "tbh_abi_version", "tbh_last_error", "tbh_status_string",
     "tbh_device_open", "tbh_device_close", "tbh_device_get_info", "tbh_device_set_option",
-    "tbh_weight_create", "tbh_weight_destroy", "tbh_weight_get_info",
+    "tbh_weight_create", "tbh_weight_create_concat", "tbh_weight_destroy", "tbh_weight_get_info",
     "tbh_matmul", "tbh_matmul_device", "tbh_matmul_device_noalloc", "tbh_matmul_bf16_device",
     "tbh_linear_device", "tbh_dequantize", "tbh_dequantize_device",
     "tbh_decoder_create", "tbh_decoder_set_layer", "tbh_decoder_destroy",
@@ -151,6 +151,7 @@ def lib() -> ctypes.CDLL:
     L.tbh_device_get_info.argtypes = [vp, ctypes.POINTER(i32), ctypes.POINTER(i32)]
     L.tbh_device_set_option.argtypes = [vp, i32, i64]
     L.tbh_weight_create.argtypes = [vp, ctypes.POINTER(QTensorDesc), pp]
+    L.tbh_weight_create_concat.argtypes = [vp, i32, ctypes.POINTER(ctypes.POINTER(QTensorDesc)), pp]
     L.tbh_weight_destroy.argtypes = [vp]
     L.tbh_weight_get_info.argtypes = [vp, ctypes.POINTER(WeightInfo)]
     L.tbh_matmul.argtypes = [vp, vp, i64, i64, vp, vp]
@@ -197,7 +198,7 @@ def lib() -> ctypes.CDLL:
                  "tbh_decoder_step_device", "tbh_decoder_step"):
         getattr(L, name).restype = i32
     for name in ("tbh_device_open", "tbh_device_close", "tbh_device_get_info", "tbh_device_set_option",
-                 "tbh_weight_create", "tbh_weight_destroy", "tbh_weight_get_info",
+                 "tbh_weight_create", "tbh_weight_create_concat", "tbh_weight_destroy", "tbh_weight_get_info",
                  "tbh_matmul", "tbh_matmul_device", "tbh_matmul_device_noalloc", "tbh_matmul_bf16_device",
                  "tbh_linear_device",
                  "tbh_dequantize", "tbh_dequantize_device",

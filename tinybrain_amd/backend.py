@@ -31,7 +31,7 @@ import ctypes
 import threading
 import uuid
 import weakref
-from typing import Dict, Optional
+from typing import Dict, Optional, Sequence
 
 import numpy as np
 
@@ -55,20 +55,35 @@ def _check(st: int) -> None:
 class DeviceWeight:
     """A weight uploaded and repacked on the device (tbh_weight)."""
 
-    def __init__(self, backend: "HIPBackend", quantized: QuantizedTensor):
+    def __init__(self, backend: "HIPBackend", quantized: Optional[QuantizedTensor], _handle=None):
         self._lib = _abi.lib()
         self._h = ctypes.c_void_p()
-        desc = quantized.desc()
-        _check(self._lib.tbh_weight_create(backend._dev, ctypes.byref(desc), ctypes.byref(self._h)))
+        if _handle is None:
+            desc = quantized.desc()
+            _check(self._lib.tbh_weight_create(backend._dev, ctypes.byref(desc), ctypes.byref(self._h)))
+        else:
+            self._h = _handle
         self.backend = backend
         backend._own(self)
-        self.K, self.N = quantized.shape
         info = _abi.WeightInfo()
         _check(self._lib.tbh_weight_get_info(self._h, ctypes.byref(info)))
+        self.K, self.N = info.K, info.N
         self.path = _abi.PATH_NAMES[info.path]
         self.device_bytes = info.device_bytes
         self.stream_bytes = info.stream_bytes
         self.has_zero_points = bool(info.has_zero_points)
+
+    @classmethod
+    def concat(cls, backend: "HIPBackend", parts: Sequence[QuantizedTensor]) -> "DeviceWeight":
+        """One weight computing every part's outputs side by side
+        (tbh_weight_create_concat): x . [W_0 | W_1 | ...] in one launch, for
+        projections that read the same input (q, k, v; gate, up)."""
+        lib = _abi.lib()
+        descs = [p.desc() for p in parts]
+        arr = (ctypes.POINTER(_abi.QTensorDesc) * len(descs))(*[ctypes.pointer(d) for d in descs])
+        h = ctypes.c_void_p()
+        _check(lib.tbh_weight_create_concat(backend._dev, len(descs), arr, ctypes.byref(h)))
+        return cls(backend, None, _handle=h)
 
     @property
     def handle(self) -> ctypes.c_void_p:

@@ -386,13 +386,13 @@ int64_t expected_scales(const tbh_qtensor_desc &d) {
 tbh_status concat_n(const tbh_qtensor_desc *const *parts, int n, OwnedDesc &out) {
     for (int i = 0; i < n; ++i) {
         const tbh_qtensor_desc *d = parts[i];
-        if (!d || !d->data || !d->scales) return set_error(TBH_E_INVALID, "decoder: NULL weight");
+        if (!d || !d->data || !d->scales) return set_error(TBH_E_INVALID, "concatenated weights: NULL weight");
         if (d->K != parts[0]->K || d->precision != parts[0]->precision)
-            return set_error(TBH_E_INVALID, "decoder: concatenated weights differ in K or precision");
+            return set_error(TBH_E_INVALID, "concatenated weights differ in K or precision");
         if (d->n_scales != expected_scales(*d))
-            return set_error(TBH_E_INVALID, "decoder: scale count does not match mode/shape");
+            return set_error(TBH_E_INVALID, "concatenated weights: scale count does not match mode/shape");
         if ((d->zero_points != nullptr) != (parts[0]->zero_points != nullptr))
-            return set_error(TBH_E_UNSUPPORTED, "decoder: zero points on some parts only");
+            return set_error(TBH_E_UNSUPPORTED, "concatenated weights: zero points on some parts only");
     }
     const int64_t K = parts[0]->K;
     int64_t N = 0;
@@ -405,7 +405,7 @@ tbh_status concat_n(const tbh_qtensor_desc *const *parts, int n, OwnedDesc &out)
             if (parts[i]->layout != TBH_LAYOUT_KN_FLAT || parts[i]->data_bytes != K * parts[i]->N ||
                 !(parts[i]->mode == TBH_MODE_PER_CHANNEL || parts[i]->mode == TBH_MODE_SYMMETRIC ||
                   parts[i]->mode == TBH_MODE_ASYMMETRIC))
-                return set_error(TBH_E_UNSUPPORTED, "decoder: INT8 weights must be [K][N] runtime layout");
+                return set_error(TBH_E_UNSUPPORTED, "concatenated weights: INT8 parts must be the [K][N] runtime layout");
         out.data.resize((size_t)(K * N));
         out.scales.resize((size_t)N);
         if (has_zp) out.zp.resize((size_t)N);
@@ -431,7 +431,7 @@ tbh_status concat_n(const tbh_qtensor_desc *const *parts, int n, OwnedDesc &out)
                 parts[i]->group_size != gs || gs <= 0 || parts[i]->N % gs != 0 || gs % 2 != 0 ||
                 parts[i]->data_bytes != K * parts[i]->N / 2)
                 return set_error(TBH_E_UNSUPPORTED,
-                                 "decoder: runtime-layout INT4 weights need groups that tile N");
+                                 "concatenated weights: runtime-layout INT4 parts need groups that tile N");
         out.data.resize((size_t)(K * N / 2));
         out.scales.resize((size_t)(K * N / gs));
         if (has_zp) out.zp.resize(out.scales.size());
@@ -455,7 +455,7 @@ tbh_status concat_n(const tbh_qtensor_desc *const *parts, int n, OwnedDesc &out)
                 parts[i]->group_size != gs || gs <= 0 || K % gs != 0 || (K * parts[i]->N) % 2 != 0 ||
                 parts[i]->data_bytes != K * parts[i]->N / 2)
                 return set_error(TBH_E_UNSUPPORTED,
-                                 "decoder: INT4 weights must be the converter layout with K-groups");
+                                 "concatenated weights: INT4 parts must be the converter layout with K-groups");
         for (int i = 0; i < n; ++i) {
             const tbh_qtensor_desc &d = *parts[i];
             out.data.insert(out.data.end(), d.data, d.data + d.data_bytes);
@@ -569,6 +569,18 @@ tbh_status dmalloc(tbh_decoder *d, T **p, size_t count) {
 using namespace tbh;
 
 extern "C" {
+
+tbh_status tbh_weight_create_concat(tbh_device *dev, int32_t n, const tbh_qtensor_desc *const *parts,
+                                    tbh_weight **out) {
+    if (!dev || !parts || !out) return set_error(TBH_E_INVALID, "tbh_weight_create_concat: NULL argument");
+    if (n < 1) return set_error(TBH_E_INVALID, "tbh_weight_create_concat: n < 1");
+    *out = nullptr;
+    if (n == 1) return tbh_weight_create(dev, parts[0], out);
+    OwnedDesc od;
+    const tbh_status st = concat_n(parts, n, od);
+    if (st != TBH_OK) return st;
+    return tbh_weight_create(dev, &od.d, out);
+}
 
 tbh_status tbh_decoder_destroy(tbh_decoder *d) {
     if (!d) return TBH_OK;
