@@ -368,8 +368,19 @@ hipError_t launch_sgemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s, c
         const char *v = std::getenv("TBH_SGEMV_SPLIT_PCT");   // percent of the CUs to fill by K splits
         return v && *v ? std::atoi(v) : 300;
     }();
-    const int64_t want =
+    // At most kMaxSplits splits unless fewer would leave CUs without a block:
+    // past that, more splits add partial sums faster than they add blocks
+    // (us per call at M = 8 / 4, 22 / 8 splits: 4096x11008 16.4 / 15.0,
+    // 14.0 / 12.8; 2048x5632, whose 16 row blocks need 11 splits for a block
+    // per CU, 9.7 against 10.5 with 6).  TBH_SGEMV_MAX_SPLITS overrides it.
+    static const int max_splits = [] {
+        const char *v = std::getenv("TBH_SGEMV_MAX_SPLITS");
+        return v && *v ? std::atoi(v) : 0;
+    }();
+    constexpr int64_t kMaxSplits = 8;
+    int64_t want =
         4 * nblk >= 3 * cus ? 1 : std::max<int64_t>(1, (split_pct * cus / 100 + nblk - 1) / nblk);
+    want = std::min<int64_t>(want, max_splits > 0 ? max_splits : std::max(kMaxSplits, (cus + nblk - 1) / nblk));
     int64_t kchunks = ((p.chunks + want - 1) / want + kGrain - 1) / kGrain * kGrain;
     kchunks = std::min<int64_t>(kchunks, kMaxChunks);
     int64_t splits = (p.chunks + kchunks - 1) / kchunks;
