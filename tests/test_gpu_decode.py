@@ -153,7 +153,7 @@ def test_decode_tinyllama_context_520(backend):
     # BASELINE configs[2]'s head layout at its own context: hidden 2048, 32
     # query heads over 4 KV heads (8 per KV head), head_dim 64, FFN 5632,
     # vocab 32000, INT8 per-channel, 2 layers, 520 steps.  Positions 511..519
-    # run eight and nine 64-position attention ranges through the merge, as
+    # run 16 and 17 attention ranges of 32 positions through the merge, as
     # the 1.1B bench step at context 512 does.  The caches and positions
     # advance at every step on both sides; logits are gated at the range
     # edges (the oracle skips its LM head elsewhere).
@@ -239,9 +239,10 @@ def test_decode_head_dims_off_powers_of_two(backend, hd, nh, nkv, prec):
 
 
 def test_decode_merge_beyond_one_load_round(backend):
-    # head_dim 128: the merge kernel loads 16 ranges (1024 positions) per
-    # head in its first round and loops over the rest; 1100 steps reach 18
-    # ranges, so every range past the 16th goes through that loop
+    # head_dim 128: attention ranges of 32 positions; the merge kernel loads
+    # 32 ranges (1024 positions) per head in its first round and loops over
+    # the rest; 1100 steps reach 35 ranges, so every range past the 32nd
+    # goes through that loop
     cfg = T.DecoderConfig(**dict(SMALL, num_layers=1, num_heads=2, num_kv_heads=1, max_seq=1104))
     dec, ref = _model(backend, cfg, "int8", seed=71)
     rng = np.random.default_rng(71)
@@ -254,9 +255,9 @@ def test_decode_merge_beyond_one_load_round(backend):
 
 
 def test_decode_long_context_head_dim_64(backend):
-    # head_dim 64 (the 1.1B model's), 1100 steps: 18 attention ranges of 64
-    # positions, all in the merge kernel's first load round (4 lane groups x
-    # 8 loads for head_dim 64)
+    # head_dim 64 (the 1.1B model's), 1100 steps: 35 attention ranges of 32
+    # positions; the merge kernel's first load round (4 lane groups x 8
+    # loads for head_dim 64) takes 32 of them, its loop the rest
     cfg = T.DecoderConfig(**dict(SMALL, num_layers=1, max_seq=1104))
     dec, ref = _model(backend, cfg, "int8", seed=73)
     rng = np.random.default_rng(73)
@@ -269,9 +270,8 @@ def test_decode_long_context_head_dim_64(backend):
 
 
 def test_decode_merge_beyond_one_load_round_head_dim_64(backend):
-    # head_dim 64: the merge kernel's first load round covers 32 ranges
-    # (2048 positions); 2100 steps reach 33, so the last range goes through
-    # its loop
+    # head_dim 64: the merge kernel's first load round covers 32 ranges of
+    # 32 positions; 2100 steps reach 66, so 34 ranges go through its loop
     cfg = T.DecoderConfig(**dict(SMALL, num_layers=1, max_seq=2112))
     dec, ref = _model(backend, cfg, "int8", seed=79)
     rng = np.random.default_rng(79)

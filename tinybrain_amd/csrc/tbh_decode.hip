@@ -20,7 +20,8 @@
 // holds both rows of a pair and its epilogue writes silu(gate) * up),
 // RMSNorm runs in the GEMV's x staging, the residual adds in its epilogue,
 // and attention is two kernels:
-// one block per (KV head, 64 cache positions) does RoPE, the cache append
+// one block per (KV head, range of 32 cache positions at head_dim 64 and 128,
+// else 64) does RoPE, the cache append
 // and that range's softmax partials for the KV head's query heads, and a
 // merge kernel assembles the context.  The token position lives
 // in device memory and the step ends with a one-thread kernel that advances
@@ -75,7 +76,12 @@ struct AttnParams {
 };
 
 constexpr int kMaxHd = 128;
-constexpr int kSplit = 64;   // cache positions one attention block covers
+// Cache positions one attention wave covers: 32 at head_dim 64 and 128, else
+// 64.  At head_dim 128, 64 positions' key and value rows took every register
+// of the wave (256 VGPRs and 79 AGPRs, one wave per SIMD; 166 VGPRs with
+// 32).  Tokens per second at context 512, ranges of 64 / 32 / 16 positions:
+// 7B shape 650 / 669 / 650, 1.1B shape 1751 / 1788 / 1776.
+constexpr int attn_range(int hd) { return hd == 128 || hd == 64 ? 32 : 64; }
 
 // sin and cos of a RoPE angle formed in fp32 as the reference forms it
 // (Float(pos) * theta, ModelRunner.swift:480-486).  The angle is reduced by
@@ -97,7 +103,7 @@ __device__ __forceinline__ void wave_lds_fence() {
 }
 
 // Attention of one decode step, split over the cache.  One wave per (query
-// head, range of kSplit positions <= pos): it writes the range's softmax
+// head, range of attn_range(HD) positions <= pos): it writes the range's softmax
 // partial -- max m, sum l of exp(score - m), and sum of exp(score - m) * v --
 // and attention_merge combines the ranges.  A block's waves are up to four
 // query heads of one KV head (ModelRunner.swift:524-536, kvHead = head /
@@ -117,8 +123,10 @@ __device__ __forceinline__ void wave_lds_fence() {
 // group's first head appends the new k and v to the cache (:503-516).
 template <int HD>
 __global__ __launch_bounds__(256) void attention_split(const AttnParams a) {
+    constexpr int kSplit = attn_range(HD);
     constexpr int HD4 = HD / 4, PPI = 64 / HD4, NV = (kSplit + PPI - 1) / PPI, NP = HD / 2;
     constexpr int NPL = (NP + 63) / 64;  // RoPE pairs per lane
+    static_assert(kSplit == 64 || (HD4 & (HD4 - 1)) == 0, "short ranges take the cooperative key loads");
     __shared__ __attribute__((aligned(16))) float qs[4][HD];
     __shared__ __attribute__((aligned(16))) float kn[4][HD];
     __shared__ __attribute__((aligned(16))) float vn[4][HD];
@@ -154,7 +162,11 @@ __global__ __launch_bounds__(256) void attention_split(const AttnParams a) {
     // rows pg, pg + PPI, ... (whole row segments per load instruction) and a
     // DPP transpose-sum assembles the scores; otherwise one row per lane
     constexpr bool kCoop = (HD4 & (HD4 - 1)) == 0;
-    constexpr int NK = kCoop ? kSplit / PPI : HD4;
+    constexpr int NK = kCoop ? kSplit / PPI : HD4;   // key loads per lane
+    // values a lane carries into the transpose-sum: one per lane of its HD4
+    // group (key loads past NK are zero)
+    constexpr int NT = kCoop ? HD4 : 1;
+    static_assert(!kCoop || NK <= NT, "a lane's key loads fit its transpose group");
     const int pg = lane / HD4, d4 = lane % HD4;
     float4 kreg[NK];
     if constexpr (kCoop) {
@@ -197,22 +209,26 @@ __global__ __launch_bounds__(256) void attention_split(const AttnParams a) {
     wave_lds_fence();
 
     // one position per lane: lane (pg, d4) scores position pg + PPI * d4
-    // (cooperative form) or position lane
+    // (cooperative form; lanes past the range score nothing) or position lane
     const int tl = kCoop ? pg + PPI * d4 : lane;
     const int t = c0 + tl;
-    const bool tvalid = t <= pos;
+    const bool tvalid = t <= pos && tl < kSplit;
     float d = 0.0f;
     if constexpr (kCoop) {
         const float4 q4 = *(const float4 *)&qs[w][4 * d4];
         const float4 n4 = *(const float4 *)&kn[w][4 * d4];
         const float dn = q4.x * n4.x + q4.y * n4.y + q4.z * n4.z + q4.w * n4.w;
-        float part[NK];
+        float part[NT];
 #pragma unroll
-        for (int j = 0; j < NK; ++j) {
-            const float dj = q4.x * kreg[j].x + q4.y * kreg[j].y + q4.z * kreg[j].z + q4.w * kreg[j].w;
-            part[j] = c0 + pg + j * PPI == pos ? dn : dj;   // row pos: the new k
+        for (int j = 0; j < NT; ++j) {
+            if (j < NK) {
+                const float dj = q4.x * kreg[j].x + q4.y * kreg[j].y + q4.z * kreg[j].z + q4.w * kreg[j].w;
+                part[j] = c0 + pg + j * PPI == pos ? dn : dj;   // row pos: the new k
+            } else {
+                part[j] = 0.0f;
+            }
         }
-        d = wave::transpose_sum<NK>(part, lane);
+        d = wave::transpose_sum<NT>(part, lane);
     } else {
         const bool tnew = t == pos;
 #pragma unroll
@@ -226,7 +242,7 @@ __global__ __launch_bounds__(256) void attention_split(const AttnParams a) {
     const float m = wave::max(sc);                    // finite: position c0 <= pos
     const float p = tvalid ? expf(sc - m) : 0.0f;
     const float l = wave::sum(p);
-    ps[w][tl] = p;
+    if (tl < kSplit) ps[w][tl] = p;
     wave_lds_fence();
 
     float4 acc = float4{0.f, 0.f, 0.f, 0.f};
@@ -273,14 +289,15 @@ __global__ __launch_bounds__(256) void attention_split(const AttnParams a) {
 // with M = max m_s (the softmax of :545-551 assembled from the ranges).  One
 // wave per head, no block barriers: lane (sg, d4) loads the partials
 // of splits sg, sg + 64 / (hd / 4), ... (up to kMergeLoads of them) together
-// with the position, so up to 32 ranges (2048 positions at head_dim 64)
-// cost one memory round trip; splits past pos are masked out afterwards.
-// Max and sum by DPP; the value pieces of the split groups meet in LDS.
-constexpr int kMergeLoads = 8;
-
+// with the position, so up to 32 ranges (1024 positions at head_dim 64 and
+// 128, 2048 at 48 or 80..112) cost one memory round trip; splits past pos are
+// masked out afterwards.  Max and sum by DPP; the value pieces of the split
+// groups meet in LDS.
 template <int HD>
 __global__ __launch_bounds__(64) void attention_merge(const AttnParams a) {
     constexpr int HD4 = HD / 4, NSG = 64 / HD4;
+    constexpr int kSplit = attn_range(HD);
+    constexpr int kMergeLoads = HD == 128 ? 16 : 8;
     __shared__ float4 red[64];
     const int lane = threadIdx.x;
     const int head = blockIdx.x;
@@ -641,7 +658,7 @@ tbh_status tbh_decoder_create(tbh_device *dev, const tbh_decoder_config *cfg, co
     if ((st = dmalloc(d.get(), &d->gu, 2 * (size_t)c.intermediate)) != TBH_OK) return st;
     if ((st = dmalloc(d.get(), &d->logits, (size_t)c.vocab)) != TBH_OK) return st;
     if ((st = dmalloc(d.get(), &d->pos, 2)) != TBH_OK) return st;
-    d->attn_splits = (c.max_seq + kSplit - 1) / kSplit;
+    d->attn_splits = (c.max_seq + attn_range(d->head_dim) - 1) / attn_range(d->head_dim);
     if ((st = dmalloc(d.get(), &d->attn_o, (size_t)d->attn_splits * H)) != TBH_OK) return st;
     if ((st = dmalloc(d.get(), &d->attn_ml, (size_t)d->attn_splits * c.num_heads)) != TBH_OK) return st;
     // RoPE frequencies theta_i = base^(-2i / hd) in fp32 (ModelRunner.swift:476-479)
