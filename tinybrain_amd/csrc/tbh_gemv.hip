@@ -33,6 +33,7 @@
 #include <cstdlib>
 
 #include "tbh_internal.h"
+#include "tbh_wave.h"
 
 namespace tbh {
 namespace {
@@ -556,8 +557,7 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
         for (int r = 0; r < XR; ++r)
             ss += xv[0][r].x * xv[0][r].x + xv[0][r].y * xv[0][r].y + xv[0][r].z * xv[0][r].z +
                   xv[0][r].w * xv[0][r].w;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+        ss = wave::sum(ss);   // DPP and readlane: no LDS round trip per step
         if (lane == 0) red[wave] = ss;
         lds_barrier();
         ss = (red[0] + red[1]) + (red[2] + red[3]);
