@@ -113,11 +113,24 @@ __device__ __forceinline__ float dpp(float v) {
                                                                  0xF, 0xF, false));
 }
 
-// Partner value of lane ^ O.
+// Partner value of lane ^ O.  Across rows by v_permlane16_swap /
+// v_permlane32_swap of v with itself (a VALU exchange: v_permlane16_swap
+// trades odd rows of its first operand with even rows of its second, so
+// result [1] holds row r ^ 1 in even rows and [0] in odd rows; likewise for
+// 32-lane halves), inside a row by DPP; __shfl_xor would be an LDS round trip.
 template <int O>
 __device__ __forceinline__ float xchg(float v) {
-    if constexpr (O == 8) return dpp<kDppRor8>(v);
-    else return __shfl_xor(v, O);
+    if constexpr (O == 8) {
+        return dpp<kDppRor8>(v);
+    } else if constexpr (O == 16 || O == 32) {
+        const uint32_t u = __builtin_bit_cast(uint32_t, v);
+        const auto r = O == 16 ? __builtin_amdgcn_permlane16_swap(u, u, false, false)
+                               : __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        const bool upper = (__lane_id() & O) != 0;
+        return __builtin_bit_cast(float, upper ? r[0] : r[1]);
+    } else {
+        return __shfl_xor(v, O);
+    }
 }
 
 // One transpose-reduce stage over the first CNT values: lanes with bit O set
@@ -144,8 +157,8 @@ __device__ __forceinline__ float group_sum(float r) {
     if constexpr (G >= 4) r += dpp<kDppXor2>(r);
     if constexpr (G >= 8) r += dpp<kDppHalfMirror>(r);   // quads already reduced
     if constexpr (G >= 16) r += dpp<kDppRowMirror>(r);   // halves already reduced
-    if constexpr (G >= 32) r += __shfl_xor(r, 16);
-    if constexpr (G >= 64) r += __shfl_xor(r, 32);
+    if constexpr (G >= 32) r += xchg<16>(r);
+    if constexpr (G >= 64) r += xchg<32>(r);
     return r;
 }
 
