@@ -757,7 +757,7 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
         // value ridx ^ 1 (the pair's other row) sits at lane ^ (64 / V)
         static_assert(M == 1 && U >= 2, "pairs of rows within one wave");
         const float r = PREC == 8 ? tot * rs : tot;
-        const float other = __shfl_xor(r, 64 / V);
+        const float other = xchg<64 / V>(r);
         if ((lane & (64 / V - 1)) == 0 && (ridx & 1) == 0) {
             const int n = r0 + ridx;
             if (n < p.N) p.y[n / 2] = (r / (1.0f + expf(-r))) * other;

@@ -60,12 +60,21 @@ __device__ __forceinline__ float max(float v) {
     return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
 }
 
+// Value of lane ^ 16: v_permlane16_swap of v with itself trades odd rows of
+// the first operand with even rows of the second, so result [1] holds row
+// r ^ 1 in even rows and [0] in odd rows (a VALU exchange, no LDS).
+__device__ __forceinline__ float row_swap(float v, bool odd_row) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return __builtin_bit_cast(float, odd_row ? r[0] : r[1]);
+}
+
 // Transpose-sum inside aligned groups of G lanes (G = 4, 8, 16 or 32), each
 // lane holding G values: afterwards lane l holds the group's total of value
 // index l % G.  Each stage halves the values a lane carries -- a lane keeps
 // the upper half when its stage bit is set and adds the partner's copy of
 // the half it keeps -- so the cost is G - 1 exchanges instead of G full
-// reductions.  Partners: lane ^ 16 (through LDS), then row mirror, half-row
+// reductions.  Partners: lane ^ 16 (row swap), then row mirror, half-row
 // mirror, quad swaps (DPP); a mirror partner differs in the stage bit and
 // shares every higher bit, which is all the pairing needs.
 template <int CTRL, int N>
@@ -74,7 +83,7 @@ __device__ __forceinline__ void transpose_stage(float *v, bool upper) {
     for (int i = 0; i < N; ++i) {
         const float send = upper ? v[i] : v[i + N];
         const float keep = upper ? v[i + N] : v[i];
-        if constexpr (CTRL < 0) v[i] = keep + __shfl_xor(send, 16);
+        if constexpr (CTRL < 0) v[i] = keep + row_swap(send, upper);
         else v[i] = keep + dpp<CTRL>(send);
     }
 }
