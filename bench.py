@@ -25,9 +25,10 @@ OMP_NUM_THREADS grants) on a bounded sample of the same workload.  The
 default line also carries "decode_1p1b_int8": tokens/s of the 1.1B-shaped
 INT8 decode step (the headline metric's second half), same step counts,
 and one key per remaining BASELINE row (TABLE below: INT8 configs[0],
-INT4 configs[1] at M=8, configs[3] prefill INT8 M=2048 and INT4 M=512,
-configs[4] 7B projection set at M=8), each with its own roofline and a
-bounded CPU baseline sample (a third of --cpu-budget); --no-table skips them.
+INT4 configs[1] at M=4 and 8, configs[3] prefill INT8 M=2048 and INT4
+M=512, configs[4] 7B projection set at M=1 and 8 and the 7B decode step),
+each with its own roofline and a bounded CPU baseline sample (a fifth of
+--cpu-budget); --no-table skips them.
 """
 from __future__ import annotations
 
@@ -99,7 +100,8 @@ RIDGE_FLOP_PER_BYTE = MFMA_BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
 # The rest of the BASELINE table, measured after the headline workload and
 # the 1.1B decode step in the default run, each as a key of the default line
 # with its own roofline and a bounded CPU baseline sample.
-TABLE = ["int8_pc_gemv_m1", "int4_g32_gemv_m8", "prefill_int8_m2048", "prefill_int4_m512", "proj_7b_int4_m8"]
+TABLE = ["int8_pc_gemv_m1", "int4_g32_gemv_m4", "int4_g32_gemv_m8", "prefill_int8_m2048", "prefill_int4_m512",
+         "proj_7b_int4_m1", "proj_7b_int4_m8", "decode_7b_int4"]
 
 # What roofline.frac is computed from.
 FRAC_BASIS_KERNEL = ("events: HIP events on the replay stream around graphs of back-to-back launches of "
@@ -957,13 +959,16 @@ def main():
         if not args.no_table:
             # the rest of the BASELINE table, each row with its roofline and a
             # bounded sample of the reference CPU path
-            budget = args.cpu_budget / 3
+            budget = args.cpu_budget / 5
             for name in TABLE:
                 _release(torch)
                 if name in WORKLOADS:
                     r = measure_gemv(args, backend, T, torch, name, budget, with_host_entry=False)
                 elif name in PREFILL:
                     r = measure_prefill(args, backend, T, torch, name, budget)
+                elif name in DECODE:
+                    r = measure_decode(args, backend, T, torch, name, budget)
+                    r.pop("tokens_per_s")
                 else:
                     r = measure_proj(args, backend, T, torch, name, budget)
                 out[name] = r
