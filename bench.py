@@ -137,6 +137,31 @@ def profiled_traffic(prec: str, N: int, K: int, M: int, kind: str = ""):
     return None
 
 
+def profiled_step_traffic(workload: str):
+    """HBM bytes per step of a decode or projection-set workload measured with
+    rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE summed over one step's launches,
+    calibrated against a copy kernel of known size), as recorded in
+    profiles/traffic_<workload>.txt; None when no record exists."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{workload}.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_step:"):
+            return int(line.split(":", 1)[1].strip())
+    return None
+
+
+def pmc_copies(torch, dev):
+    """The calibration kernel of a --pmc-pass run: 5 device-to-device copies
+    of 64 MiB (64 MiB read and 64 MiB written per launch)."""
+    src = torch.ones(16 << 20, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return src.numel() * 4
+
+
 def host_info() -> dict:
     """Host cores as this process sees them: nproc, the CPUs it may run on,
     the CPU share the environment grants (OMP_NUM_THREADS; 16 per GPU on the
@@ -553,6 +578,19 @@ def measure_decode(args, backend, T, torch, workload, cpu_budget=None):
     cap = torch.cuda.Stream(dev)
     logits = torch.empty(c["vocab"], dtype=torch.float32, device=dev)
     tok = 1
+    if args.pmc_pass:
+        # every attention block loads its range's cache rows before it reads
+        # the position, so a step's traffic is that of context ctx whatever
+        # the (zero-filled) cache holds: no fill steps
+        dec.set_position(ctx)
+        copy_bytes = pmc_copies(torch, dev)
+        for _ in range(3):
+            dec.step_device(tok, logits, cap)
+        torch.cuda.synchronize()
+        dec.close()
+        return {"pmc_pass": True, "copy_bytes": copy_bytes, "workload": workload, "steps": 3,
+                "launches_per_step": 6 * c["num_layers"] + 1,
+                "alg_bytes_per_step": int(decode_bytes(prec, gs, c, ctx + 2))}
     for _ in range(ctx):                      # fill the KV cache: context `ctx`
         dec.step_device(tok, logits, cap)
     torch.cuda.synchronize()
@@ -601,7 +639,7 @@ def measure_decode(args, backend, T, torch, workload, cpu_budget=None):
         },
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_step_traffic(workload),
             "kernel": "decode step (graph of all launches)", "kernel_us": round(step_us, 2),
             "alg_bytes_per_launch": int(byts), "frac_basis": FRAC_BASIS_STEP,
         },
@@ -616,7 +654,7 @@ def measure_decode(args, backend, T, torch, workload, cpu_budget=None):
 
 def run_decode(args, backend, T, torch):
     out = measure_decode(args, backend, T, torch, args.workload)
-    out.pop("tokens_per_s")
+    out.pop("tokens_per_s", None)
     print(json.dumps(out), flush=True)
     backend.close()
 
@@ -659,6 +697,17 @@ def measure_proj(args, backend, T, torch, workload, cpu_budget):
             for (K, N, _), w in zip(launches, ws):
                 backend.matmul_device(xs[K], w, out=ys[N], stream=cap)
         backend.matmul_device(xs[lm[0]], head, out=ys[lm[1]], stream=cap)
+
+    if args.pmc_pass:
+        step()                                # sizes the split-K workspace
+        copy_bytes = pmc_copies(torch, dev)
+        for _ in range(3):
+            step()
+        torch.cuda.synchronize()
+        byts = c["num_layers"] * sum(alg_bytes(prec, gs, N, K, M) for K, N, _ in launches) + \
+            alg_bytes(prec, gs, lm[1], lm[0], M)
+        return {"pmc_pass": True, "copy_bytes": copy_bytes, "workload": workload, "steps": 3,
+                "calls_per_step": len(launches) * c["num_layers"] + 1, "alg_bytes_per_step": int(byts)}
 
     step()                                    # eager: sizes the split-K workspace of `cap`
     torch.cuda.synchronize()
@@ -714,7 +763,7 @@ def measure_proj(args, backend, T, torch, workload, cpu_budget):
         },
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_step_traffic(workload),
             "kernel": "projection step (graph of all launches)", "kernel_us": round(step_us, 2),
             "alg_bytes_per_launch": int(byts), "frac_basis": FRAC_BASIS_STEP,
         },
@@ -925,7 +974,8 @@ def main():
     ap.add_argument("--pmc-pass", action="store_true",
                     help="for rocprofv3 --pmc: 5 plain copies of 64 MiB (calibration kernel of "
                          "known size) then 20 launches of the dominant GEMV (of the GEMM for a "
-                         "prefill workload); no timing")
+                         "prefill workload; 3 eager steps for a decode or projection-set workload); "
+                         "no timing")
     args = ap.parse_args()
 
     if args.trace_summary:
