@@ -967,16 +967,20 @@ constexpr double kHostSpinUs = 200.0;
 static hipError_t host_wait(tbh_device *dev) {
     if (dev->host_wait.load(std::memory_order_relaxed) == 1) {
         if (!dev->done_flag) {
-            void *p = nullptr;
+            void *p = nullptr, *pd = nullptr;
             if (hipHostMalloc(&p, 64, hipHostMallocMapped | hipHostMallocCoherent) == hipSuccess) {
-                dev->done_flag = (uint32_t *)p;
-                __atomic_store_n(dev->done_flag, 0u, __ATOMIC_RELEASE);
+                if (hipHostGetDevicePointer(&pd, p, 0) == hipSuccess) {
+                    dev->done_flag = (uint32_t *)p;
+                    dev->done_flag_dev = (uint32_t *)pd;
+                    __atomic_store_n(dev->done_flag, 0u, __ATOMIC_RELEASE);
+                } else {
+                    (void)hipHostFree(p);
+                }
             }
         }
-        uint32_t *dflag = nullptr;
-        if (dev->done_flag && hipHostGetDevicePointer((void **)&dflag, dev->done_flag, 0) == hipSuccess) {
+        if (dev->done_flag) {
             const uint32_t seq = ++dev->done_seq;
-            hipLaunchKernelGGL(mark_done, dim3(1), dim3(64), 0, dev->stream, dflag, seq);
+            hipLaunchKernelGGL(mark_done, dim3(1), dim3(64), 0, dev->stream, dev->done_flag_dev, seq);
             hipError_t e = hipGetLastError();
             if (e != hipSuccess) return e;
             const auto t0 = std::chrono::steady_clock::now();
@@ -1035,15 +1039,24 @@ tbh_status tbh_matmul(tbh_device *dev, const float *x, int64_t M, int64_t K, con
     if (pinned && dev->pin_bytes < need) {
         if (dev->pin) (void)hipHostFree(dev->pin);   // every earlier call has synchronised
         dev->pin = nullptr;
+        dev->pin_dev = nullptr;
         dev->pin_bytes = 0;
         size_t grown = (size_t)1 << 20;
         while (grown < need) grown *= 2;
         // coherent: kernels that read x from it or write y into it (TBH_HOST_ENTRY
         // 1, 2) see the host's latest bytes, and the host sees theirs once the
         // stream has synchronised, whatever the caches held from earlier calls
-        if (hipHostMalloc(&dev->pin, grown, hipHostMallocMapped | hipHostMallocCoherent) == hipSuccess)
+        if (hipHostMalloc(&dev->pin, grown, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess) {
+            dev->pin = nullptr;
+            pinned = false;
+        } else if (hipHostGetDevicePointer(&dev->pin_dev, dev->pin, 0) != hipSuccess) {
+            (void)hipHostFree(dev->pin);
+            dev->pin = nullptr;
+            dev->pin_dev = nullptr;
+            pinned = false;
+        } else {
             dev->pin_bytes = grown;
-        else dev->pin = nullptr, pinned = false;
+        }
     }
     float *px = pinned ? (float *)dev->pin : nullptr;
     float *py = pinned ? (float *)((char *)dev->pin + ((xb + 255) & ~size_t(255))) : nullptr;
@@ -1052,8 +1065,7 @@ tbh_status tbh_matmul(tbh_device *dev, const float *x, int64_t M, int64_t K, con
     const int mode = pinned && M <= 8 ? dev->host_entry.load(std::memory_order_relaxed) : 0;
     if (mode > 0) {
         // the kernels address the locked buffer directly (device view of it)
-        float *dpx = nullptr;
-        TBH_HIP(hipHostGetDevicePointer((void **)&dpx, dev->pin, 0), "tbh_matmul: locked buffer address");
+        float *dpx = (float *)dev->pin_dev;
         float *dpy = (float *)((char *)dpx + ((xb + 255) & ~size_t(255)));
         std::memcpy(px, x, xb);
         const float *xin = dpx;

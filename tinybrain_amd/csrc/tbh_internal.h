@@ -64,8 +64,10 @@ struct tbh_device {
     void *stage = nullptr;       // device staging for the host-pointer calls
     size_t stage_bytes = 0;
     void *pin = nullptr;         // page-locked host staging for the host-pointer calls
+    void *pin_dev = nullptr;     // the device's view of it
     size_t pin_bytes = 0;
     uint32_t *done_flag = nullptr;   // coherent host word a host-pointer call's last launch writes
+    uint32_t *done_flag_dev = nullptr;   // the device's view of it
     uint32_t done_seq = 0;           // value the next call waits for (under mu)
     std::atomic<int> host_entry{2};  // TBH_OPT_HOST_ENTRY: how tbh_matmul moves x and y
     std::atomic<int> host_wait{1};   // TBH_OPT_HOST_WAIT: how tbh_matmul waits
