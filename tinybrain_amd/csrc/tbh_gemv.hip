@@ -447,23 +447,37 @@ __device__ __forceinline__ void lds_barrier() {
 // N-block; NG = 2 (M = 1): rows alternate between two interleaved weights
 // (gate and up rows), the block stages one scaled copy of x for each, and
 // row u reads copy u & 1.
-template <int PREC, int M, int U, int I, int PRO, int EPI, int NG>
-__global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
+//
+// WV waves per block; KS = 2 splits every row's chunks between two waves of
+// the block (wave w takes row group w % (WV / 2) and chunk iterations
+// I (w / (WV / 2)) .. I (w / (WV / 2)) + I - 1), and the upper part's wave
+// totals are added to the lower part's through LDS, lower + upper, in the
+// same launch.  Long rows then keep more waves per CU busy on the same
+// rows: a block stages all of x once whatever its K split.
+template <int PREC, int M, int U, int I, int PRO, int EPI, int NG, int WV = 4, int KS = 1>
+__global__ __launch_bounds__(64 * WV) void gemv_burst(const KParams p) {
     constexpr int CE = PREC == 8 ? 16 : 32;
     constexpr int CS = CE + 4;
     constexpr int V = M * U;           // M and U are powers of two
-    constexpr int XR = I * CE / 16;    // float4 x loads per thread and x row
+    constexpr int NT = 64 * WV;        // threads per block
+    constexpr int RG = WV / KS;        // row groups per block
+    constexpr int XR = 16 * I * KS * CE / NT;  // float4 x loads per thread and x row
     constexpr int XC = NG == 2 ? 2 : M;   // x copies in LDS
     static_assert(PRO == PRO_NONE || M == 1, "fused prologues take one x row");
     static_assert(NG == 0 || PREC == 4, "groups along N are INT4 only");
     static_assert(NG != 2 || (M == 1 && U % 2 == 0), "interleaved pairs: one x row, whole pairs per wave");
+    static_assert((WV == 4 || WV == 8) && (KS == 1 || KS == 2), "four or eight waves, one or two K parts");
+    static_assert(XR * NT == 16 * I * KS * CE, "whole float4 x loads per thread");
     extern __shared__ float4 xs4[];
-    __shared__ float red[4];
+    __shared__ float red[WV];
+    __shared__ float upper_tot[KS > 1 ? RG * 64 : 1];
 
-    constexpr int lds_row = 64 * I * CS;  // LDS floats per x row: every slot the loads cover
+    constexpr int lds_row = 64 * I * KS * CS;  // LDS floats per x row: every slot the loads cover
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps r0 scalar
-    const int r0 = (blockIdx.x * 4 + wave) * U;
+    const int part = KS == 1 ? 0 : wave / RG;   // K part of this wave
+    const int grp = KS == 1 ? wave : wave % RG;  // row group of this wave
+    const int r0 = (blockIdx.x * RG + grp) * U;
 
     // ---- 1. x loads (16-byte aligned rows, K % 4 == 0; clamped addresses,
     // zeroed beyond K).  No branches before the weight loads: a branch merge
@@ -474,7 +488,7 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
         const float *xr = p.x + (int64_t)(M == 1 ? 0 : min(m, p.m_act - 1)) * p.ldx;
 #pragma unroll
         for (int r = 0; r < XR; ++r) {
-            const int k = 4 * (tid + 256 * r);
+            const int k = 4 * (tid + NT * r);
             const float4 t = *(const float4 *)(xr + min(k, p.K - 4));  // x_vec4 holds
             const bool in = k < p.K;
             xv[m][r] = float4{in ? t.x : 0.f, in ? t.y : 0.f, in ? t.z : 0.f, in ? t.w : 0.f};
@@ -483,14 +497,14 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
     // NG: this block's per-k scale row(s), [Kp] each, read like x
     float4 tv[NG == 2 ? 2 : 1][XR];
     if constexpr (NG > 0) {
-        const int rb = blockIdx.x * 4 * U;   // the block's first row
+        const int rb = blockIdx.x * RG * U;   // the block's first row
 #pragma unroll
         for (int c = 0; c < (NG == 2 ? 2 : 1); ++c) {
             const int nb = NG == 2 ? c * p.nb_half + min((rb >> 1) / p.rpn, p.nb_half - 1) : rb / p.rpn;
             const float *tr = p.scales + (int64_t)nb * p.Kp;
 #pragma unroll
             for (int r = 0; r < XR; ++r) {
-                const int k = 4 * (tid + 256 * r);
+                const int k = 4 * (tid + NT * r);
                 tv[c][r] = *(const float4 *)(tr + min(k, p.Kp - 4));   // beyond Kp: x is zero
             }
         }
@@ -499,7 +513,7 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
     if constexpr (PRO == PRO_RMSNORM) {
 #pragma unroll
         for (int r = 0; r < XR; ++r) {
-            const int k = 4 * (tid + 256 * r);
+            const int k = 4 * (tid + NT * r);
             const float4 t = *(const float4 *)(p.g + min(k, p.K - 4));
             const bool in = k < p.K;
             av[r] = float4{in ? t.x : 0.f, in ? t.y : 0.f, in ? t.z : 0.f, in ? t.w : 0.f};
@@ -513,7 +527,7 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
     float s[I][U];
 #pragma unroll
     for (int i = 0; i < I; ++i) {
-        const int c = min(lane + 64 * i, p.chunks - 1);  // idle lanes re-read a valid chunk
+        const int c = min(lane + 64 * (part * I + i), p.chunks - 1);  // idle lanes re-read a valid chunk
         // a shift, not a division: a per-lane integer division here delays
         // every wave's first loads (measured 9.7 -> 9.0 us on 32000x2048)
         const int g = c >> p.cpg_shift;
@@ -555,7 +569,7 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
         if (p.xcopy != nullptr && blockIdx.x == 0) {
 #pragma unroll
             for (int r = 0; r < XR; ++r) {
-                const int k = 4 * (tid + 256 * r);
+                const int k = 4 * (tid + NT * r);
                 if (k < p.K) *(float4 *)(p.xcopy + k) = xv[0][r];
             }
         }
@@ -574,6 +588,7 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
         if (lane == 0) red[wave] = ss;
         lds_barrier();
         ss = (red[0] + red[1]) + (red[2] + red[3]);
+        if constexpr (WV == 8) ss += (red[4] + red[5]) + (red[6] + red[7]);
         const float inv = 1.0f / __builtin_sqrtf(ss / (float)p.K + p.eps);
 #pragma unroll
         for (int r = 0; r < XR; ++r) {
@@ -591,7 +606,7 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
     for (int m = 0; m < XC; ++m)
 #pragma unroll
         for (int r = 0; r < XR; ++r) {
-            const int k = 4 * (tid + 256 * r);
+            const int k = 4 * (tid + NT * r);
             float4 t = xv[NG == 2 ? 0 : m][r];
             if constexpr (NG > 0) {
                 const float4 sc = tv[NG == 2 ? m : 0][r];
@@ -601,7 +616,10 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
             xs4[(m * lds_row + lds_index<CE>(k)) >> 2] = t;
         }
     lds_barrier();
-    if (r0 >= p.Np) return;  // idle wave of the last block (after the barrier)
+    // idle wave of the last block (after the barrier); with a K split every
+    // wave reaches the second barrier below (an idle one computes on clamped,
+    // valid rows and stores nothing)
+    if (KS == 1 && r0 >= p.Np) return;
 
     // ---- 4. unpack and accumulate, chunk by chunk in issue order: the x
     // elements of chunk c are read from LDS once, then every row's chunk is
@@ -617,12 +635,13 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
 
 #pragma unroll
     for (int i = 0; i < I; ++i) {
-        const int c = lane + 64 * i;
+        const int c = lane + 64 * (part * I + i);
+        const bool has = (KS == 1 && i < I - 1) || c < p.chunks;
         if constexpr (M >= 8) {
             // eight x rows: each row's chunk is unpacked once into f16
             // pairs, then the x rows are taken one at a time (all eight
             // rows' x chunks at once would not fit the registers)
-            if (i < I - 1 || c < p.chunks) {
+            if (has) {
                 constexpr int XQ = CE / 4;
                 constexpr int NPAIR = CE / 2;   // f16 pairs per chunk
                 h2 ph[U][NPAIR];
@@ -680,7 +699,7 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
                     }
                 }
             }
-        } else if (i < I - 1 || c < p.chunks) {
+        } else if (has) {
             constexpr int XQ = CE / 4;  // float4 of x per chunk and x row
             float4 xq[XC][XQ];
 #pragma unroll
@@ -752,7 +771,14 @@ __global__ __launch_bounds__(256) void gemv_burst(const KParams p) {
     float v[V];
 #pragma unroll
     for (int j = 0; j < V; ++j) v[j] = acc[j / U][j % U];
-    const float tot = reduce_multi<V>(v, lane);
+    float tot = reduce_multi<V>(v, lane);
+    if constexpr (KS > 1) {
+        // lower K part + upper K part, in that order
+        if (part == 1) upper_tot[grp * 64 + lane] = tot;
+        lds_barrier();
+        if (part == 1) return;
+        tot += upper_tot[grp * 64 + lane];
+    }
     if constexpr (EPI == EPI_SILU_PAIR) {
         // value ridx ^ 1 (the pair's other row) sits at lane ^ (64 / V)
         static_assert(M == 1 && U >= 2, "pairs of rows within one wave");
@@ -817,51 +843,67 @@ int env_int(const char *name, int dflt) {
 constexpr int kBurstMaxI = 6;
 constexpr int64_t kBurst8LdsBytes = 80 * 1024;
 
-template <int PREC, int M, int U, int I, int PRO, int EPI, int NG>
+// Block layouts of the burst kernel: waves per block and K parts per row.
+enum BurstLayout : int { kW4K1 = 0, kW4K2 = 1, kW8K2 = 2 };
+
+template <int PREC, int M, int U, int I, int PRO, int EPI, int NG, int WV, int KS>
 hipError_t launch_burst_one(const KParams &p, size_t lds, hipStream_t s) {
     if constexpr (U * I > 16 || M * U > 32 || (EPI == EPI_SILU_PAIR && (U < 2 || M != 1)) ||
                   (NG > 0 && PREC != 4) || (NG == 2 && (M != 1 || U % 2 != 0)) || (M == 8 && I > 2)) {
         return hipErrorInvalidValue;
     } else {
+        constexpr int RG = WV / KS;   // row groups per block
         const int64_t waves = (p.Np + U - 1) / U;
-        const unsigned blocks = (unsigned)((waves + 3) / 4);
-        hipLaunchKernelGGL((gemv_burst<PREC, M, U, I, PRO, EPI, NG>), dim3(blocks), dim3(256), lds, s, p);
+        const unsigned blocks = (unsigned)((waves + RG - 1) / RG);
+        hipLaunchKernelGGL((gemv_burst<PREC, M, U, I, PRO, EPI, NG, WV, KS>), dim3(blocks), dim3(64 * WV), lds, s,
+                           p);
         return hipGetLastError();
     }
 }
 
+// K-split layouts are built for one x row and up to 3 chunk iterations per part
+template <int PREC, int M, int U, int I, int PRO, int EPI, int NG>
+hipError_t burst_layout(int kw, const KParams &p, size_t lds, hipStream_t s) {
+    if (kw == kW4K1) return launch_burst_one<PREC, M, U, I, PRO, EPI, NG, 4, 1>(p, lds, s);
+    if constexpr (M == 1 && I <= 3) {
+        if (kw == kW4K2) return launch_burst_one<PREC, M, U, I, PRO, EPI, NG, 4, 2>(p, lds, s);
+        if (kw == kW8K2) return launch_burst_one<PREC, M, U, I, PRO, EPI, NG, 8, 2>(p, lds, s);
+    }
+    return hipErrorInvalidValue;
+}
+
 template <int PREC, int M, int I, int PRO, int EPI, int NG>
-hipError_t burst_u(int U, const KParams &p, size_t lds, hipStream_t s) {
+hipError_t burst_u(int U, int kw, const KParams &p, size_t lds, hipStream_t s) {
     switch (U) {
-    case 1: return launch_burst_one<PREC, M, 1, I, PRO, EPI, NG>(p, lds, s);
-    case 2: return launch_burst_one<PREC, M, 2, I, PRO, EPI, NG>(p, lds, s);
-    case 4: return launch_burst_one<PREC, M, 4, I, PRO, EPI, NG>(p, lds, s);
-    case 8: return launch_burst_one<PREC, M, 8, I, PRO, EPI, NG>(p, lds, s);
-    case 16: return launch_burst_one<PREC, M, 16, I, PRO, EPI, NG>(p, lds, s);
+    case 1: return burst_layout<PREC, M, 1, I, PRO, EPI, NG>(kw, p, lds, s);
+    case 2: return burst_layout<PREC, M, 2, I, PRO, EPI, NG>(kw, p, lds, s);
+    case 4: return burst_layout<PREC, M, 4, I, PRO, EPI, NG>(kw, p, lds, s);
+    case 8: return burst_layout<PREC, M, 8, I, PRO, EPI, NG>(kw, p, lds, s);
+    case 16: return burst_layout<PREC, M, 16, I, PRO, EPI, NG>(kw, p, lds, s);
     default: return hipErrorInvalidValue;
     }
 }
 
 template <int PREC, int M, int PRO, int EPI, int NG = 0>
-hipError_t burst_i(int I, int U, const KParams &p, size_t lds, hipStream_t s) {
+hipError_t burst_i(int I, int U, int kw, const KParams &p, size_t lds, hipStream_t s) {
     switch (I) {
-    case 1: return burst_u<PREC, M, 1, PRO, EPI, NG>(U, p, lds, s);
-    case 2: return burst_u<PREC, M, 2, PRO, EPI, NG>(U, p, lds, s);
-    case 3: return burst_u<PREC, M, 3, PRO, EPI, NG>(U, p, lds, s);
-    case 4: return burst_u<PREC, M, 4, PRO, EPI, NG>(U, p, lds, s);
-    case 5: return burst_u<PREC, M, 5, PRO, EPI, NG>(U, p, lds, s);
-    case 6: return burst_u<PREC, M, 6, PRO, EPI, NG>(U, p, lds, s);
+    case 1: return burst_u<PREC, M, 1, PRO, EPI, NG>(U, kw, p, lds, s);
+    case 2: return burst_u<PREC, M, 2, PRO, EPI, NG>(U, kw, p, lds, s);
+    case 3: return burst_u<PREC, M, 3, PRO, EPI, NG>(U, kw, p, lds, s);
+    case 4: return burst_u<PREC, M, 4, PRO, EPI, NG>(U, kw, p, lds, s);
+    case 5: return burst_u<PREC, M, 5, PRO, EPI, NG>(U, kw, p, lds, s);
+    case 6: return burst_u<PREC, M, 6, PRO, EPI, NG>(U, kw, p, lds, s);
     default: return hipErrorInvalidValue;
     }
 }
 
 template <int PREC, int NG = 0>
-hipError_t burst_m(int M, int I, int U, const KParams &p, size_t lds, hipStream_t s) {
+hipError_t burst_m(int M, int I, int U, int kw, const KParams &p, size_t lds, hipStream_t s) {
     switch (M) {
-    case 1: return burst_i<PREC, 1, PRO_NONE, EPI_STORE, NG>(I, U, p, lds, s);
-    case 2: return burst_i<PREC, 2, PRO_NONE, EPI_STORE, NG>(I, U, p, lds, s);
-    case 4: return burst_i<PREC, 4, PRO_NONE, EPI_STORE, NG>(I, U, p, lds, s);
-    case 8: return burst_i<PREC, 8, PRO_NONE, EPI_STORE, NG>(I, U, p, lds, s);
+    case 1: return burst_i<PREC, 1, PRO_NONE, EPI_STORE, NG>(I, U, kw, p, lds, s);
+    case 2: return burst_i<PREC, 2, PRO_NONE, EPI_STORE, NG>(I, U, kw, p, lds, s);
+    case 4: return burst_i<PREC, 4, PRO_NONE, EPI_STORE, NG>(I, U, kw, p, lds, s);
+    case 8: return burst_i<PREC, 8, PRO_NONE, EPI_STORE, NG>(I, U, kw, p, lds, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -870,13 +912,13 @@ hipError_t burst_m(int M, int I, int U, const KParams &p, size_t lds, hipStream_
 // step uses.  Interleaved gate|up weights with groups along N take the
 // two-copy form (NG = 2) of the pair epilogue.
 template <int PREC, int NG = 0>
-hipError_t burst_fused(int pro, int epi, int I, int U, const KParams &p, size_t lds, hipStream_t s) {
+hipError_t burst_fused(int pro, int epi, int I, int U, int kw, const KParams &p, size_t lds, hipStream_t s) {
     if (NG < 2 && pro == PRO_RMSNORM && epi == EPI_STORE)
-        return burst_i<PREC, 1, PRO_RMSNORM, EPI_STORE, NG>(I, U, p, lds, s);
+        return burst_i<PREC, 1, PRO_RMSNORM, EPI_STORE, NG>(I, U, kw, p, lds, s);
     if (NG < 2 && pro == PRO_NONE && epi == EPI_ACCUMULATE)
-        return burst_i<PREC, 1, PRO_NONE, EPI_ACCUMULATE, NG>(I, U, p, lds, s);
+        return burst_i<PREC, 1, PRO_NONE, EPI_ACCUMULATE, NG>(I, U, kw, p, lds, s);
     if (NG != 1 && pro == PRO_RMSNORM && epi == EPI_SILU_PAIR)
-        return burst_i<PREC, 1, PRO_RMSNORM, EPI_SILU_PAIR, NG>(I, U, p, lds, s);
+        return burst_i<PREC, 1, PRO_RMSNORM, EPI_SILU_PAIR, NG>(I, U, kw, p, lds, s);
     return hipErrorInvalidValue;
 }
 
@@ -927,24 +969,46 @@ KParams make_params(const tbh_weight &w, const GemvArgs &a) {
 // `waves_per_cu` waves per CU, so small matrices spread over the whole GPU
 // and large ones keep up to 16 chunk loads in flight per lane.
 bool burst_shape(const tbh_weight &w, const KParams &p, int M, int *I_out, int *U_out,
-                 int64_t *lds_out) {
+                 int64_t *lds_out, int *kw_out) {
     static const int kernel_sel = env_int("TBH_GEMV_PERSISTENT", 0);
     static const int burst_wpc = env_int("TBH_GEMV_WAVES_PER_CU", 16);
     static const int u_force = env_int("TBH_GEMV_U", 0);
-    const int I = (p.chunks + 63) / 64;
+    static const int ks_force = env_int("TBH_GEMV_KS", 0);
+    static const int wv_force = env_int("TBH_GEMV_WV", 0);
+    const int It = (p.chunks + 63) / 64;   // chunk iterations per row
+    const int64_t cus = std::max(1, w.dev->cu_count);
+    // K parts per row.  One x row with rows of five or six chunk iterations
+    // (INT4 K > 8192, INT8 K > 4096), or of four with at least 32 rows per CU:
+    // two waves per row, four rows per wave, when that still leaves 8 waves
+    // per CU.  A wave then reads each staged x chunk for four rows, and the
+    // waves of a long matrix hold 8-12 chunks each instead of 12-16 (us per
+    // launch, one part / two: INT4 4096x11008 9.07-9.29 / 8.41-8.54, INT8
+    // 11008x4096 10.0-10.8 / 9.50-9.77, INT4 8192x8192 11.07 / 10.26; INT8
+    // 4096x4096, already two rows of 8 chunks per wave, 4.86 / 4.94; INT8
+    // 2048x5632, too few rows, 3.97 / 4.01; rows of two or three iterations
+    // no faster).
+    int ks = 1, wv = 4;
+    const bool split = ks_force == 2 || (ks_force == 0 && M == 1 && It >= 4 && w.Np / 4 >= 4 * cus &&
+                                         (It >= 5 || w.Np / 4 >= 8 * cus));
+    if (M == 1 && split && It >= 2 && (It + 1) / 2 <= 3) {
+        ks = 2;
+        wv = wv_force == 8 ? 8 : 4;
+    }
+    const int I = (It + ks - 1) / ks;     // chunk iterations per wave
     const int ce = w.precision == TBH_PREC_INT8 ? kInt8ChunkElems : kInt4ChunkElems;
     const bool ng = w.path == Path::Int4NGroup;
     const int copies = w.ng_pairs ? 2 : M;   // x copies the block stages in LDS
-    const int64_t blds = (int64_t)copies * 64 * I * (ce + 4) * (int64_t)sizeof(float);
-    if (kernel_sel || !(M == 1 || M == 2 || M == 4 || M == 8) || w.zp != nullptr || I > kBurstMaxI ||
-        !p.x_vec4 || blds > (M == 8 ? kBurst8LdsBytes : kMaxLdsBytes) || (M == 8 && I > 2) || !(w.path == Path::Int8Row || w.path == Path::Int4KGroup || ng) ||
+    const int64_t blds = (int64_t)copies * 64 * I * ks * (ce + 4) * (int64_t)sizeof(float);
+    if (kernel_sel || !(M == 1 || M == 2 || M == 4 || M == 8) || w.zp != nullptr || It > kBurstMaxI ||
+        !p.x_vec4 || blds > (M == 8 ? kBurst8LdsBytes : kMaxLdsBytes) || (M == 8 && It > 2) || !(w.path == Path::Int8Row || w.path == Path::Int4KGroup || ng) ||
         (w.path == Path::Int4KGroup && p.cpg_shift < 0) || w.mfma_tiles || (w.ng_pairs && M != 1) ||
         (ng && (p.rpn <= 0 || p.Kp % 4 != 0)))
         return false;
-    const int64_t cus = std::max(1, w.dev->cu_count);
     // U * I <= 16 weight chunks per lane; M * U <= 32 values in the reduce
     int U = 1;
-    if (M == 1) {
+    if (M == 1 && ks == 2 && ks_force == 0) {
+        U = 4;
+    } else if (M == 1) {
         // one x row: four rows per wave once that still leaves >= 8 waves
         // per CU, else two (measured on every decode shape of the 1.1B and
         // 7B models and the four INT4 shapes: one row per wave is slower
@@ -972,13 +1036,15 @@ bool burst_shape(const tbh_weight &w, const KParams &p, int M, int *I_out, int *
         // 3.52 with too few waves)
         if (u_force == 0 && M == 1 && !w.ng_pairs && 8 * I <= 16 && p.rpn % 32 == 0 && w.Np >= 4096) U = 8;
         if (w.ng_pairs) U = std::max(U, 2);
-        const int per_block = w.ng_pairs ? 2 : 4;
+        const int rg = wv / ks;   // row groups per block
+        const int per_block = w.ng_pairs ? rg / 2 : rg;
         while (U > 1 && p.rpn % (per_block * U) != 0) U /= 2;
         if (p.rpn % (per_block * U) != 0 || (w.ng_pairs && U < 2) || U * I > 16) return false;
     }
     *I_out = I;
     *U_out = U;
     *lds_out = blds;
+    *kw_out = ks == 1 ? kW4K1 : wv == 4 ? kW4K2 : kW8K2;
     return true;
 }
 
@@ -988,18 +1054,18 @@ bool gemv8_supported(const tbh_weight &w, const float *x, int64_t ldx) {
     if (w.ng_pairs) return false;
     GemvArgs a{x, ldx, nullptr, w.N, 8};
     KParams p = make_params(w, a);
-    int I, U;
+    int I, U, kw;
     int64_t lds;
-    return burst_shape(w, p, 8, &I, &U, &lds);
+    return burst_shape(w, p, 8, &I, &U, &lds, &kw);
 }
 
 bool gemv_fused_supported(const tbh_weight &w) {
     GemvArgs a{nullptr, w.K, nullptr, w.N, 1};
     KParams p = make_params(w, a);
     p.x_vec4 = w.K % 4 == 0;  // the caller's buffers are 16-byte aligned
-    int I, U;
+    int I, U, kw;
     int64_t lds;
-    return burst_shape(w, p, 1, &I, &U, &lds);
+    return burst_shape(w, p, 1, &I, &U, &lds, &kw);
 }
 
 hipError_t launch_gemv_fused(const tbh_weight &w, const FusedGemvArgs &f, hipStream_t s) {
@@ -1010,31 +1076,31 @@ hipError_t launch_gemv_fused(const tbh_weight &w, const FusedGemvArgs &f, hipStr
     p.xcopy = f.x_copy;
     p.advance = f.advance;
     if (f.g && ((uintptr_t)f.g & 15)) return hipErrorInvalidValue;
-    int I, U;
+    int I, U, kw;
     int64_t lds;
-    if (!burst_shape(w, p, 1, &I, &U, &lds)) return hipErrorInvalidValue;
+    if (!burst_shape(w, p, 1, &I, &U, &lds, &kw)) return hipErrorInvalidValue;
     if (f.epilogue == EPI_SILU_PAIR) {
         if (w.N % 2 != 0 || 2 * I > 16) return hipErrorInvalidValue;
         U = std::max(U, 2);   // both rows of a pair in one wave
     }
     if (w.ng_pairs != (f.epilogue == EPI_SILU_PAIR && w.path == Path::Int4NGroup)) return hipErrorInvalidValue;
-    if (w.precision == TBH_PREC_INT8) return burst_fused<8>(f.prologue, f.epilogue, I, U, p, (size_t)lds, s);
+    if (w.precision == TBH_PREC_INT8) return burst_fused<8>(f.prologue, f.epilogue, I, U, kw, p, (size_t)lds, s);
     if (w.path == Path::Int4NGroup)
-        return w.ng_pairs ? burst_fused<4, 2>(f.prologue, f.epilogue, I, U, p, (size_t)lds, s)
-                          : burst_fused<4, 1>(f.prologue, f.epilogue, I, U, p, (size_t)lds, s);
-    return burst_fused<4>(f.prologue, f.epilogue, I, U, p, (size_t)lds, s);
+        return w.ng_pairs ? burst_fused<4, 2>(f.prologue, f.epilogue, I, U, kw, p, (size_t)lds, s)
+                          : burst_fused<4, 1>(f.prologue, f.epilogue, I, U, kw, p, (size_t)lds, s);
+    return burst_fused<4>(f.prologue, f.epilogue, I, U, kw, p, (size_t)lds, s);
 }
 
 hipError_t launch_gemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s) {
     const int M = (int)a.M;
     if (M >= 5 && M <= 8 && !w.ng_pairs) {   // the eight-row burst kernel only (rows past M masked)
         KParams p = make_params(w, a);
-        int I, U;
+        int I, U, kw;
         int64_t blds;
-        if (!burst_shape(w, p, 8, &I, &U, &blds)) return hipErrorInvalidValue;
-        if (w.path == Path::Int8Row) return burst_m<8>(8, I, U, p, (size_t)blds, s);
-        return w.path == Path::Int4NGroup ? burst_m<4, 1>(8, I, U, p, (size_t)blds, s)
-                                          : burst_m<4>(8, I, U, p, (size_t)blds, s);
+        if (!burst_shape(w, p, 8, &I, &U, &blds, &kw)) return hipErrorInvalidValue;
+        if (w.path == Path::Int8Row) return burst_m<8>(8, I, U, kw, p, (size_t)blds, s);
+        return w.path == Path::Int4NGroup ? burst_m<4, 1>(8, I, U, kw, p, (size_t)blds, s)
+                                          : burst_m<4>(8, I, U, kw, p, (size_t)blds, s);
     }
     if (M < 1 || M > 4 || w.ng_pairs) return hipErrorInvalidValue;
     const int64_t lds = lds_bytes_for(w, M);
@@ -1046,12 +1112,12 @@ hipError_t launch_gemv(const tbh_weight &w, const GemvArgs &a, hipStream_t s) {
         // (us per launch, VALU kernel at M = 3 / burst at M = 4: INT4
         // 2048x2048 4.48 / 3.61-3.78, 5632x2048 6.16 / 5.59)
         const int Mb = M == 3 ? 4 : M;
-        int I, U;
+        int I, U, kw;
         int64_t blds;
-        if (burst_shape(w, p, Mb, &I, &U, &blds)) {
-            if (w.path == Path::Int8Row) return burst_m<8>(Mb, I, U, p, (size_t)blds, s);
-            return w.path == Path::Int4NGroup ? burst_m<4, 1>(Mb, I, U, p, (size_t)blds, s)
-                                              : burst_m<4>(Mb, I, U, p, (size_t)blds, s);
+        if (burst_shape(w, p, Mb, &I, &U, &blds, &kw)) {
+            if (w.path == Path::Int8Row) return burst_m<8>(Mb, I, U, kw, p, (size_t)blds, s);
+            return w.path == Path::Int4NGroup ? burst_m<4, 1>(Mb, I, U, kw, p, (size_t)blds, s)
+                                              : burst_m<4>(Mb, I, U, kw, p, (size_t)blds, s);
         }
     }
 
