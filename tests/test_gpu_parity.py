@@ -176,6 +176,27 @@ def test_burst_shapes(backend, prec, K, N):
         backend.set_option(_abi.OPT_SGEMV_MIN_ROWS, 0)
 
 
+# One x row with rows of five or six chunk iterations (or four, on at least
+# 8192 rows) and at least 4096 rows: each row is split between two waves of
+# its block, whose totals meet in LDS.  Ragged K leaves the upper half's last
+# iterations partly or wholly past the row (lanes there re-read the last
+# chunk and add nothing); ragged N leaves row groups of the last block idle.
+@pytest.mark.parametrize("prec,K,N", [
+    ("int4", 9024, 4100),    # 282 chunks: I = 3 per half, the upper half's last iteration empty
+    ("int4", 8192, 8192),    # I = 4 over 8192 rows
+    ("int8", 4104, 8200),    # 257 chunks: one chunk in the upper half's second iteration
+    ("int8", 4096, 8192),    # I = 4 over 8192 rows
+])
+def test_burst_k_split(backend, prec, K, N):
+    if prec == "int8":
+        oq = _int8_pc(47 + K + N, K, N)
+        pq = _product(oq, (K, N))
+    else:
+        oq = _int4_nk(53 + K + N, K, N, 32)
+        pq = _product(oq, (K, N), T.Layout.NK_FLAT)
+    _check(backend, pq, oq, Ms=(1, 2), cpu_path=False)
+
+
 @pytest.mark.parametrize("kind,K,N", [
     ("int8", 2048, 5632),     # INT8 under 16384 outputs: 8 rows on one burst launch, the GEMM from 9
     ("int8", 2048, 1003),     # ragged N

@@ -9,8 +9,10 @@
 // 1 KiB of contiguous HBM.
 //
 // Two schedules:
-//   * gemv_burst (M in {1, 2, 4}, no zero points, rows up to 64 * 6 chunks):
-//     one wave per U rows, every load of the wave issued at kernel start, so a launch
+//   * gemv_burst (M in {1, 2, 4, 8}, no zero points, rows up to 64 * 6 chunks):
+//     one wave per U rows (long rows at M = 1: two waves per U rows, each
+//     taking half of every row's chunks), every load of the wave issued at
+//     kernel start, so a launch
 //     puts the whole matrix's reads in flight at once and pays HBM latency
 //     about once -- the decode shapes are only 2-70 MB, a few microseconds
 //     of HBM time, so latency and ramp dominate otherwise;
@@ -452,8 +454,11 @@ __device__ __forceinline__ void lds_barrier() {
 // the block (wave w takes row group w % (WV / 2) and chunk iterations
 // I (w / (WV / 2)) .. I (w / (WV / 2)) + I - 1), and the upper part's wave
 // totals are added to the lower part's through LDS, lower + upper, in the
-// same launch.  Long rows then keep more waves per CU busy on the same
-// rows: a block stages all of x once whatever its K split.
+// same launch.  A long row then takes half its chunk iterations in each of
+// two waves of four rows, instead of all of them in one wave of two rows:
+// every x chunk a wave reads from LDS serves four rows, and an INT4 row
+// quad's four scales come in one load.  A block stages all of x once
+// whatever its K split.
 template <int PREC, int M, int U, int I, int PRO, int EPI, int NG, int WV = 4, int KS = 1>
 __global__ __launch_bounds__(64 * WV) void gemv_burst(const KParams p) {
     constexpr int CE = PREC == 8 ? 16 : 32;
