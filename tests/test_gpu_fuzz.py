@@ -64,9 +64,46 @@ def backend():
 
 @pytest.mark.parametrize("seed", SEEDS)
 def test_random_case(backend, seed):
+    _run_case(backend, *_case(seed), seed)
+
+
+# Long rows over many output rows, which the draw above never reaches: one
+# or two x rows, INT8 K in (3072, 6144] or INT4 K in (6144, 12288], 4096 to
+# 9000 output rows -- the shapes on which the burst GEMV splits every row
+# between two waves of its block at one x row.
+LONG_KINDS = ["int8", "int8_sym", "int4_nk_g32", "int4_nk_g64", "int4_nk_g128", "int4_kn_g32", "int4_kn_g64"]
+
+
+def _long_case(seed):
+    r = np.random.RandomState(seed)
+    kind = LONG_KINDS[r.randint(len(LONG_KINDS))]
+    gs = int(kind.split("_g")[1]) if "_g" in kind else 0
+    if kind.startswith("int8"):
+        K = 8 * r.randint(3072 // 8 + 1, 6144 // 8 + 1)
+    else:
+        step = gs if kind.startswith("int4_nk") else 8
+        K = step * r.randint(6144 // step + 1, 12288 // step + 1)
+    step = gs if kind.startswith("int4_kn") else 1
+    N = step * r.randint(4096 // step, 9000 // step + 1)
+    M = (1, 1, 1, 2)[r.randint(4)]
+    return kind, int(K), int(N), int(M)
+
+
+# TBH_FUZZ_LONG_SEEDS=first:count runs another range of seeds
+_long_range = os.environ.get("TBH_FUZZ_LONG_SEEDS")
+LONG_SEEDS = (list(range(int(_long_range.split(":")[0]),
+                         int(_long_range.split(":")[0]) + int(_long_range.split(":")[1])))
+              if _long_range else list(range(0x1F0, 0x1F0 + 12)))
+
+
+@pytest.mark.parametrize("seed", LONG_SEEDS)
+def test_random_long_rows(backend, seed):
+    _run_case(backend, *_long_case(seed), seed)
+
+
+def _run_case(backend, kind, K, N, M, seed):
     import torch
 
-    kind, K, N, M = _case(seed)
     qt, pq = _weight(kind, K, N, seed=seed)
     W = _oracle_weight(qt, pq.layout)
     deq = backend.dequantize(pq)
