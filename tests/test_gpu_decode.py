@@ -202,7 +202,8 @@ def test_decode_7b_width(backend):
 
 @pytest.mark.parametrize("heads", [(4, 2), (16, 2), (8, 8)])
 def test_decode_long_context(backend, heads):
-    # more than two 64-position attention ranges, so the step's attention
+    # more than two attention ranges (32 positions at head_dim 64 for 4/2,
+    # 64 at head_dim 16 and 32 for 16/2 and 8/8), so the step's attention
     # combines several range partials (and, for 4/2, a quad with idle waves)
     nh, nkv = heads
     cfg = T.DecoderConfig(**dict(SMALL, num_heads=nh, num_kv_heads=nkv, max_seq=160))
