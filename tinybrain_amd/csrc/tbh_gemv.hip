@@ -1021,6 +1021,23 @@ bool burst_shape(const tbh_weight &w, const KParams &p, int M, int *I_out, int *
         // everywhere)
         if (4 * I <= 16 && w.Np / 4 >= 8 * cus) U = 4;
         else if (2 * I <= 16) U = 2;
+        // ... and four (at most 8 chunks per lane) where that brings the
+        // launch to at most one four-wave block per CU: one round of blocks
+        // beat two or a partial second (us per launch, U = 2 / 4, graphs of
+        // one shape: INT4 4096x2048 3.36 / 3.05, INT8 2560x2048 3.07 / 2.96
+        // -- the 1.1B decode step's Q|K|V, 1828 -> 1850 tokens/s on one box).
+        // Eight rows per wave also reached one round on INT4 5632x2048 and
+        // 8192x2048 and read faster alone (3.80 -> 3.66, 4.17 -> 4.00 us), but
+        // in the four-shape step 5632x2048 went 3.65-3.67 -> 3.76-3.79 us, so
+        // the rule stops at four.
+        if (!ng) {
+            for (int u = U; u <= 4 && u * I <= 8; u *= 2) {
+                if ((w.Np + 4 * u - 1) / (4 * u) <= cus) {
+                    U = u;
+                    break;
+                }
+            }
+        }
     } else {
         // two or four x rows: at least two rows per wave (the block stages its
         // x rows once for 4 U weight rows; us per launch, U = 1 / 2, M = 2
