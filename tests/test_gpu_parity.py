@@ -845,6 +845,62 @@ def test_prefill_bf16(backend, prec, K, N, M):
     _prefill_check(backend, pq, oq, M, seed=5 + M)
 
 
+# Tile counts that fill whole rounds of resident blocks and leave at most
+# half a tile's time for a last round once its tiles are split along K: the
+# leftover tiles' parts are summed by a second launch (INT8 128 x 128 blocks:
+# two per CU, 512 at once; INT4: one per CU, 256).  Ragged N puts split tiles
+# on the output's edge.  INT8 M = 2048 (704 tiles, 192 left) stays unsplit:
+# its 192 tiles already have a CU each.
+@pytest.mark.parametrize("prec,K,N,M", [
+    ("int8", 2048, 5632, 1536),   # 528 tiles: 16 left, 8 parts
+    ("int8", 2048, 5000, 2048),   # 640 tiles: 128 left, 2 parts, the last N tile ragged
+    ("int8", 1000, 5632, 3072),   # 1056 tiles: 32 left; K of 16 steps, 8 parts of 2
+    ("int4", 5632, 2048, 3072),   # 384 tiles: 128 left after one round of 256, 2 parts
+    ("int8", 2048, 5632, 2048),   # unsplit
+])
+def test_prefill_split_tail(backend, prec, K, N, M):
+    if prec == "int8":
+        oq = _int8_pc(71 + K + M, K, N)
+        pq = _product(oq, (K, N))
+    else:
+        oq = _int4_nk(73 + K + M, K, N, 32)
+        pq = _product(oq, (K, N), T.Layout.NK_FLAT)
+    _prefill_check(backend, pq, oq, M, seed=9 + M)
+
+
+def test_prefill_split_tail_graph(backend):
+    # the split tail's GEMM and sum captured in a HIP graph: every replay (with
+    # eager work on the same stream between them) equals the eager call bit
+    # for bit
+    import torch
+
+    K, N, M = 2048, 5632, 1536
+    oq = _int8_pc(201, K, N)
+    pq = _product(oq, (K, N))
+    w = backend.weight(pq)
+    x = torch.from_numpy(O.fill_normal(202, M * K).reshape(M, K)).to(torch.bfloat16).cuda()
+    s = torch.cuda.Stream()
+    y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    other = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        backend.matmul_bf16_device(x, w, out=y, stream=s)
+    torch.cuda.synchronize()
+    eager = y.cpu().numpy().copy()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        backend.matmul_bf16_device(x, w, out=y, stream=s)
+    for i in range(3):
+        y.zero_()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            g.replay()
+            backend.matmul_bf16_device(x[: M // 2], w, out=other[: M // 2], stream=s)   # eager, same stream
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(y.cpu().numpy(), eager, err_msg=f"replay {i}")
+    del g
+
+
 def _prefill_tile(prec, N, M, cus=256):
     """The launch rule of tbh_prefill.hip (launch_prec), restated to show
     which tile family and wave count each case below reaches."""

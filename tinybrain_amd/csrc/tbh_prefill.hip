@@ -65,6 +65,15 @@ struct PParams {
     int32_t cpg;     // chunks per K-group
     int32_t rpn;     // runtime-layout INT4: rows per N-block (scales: [nbk][chunks * 32])
     int32_t nbk;     // runtime-layout INT4: N-blocks
+    // Split tail (bf16 x, K-group weights; tail_first >= 0): a one-dimensional
+    // grid whose blocks [0, tail_first) take tile b over the whole K, and
+    // whose remaining blocks take tile tail_first + q / tail_parts over K
+    // steps [r tail_steps, (r + 1) tail_steps), r = q % tail_parts, writing
+    // that part's tile to tail_part[r][q / tail_parts][BM][BN].  Tiles are
+    // numbered N-tile first (tiles_n per row of tiles), as the 3-D grid
+    // dispatches them.
+    int32_t tail_first, tail_parts, tail_steps, tail_n, tiles_n;
+    float *tail_part;
 };
 
 __device__ __forceinline__ void lds_barrier() {
@@ -153,12 +162,29 @@ void gemm_bf16(const PParams p) {
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int wm = wave / WC, wn = wave % WC;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    int tn = blockIdx.x, tm = blockIdx.y, kpart = blockIdx.z, tr = -1;   // tr: tail tile
+    if constexpr (XF == 0) {
+        if (p.tail_first >= 0) {
+            const int bid = blockIdx.x;
+            int tile = bid;
+            kpart = 0;
+            if (bid >= p.tail_first) {
+                const int q = bid - p.tail_first;
+                tr = q / p.tail_parts;
+                kpart = q % p.tail_parts;
+                tile = p.tail_first + tr;
+            }
+            tn = tile % p.tiles_n;
+            tm = tile / p.tiles_n;
+        }
+    }
+    const int m0 = tm * BM, n0 = tn * BN;
     const int nsteps = (p.chunks * CE + BK - 1) / BK;
     // This block's K steps [t_begin, t_end); x past kend reads as zero, so
     // the padded steps at a split's end add nothing.
-    const int t_begin = blockIdx.z * p.split_steps;
-    const int t_end = min(nsteps, t_begin + p.split_steps);
+    const int sps = tr >= 0 ? p.tail_steps : p.split_steps;
+    const int t_begin = kpart * sps;
+    const int t_end = min(nsteps, t_begin + sps);
     const int kend = min(p.K, t_end * BK);
 
     // INT8 row scales of this lane's output columns, loaded before the K loop;
@@ -483,6 +509,19 @@ void gemm_bf16(const PParams p) {
         }
         return;
     }
+    if (tr >= 0) {
+        // a split-tail part: the whole tile into its slot of tail_part (the
+        // sum reads the elements inside the output)
+        float *tp = p.tail_part + (int64_t)(kpart * p.tail_n + tr) * (BM * BN);
+#pragma unroll
+        for (int b = 0; b < TN; ++b)
+#pragma unroll
+            for (int a = 0; a < TM; ++a)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    tp[(mrow - m0 + a * 16 + e) * BN + ncol - n0 + b * 16] = acc[a][b][e] * scn[b];
+        return;
+    }
     if (m0 + BM <= p.M && n0 + BN <= p.N) {
         // whole tile in range: no per-element branches
 #pragma unroll
@@ -552,8 +591,114 @@ __global__ __launch_bounds__(256) void split_sum(const float *__restrict__ part,
     }
 }
 
+// The split tail's sums: element e of tail tile r (four at a time) =
+// tail_part[0][r][e] + tail_part[1][r][e] + ..., in part order, written to
+// y where the tile lies inside the output.
+template <int BM, int BN>
+__global__ __launch_bounds__(256) void tail_sum(const PParams p, float *y, int64_t ldy, int vec) {
+    constexpr int Q = BM * BN / 4;   // float4 per tile
+    const int64_t total = (int64_t)p.tail_n * Q;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+        const int r = (int)(i / Q), e = 4 * (int)(i % Q);
+        const int tile = p.tail_first + r;
+        const int m = (tile / p.tiles_n) * BM + e / BN, n = (tile % p.tiles_n) * BN + e % BN;
+        if (m >= p.M || n >= p.N) continue;
+        float4 acc = float4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < p.tail_parts; ++j) {
+            const float4 v = *(const float4 *)(p.tail_part + (int64_t)(j * p.tail_n + r) * (BM * BN) + e);
+            acc.x += v.x;
+            acc.y += v.y;
+            acc.z += v.z;
+            acc.w += v.w;
+        }
+        float *o = y + (int64_t)m * ldy + n;
+        if (vec && n + 3 < p.N) {
+            *(float4 *)o = acc;
+        } else {
+            const float a[4] = {acc.x, acc.y, acc.z, acc.w};
+            for (int q = 0; q < 4 && n + q < p.N; ++q) o[q] = a[q];
+        }
+    }
+}
+
+// What a launch without a K split needs to split its tail: the K steps, the
+// CU count and the workspace.
+struct TailReq {
+    int nsteps;
+    int64_t cus;
+    const Scratch *scr;
+};
+
+// Launches kern over `grid` (no K split).  With a TailReq: when the tiles
+// fill r >= 1 whole rounds of the blocks the GPU holds at once (the
+// occupancy of kern) and leave at most one tile per CU for a last round,
+// the leftover tiles are split along K into parts (2..8, as below), so the
+// last round takes a fraction of a tile's time instead of a whole one;
+// tail_sum then adds the parts.  Bits differ from the unsplit launch only in
+// those tiles' summation order, and a given shape always takes the same
+// form.
+template <int BM, int BN, typename Kern>
+hipError_t launch_tail(Kern kern, int threads, dim3 grid, PParams p, const TailReq *tq, hipStream_t s) {
+    p.tail_first = -1;
+    if (tq != nullptr && grid.z == 1) {
+        int occ = 0;
+        static const bool off = [] {   // TBH_PREFILL_TAIL=0: no split tail
+            const char *v = std::getenv("TBH_PREFILL_TAIL");
+            return v && *v == '0';
+        }();
+        if (!off && hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, threads, 0) == hipSuccess && occ > 0) {
+            const int64_t S = (int64_t)occ * tq->cus, T = (int64_t)grid.x * grid.y, R = T % S;
+            // The last round's R tiles take one tile's time on their own CUs;
+            // split P ways they take ceil(R P / CUs) / P of it (blocks sharing
+            // a CU run side by side).  Take the best P of 2..8 when that is at
+            // most half a tile's time.
+            int parts = 0, steps = 0;
+            if (T > S && R > 0 && R <= tq->cus) {
+                double best = 0.5;
+                for (int P = 2; P <= 8; ++P) {
+                    int st = (tq->nsteps + P - 1) / P;
+                    st = (st + kDepth - 1) / kDepth * kDepth;
+                    const int Pr = (tq->nsteps + st - 1) / st;   // parts after rounding the steps
+                    if (Pr < 2) continue;
+                    const double t = (double)((R * Pr + tq->cus - 1) / tq->cus) / Pr;
+                    if (t <= best && (parts == 0 || t < best)) {
+                        best = t;
+                        parts = Pr;
+                        steps = st;
+                    }
+                }
+            }
+            if (parts >= 2) {
+                const size_t bytes = (size_t)parts * (size_t)R * BM * BN * sizeof(float);
+                const bool room = !tq->scr->is_fixed() || bytes <= tq->scr->fixed_bytes;
+                float *tp = parts >= 2 && room ? (float *)tq->scr->get(s, bytes) : nullptr;
+                if (tp != nullptr) {
+                    p.tail_first = (int32_t)(T - R);
+                    p.tail_parts = parts;
+                    p.tail_steps = steps;
+                    p.tail_n = (int32_t)R;
+                    p.tiles_n = (int32_t)grid.x;
+                    p.tail_part = tp;
+                    p.split_steps = tq->nsteps;
+                    void *args[] = {&p};
+                    hipError_t e = hipLaunchKernel((const void *)kern, dim3((unsigned)(T - R + R * parts)),
+                                                   dim3(threads), args, 0, s);
+                    if (e != hipSuccess) return e;
+                    const int64_t n4 = R * (BM * BN / 4);
+                    const int vec = p.ldy % 4 == 0 && ((uintptr_t)p.y & 15) == 0;
+                    hipLaunchKernelGGL((tail_sum<BM, BN>), dim3((unsigned)std::min<int64_t>(4 * tq->cus, (n4 + 255) / 256)),
+                                       dim3(256), 0, s, p, p.y, p.ldy, vec);
+                    return hipGetLastError();
+                }
+            }
+        }
+    }
+    void *args[] = {&p};
+    return hipLaunchKernel((const void *)kern, grid, dim3(threads), args, 0, s);
+}
+
 template <int PREC, int BM, int BN, int BK, int NC>
-hipError_t launch_tile(const PParams &p, int splits, hipStream_t s) {
+hipError_t launch_tile(const PParams &p, int splits, hipStream_t s, const TailReq *tq = nullptr) {
     static const int waves = [] {   // 4 or 8 forces the waves per block
         const char *v = std::getenv("TBH_PREFILL_WAVES");
         return v && *v ? std::atoi(v) : 0;
@@ -574,11 +719,11 @@ hipError_t launch_tile(const PParams &p, int splits, hipStream_t s) {
                 else hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, false, 4, BK, 1, 0>), grid, dim3(256), 0, s, p);
             }
         } else if (p.zp) {
-            if (w8) hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, true, 8, BK, 0, 0>), grid, dim3(512), 0, s, p);
-            else hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, true, 4, BK, 0, 0>), grid, dim3(256), 0, s, p);
+            if (w8) return launch_tail<BM, BN>(gemm_bf16<PREC, BM, BN, true, 8, BK, 0, 0>, 512, grid, p, tq, s);
+            return launch_tail<BM, BN>(gemm_bf16<PREC, BM, BN, true, 4, BK, 0, 0>, 256, grid, p, tq, s);
         } else {
-            if (w8) hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, false, 8, BK, 0, 0>), grid, dim3(512), 0, s, p);
-            else hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, false, 4, BK, 0, 0>), grid, dim3(256), 0, s, p);
+            if (w8) return launch_tail<BM, BN>(gemm_bf16<PREC, BM, BN, false, 8, BK, 0, 0>, 512, grid, p, tq, s);
+            return launch_tail<BM, BN>(gemm_bf16<PREC, BM, BN, false, 4, BK, 0, 0>, 256, grid, p, tq, s);
         }
     }
     return hipGetLastError();
@@ -627,7 +772,8 @@ hipError_t launch_split(const tbh_weight &w, PParams p, int64_t tiles, int bpc, 
         p.y = part;
         p.split_stride = n;
     }
-    hipError_t e = launch_tile<PREC, BM, BN, BK, NC>(p, splits, s);
+    const TailReq tq{nsteps, cus, &scr};
+    hipError_t e = launch_tile<PREC, BM, BN, BK, NC>(p, splits, s, splits == 1 ? &tq : nullptr);
     if (e != hipSuccess || splits == 1) return e;
     const int64_t grid_cap = 4 * cus;
     if (n % 4 == 0 && ((uintptr_t)y & 15) == 0) {
@@ -747,6 +893,7 @@ bool prefill_supported(const tbh_weight &w) {
 
 static PParams prefill_params(const tbh_weight &w, int64_t ldx, float *y, int64_t ldy) {
     PParams p{};
+    p.tail_first = -1;   // the three-dimensional grid unless launch_tail splits a tail
     p.ldx = ldx;
     p.y = y;
     p.ldy = ldy;
