@@ -27,6 +27,9 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <map>
+#include <mutex>
+#include <tuple>
 #include <type_traits>
 
 namespace tbh {
@@ -621,6 +624,24 @@ __global__ __launch_bounds__(256) void tail_sum(const PParams p, float *y, int64
     }
 }
 
+// Blocks of `kern` (launched with `threads` threads) one CU holds at once on
+// the current device, from the runtime's occupancy calculation, asked once
+// per kernel, block size and device (0 when the query fails).
+static int blocks_per_cu_of(const void *kern, hipError_t (*query)(int *, const void *, int), int threads) {
+    static std::mutex mu;
+    static std::map<std::tuple<const void *, int, int>, int> seen;
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    const auto key = std::make_tuple(kern, threads, dev);
+    std::lock_guard<std::mutex> lock(mu);
+    const auto it = seen.find(key);
+    if (it != seen.end()) return it->second;
+    int occ = 0;
+    if (query(&occ, kern, threads) != hipSuccess) occ = 0;
+    seen.emplace(key, occ);
+    return occ;
+}
+
 // What a launch without a K split needs to split its tail: the K steps, the
 // CU count and the workspace.
 struct TailReq {
@@ -641,12 +662,14 @@ template <int BM, int BN, typename Kern>
 hipError_t launch_tail(Kern kern, int threads, dim3 grid, PParams p, const TailReq *tq, hipStream_t s) {
     p.tail_first = -1;
     if (tq != nullptr && grid.z == 1) {
-        int occ = 0;
         static const bool off = [] {   // TBH_PREFILL_TAIL=0: no split tail
             const char *v = std::getenv("TBH_PREFILL_TAIL");
             return v && *v == '0';
         }();
-        if (!off && hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, threads, 0) == hipSuccess && occ > 0) {
+        const int occ = off ? 0 : blocks_per_cu_of((const void *)kern, [](int *n, const void *k, int t) {
+            return hipOccupancyMaxActiveBlocksPerMultiprocessor(n, k, t, 0);
+        }, threads);
+        if (occ > 0) {
             const int64_t S = (int64_t)occ * tq->cus, T = (int64_t)grid.x * grid.y, R = T % S;
             // The last round's R tiles take one tile's time on their own CUs;
             // split P ways they take ceil(R P / CUs) / P of it (blocks sharing
@@ -671,7 +694,7 @@ hipError_t launch_tail(Kern kern, int threads, dim3 grid, PParams p, const TailR
             if (parts >= 2) {
                 const size_t bytes = (size_t)parts * (size_t)R * BM * BN * sizeof(float);
                 const bool room = !tq->scr->is_fixed() || bytes <= tq->scr->fixed_bytes;
-                float *tp = parts >= 2 && room ? (float *)tq->scr->get(s, bytes) : nullptr;
+                float *tp = room ? (float *)tq->scr->get(s, bytes) : nullptr;
                 if (tp != nullptr) {
                     p.tail_first = (int32_t)(T - R);
                     p.tail_parts = parts;
