@@ -101,6 +101,34 @@ def test_random_long_rows(backend, seed):
     _run_case(backend, *_long_case(seed), seed)
 
 
+# Large prefill batches over many output rows, which neither draw above
+# reaches: M 1024..3072, 4096..9000 output rows, K up to 1536 (so the float64
+# products stay quick) -- grids of one or more whole rounds of resident
+# blocks, whose leftover tiles the prefill GEMM may split along K.
+LARGE_KINDS = ["int8", "int8_zp", "int4_nk_g32", "int4_nk_g64", "int4_nk_g128"]
+
+
+def _large_case(seed):
+    r = np.random.RandomState(seed)
+    kind = LARGE_KINDS[r.randint(len(LARGE_KINDS))]
+    gs = int(kind.split("_g")[1]) if "_g" in kind else 8
+    K = gs * r.randint(max(1, 256 // gs), 1536 // gs + 1)
+    N = r.randint(4096, 9001)
+    M = 8 * r.randint(1024 // 8, 3072 // 8 + 1)
+    return kind, int(K), int(N), int(M)
+
+
+_large_range = os.environ.get("TBH_FUZZ_LARGE_SEEDS")
+LARGE_SEEDS = (list(range(int(_large_range.split(":")[0]),
+                          int(_large_range.split(":")[0]) + int(_large_range.split(":")[1])))
+               if _large_range else list(range(0x2F0, 0x2F0 + 8)))
+
+
+@pytest.mark.parametrize("seed", LARGE_SEEDS)
+def test_random_large_prefill(backend, seed):
+    _run_case(backend, *_large_case(seed), seed)
+
+
 def _run_case(backend, kind, K, N, M, seed):
     import torch
 
