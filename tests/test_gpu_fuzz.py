@@ -129,6 +129,33 @@ def test_random_large_prefill(backend, seed):
     _run_case(backend, *_large_case(seed), seed)
 
 
+# Runtime-layout INT4 (groups along N) at 65..600 rows of x, where the bf16
+# entry's GEMM takes x as two f16 pieces scaled per x row and per N-block:
+# group sizes that give one, two or four N-blocks per 64-output tile or a
+# group spanning rows of k, ragged K, M and N.
+NG_KINDS = ["int4_kn_g16", "int4_kn_g32", "int4_kn_g64", "int4_kn_g128", "int4_kn_g48"]
+
+
+def _ng_case(seed):
+    r = np.random.RandomState(seed)
+    kind = NG_KINDS[r.randint(len(NG_KINDS))]
+    gs = int(kind.split("_g")[1])
+    K = 8 * r.randint(1, 2048 // 8 + 1)
+    N = gs * r.randint(1, 3000 // gs + 1) if r.rand() < 0.8 else r.randint(1, 3000)
+    M = r.randint(65, 601)
+    return kind, int(K), int(N), int(M)
+
+
+_ng_range = os.environ.get("TBH_FUZZ_NG_SEEDS")
+NG_SEEDS = (list(range(int(_ng_range.split(":")[0]), int(_ng_range.split(":")[0]) + int(_ng_range.split(":")[1])))
+            if _ng_range else list(range(0x3F0, 0x3F0 + 12)))
+
+
+@pytest.mark.parametrize("seed", NG_SEEDS)
+def test_random_runtime_prefill(backend, seed):
+    _run_case(backend, *_ng_case(seed), seed)
+
+
 def _run_case(backend, kind, K, N, M, seed):
     import torch
 

@@ -1036,6 +1036,67 @@ def test_prefill_bf16_runtime_layout(backend, K, N, gs, M):
     _prefill_check(backend, pq, qk, M, seed=37 + M)
 
 
+@pytest.mark.parametrize("M", [64, 65, 96])
+def test_prefill_bf16_runtime_layout_block_ranges(backend, M):
+    # past 64 rows the runtime-layout GEMM scales fl(x * s) by a power of two
+    # per x row and per N-block before splitting it into two f16 pieces:
+    # N-blocks whose scales differ by 2^40, rows that differ by 2^30, each
+    # N-block checked on its own (M = 64 takes the three bf16 pieces)
+    import torch
+
+    K, N, gs = 1024, 256, 32
+    src = O.fill_normal(0x5CA1 + M, K * N, std=0.02).reshape(K, N)
+    for b in range(N // gs):
+        src[:, b * gs:(b + 1) * gs] *= np.float32(2.0 ** (20 * ((b % 3) - 1)))
+    qk = O.quantize_int4(src, gs)
+    pq = _product(qk, (K, N))
+    W = _oracle_weight(qk, pq.layout)
+    x = O.fill_normal(0x5CA2 + M, M * K).reshape(M, K)
+    x *= (np.float32(2.0) ** ((np.arange(M) % 3 - 1) * 15).astype(np.float32))[:, None]
+    xb = torch.from_numpy(x).to(torch.bfloat16)
+    y = backend.matmul_bf16_device(xb.cuda(), backend.weight(pq))
+    torch.cuda.synchronize()
+    y = y.cpu().numpy()
+    y64 = O.gemm_f64(xb.float().numpy(), W)
+    for r in range(3):
+        for b in range(N // gs):
+            cols = slice(b * gs, (b + 1) * gs)
+            err = O.parity_errors(y[r::3, cols], y64[r::3, cols])
+            assert err["gated"] <= GATE, (M, r, b, err)
+
+
+@pytest.mark.parametrize("M", [64, 80])
+def test_prefill_bf16_runtime_layout_nonfinite(backend, M):
+    # infinities and NaNs in x reach the outputs as the float64 product of
+    # the same dequantized weights gives them (inf * 0 = NaN, inf - inf =
+    # NaN), and leave the other rows' scaling alone
+    import torch
+
+    K, N, gs = 512, 256, 32
+    qk = _int4_kn(0xF1 + M, K, N, gs)
+    pq = _product(qk, (K, N))
+    W = _oracle_weight(qk, pq.layout)
+    x = O.fill_normal(0xF2 + M, M * K).reshape(M, K)
+    x[0, 5] = np.inf
+    x[1, 100] = -np.inf
+    x[2, 7] = np.nan
+    x[3, 3], x[3, 9] = np.inf, -np.inf
+    x[4, 11] = np.inf
+    x[4, 200] = 3.0e38                      # a finite huge value beside the infinity
+    xb = torch.from_numpy(x).to(torch.bfloat16)
+    y = backend.matmul_bf16_device(xb.cuda(), backend.weight(pq))
+    torch.cuda.synchronize()
+    y = y.cpu().numpy()
+    with np.errstate(invalid="ignore", over="ignore"):
+        y64 = O.gemm_f64(xb.float().numpy(), W)
+    for m in range(5):
+        np.testing.assert_array_equal(np.isnan(y[m]), np.isnan(y64[m]), err_msg=str(m))
+        np.testing.assert_array_equal(np.isposinf(y[m]), np.isposinf(y64[m]) | (np.isfinite(y64[m]) & (y64[m] > 3.4e38)), err_msg=str(m))
+        np.testing.assert_array_equal(np.isneginf(y[m]), np.isneginf(y64[m]) | (np.isfinite(y64[m]) & (y64[m] < -3.4e38)), err_msg=str(m))
+    err = O.parity_errors(y[5:], y64[5:])
+    assert err["gated"] <= GATE, (M, err)
+
+
 @pytest.mark.parametrize("kind,K,N,M", [
     ("int8", 2048, 1024, 64),      # split along K
     ("int8", 2048, 5632, 512),     # one block per tile, no split

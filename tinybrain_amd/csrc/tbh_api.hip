@@ -2,6 +2,7 @@
 // matmul dispatch.  Kernels live in tbh_gemv.hip and tbh_ref_kernels.hip.
 #include <algorithm>
 #include <chrono>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -424,7 +425,7 @@ hipError_t upload(T **dst, const T *src, size_t count, int64_t &bytes, int64_t &
 void free_weight(tbh_weight *w) {
     if (!w) return;
     for (void *p : {(void *)w->data, (void *)w->scales, (void *)w->zp, (void *)w->raw, (void *)w->raw_scales,
-                    (void *)w->raw_zp})
+                    (void *)w->raw_zp, (void *)w->ng_sexp})
         (void)hipFree(p);
     delete w;
 }
@@ -580,6 +581,20 @@ tbh_status tbh_weight_create(tbh_device *dev, const tbh_qtensor_desc *desc, tbh_
                     for (int64_t k = 0; k < K; ++k) t[nb * w->Kp + k] = d.scales[group_of(k, n)];
                 }
                 if (e == hipSuccess) e = upload(&w->scales, t.data(), t.size(), w->device_bytes, w->n_scales_dev);
+                // per N-block e with |s| < 2^e for its finite scales, for the
+                // prefill GEMM's f16 scaling of x * s
+                std::vector<int32_t> ex((size_t)NB, 0);
+                for (int64_t nb = 0; nb < NB; ++nb) {
+                    float mx = 0.0f;
+                    for (int64_t k = 0; k < K; ++k) {
+                        const float a = std::fabs(t[nb * w->Kp + k]);
+                        if (std::isfinite(a)) mx = std::max(mx, a);
+                    }
+                    int e2 = 0;
+                    if (mx > 0.0f) (void)std::frexp(mx, &e2);
+                    ex[(size_t)nb] = e2;
+                }
+                if (e == hipSuccess) e = upload(&w->ng_sexp, ex.data(), ex.size(), w->device_bytes, w->n_ng_sexp);
                 w->stream_bytes = (count + 1) / 2 + 4 * d.n_scales;
             }
         } else {
@@ -728,7 +743,7 @@ bool weight_arrays_ok(const tbh_weight &w) {
         if (w.rows_per_nblock <= 0 || w.zp) return false;
         if (w.ng_pairs) return w.nb_half > 0 && w.n_scales_dev == 2 * (int64_t)w.nb_half * w.Kp;
         const int64_t nb = (w.Np + w.rows_per_nblock - 1) / w.rows_per_nblock;
-        return w.n_scales_dev == nb * w.Kp;
+        return w.n_scales_dev == nb * w.Kp && w.ng_sexp && w.n_ng_sexp == nb;
     }
     return false;
 }

@@ -108,6 +108,10 @@ struct tbh_weight {
     // scales are both weights' tables stacked, nb_half N-blocks each.
     bool ng_pairs = false;
     int32_t nb_half = 0;
+    // Int4NGroup (not pairs): per N-block e with |scale| < 2^e for its finite
+    // scales (0 when all are zero), for the prefill GEMM's f16 scaling
+    int32_t *ng_sexp = nullptr;
+    int64_t n_ng_sexp = 0;
     bool mfma_tiles = false;     // data in 1 KiB MFMA tiles (else K-contiguous rows)
 
     // generic path: the reference arrays as given
@@ -230,6 +234,9 @@ struct Scratch {
     void *fixed = nullptr;
     size_t fixed_bytes = 0;
     mutable size_t shortfall = 0;   // bytes a fixed buffer could not provide
+    // bytes at the start of the buffer that a caller keeps for itself (a
+    // multiple of 256): get() hands out memory after them
+    size_t offset = 0;
 
     bool is_fixed() const { return fixed != nullptr; }
     // nullptr when the bytes are not available: a fixed buffer too small
@@ -238,11 +245,12 @@ struct Scratch {
     // the launcher then takes a path without scratch).
     void *get(hipStream_t s, size_t bytes) const {
         if (fixed) {
-            if (bytes <= fixed_bytes) return fixed;
-            shortfall = bytes;
+            if (offset + bytes <= fixed_bytes) return (char *)fixed + offset;
+            shortfall = offset + bytes;
             return nullptr;
         }
-        return stream_workspace(dev, s, bytes);
+        void *b = stream_workspace(dev, s, offset + bytes);
+        return b ? (char *)b + offset : nullptr;
     }
 };
 

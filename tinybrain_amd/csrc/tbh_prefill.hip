@@ -38,6 +38,9 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kBK = 64;           // K per staged step (two MFMA K-steps of 32) unless a launch takes 128
 // bf16 of padding per LDS row (32 bytes): rows of 160 (K steps of 64) or 288
@@ -77,6 +80,10 @@ struct PParams {
     // dispatches them.
     int32_t tail_first, tail_parts, tail_steps, tail_n, tiles_n;
     float *tail_part;
+    // XF = 3: per x row e with max_k |x| < 2^e, and the weight's per N-block
+    // e with max_k |s| < 2^e
+    const int32_t *row_exp;
+    const int32_t *nb_exp;
 };
 
 __device__ __forceinline__ void lds_barrier() {
@@ -90,6 +97,11 @@ __device__ __forceinline__ void lds_barrier() {
 __device__ __forceinline__ uint32_t pack_hi16(float lo_elem, float hi_elem) {
     return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, hi_elem),
                                  __builtin_bit_cast(uint32_t, lo_elem), 0x07060302u);
+}
+
+// Two fp32 values -> one dword of two f16 (round to nearest even).
+__device__ __forceinline__ uint32_t pack_f16(float lo_elem, float hi_elem) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo_elem, hi_elem}, f16x2));
 }
 
 // A 32-bit word as fp32.  By value: __builtin_bit_cast applied directly to
@@ -119,6 +131,15 @@ __device__ __forceinline__ float sbyte(uint32_t w) {
 // piece 3 is zero), so the four rows a lane holds in each 16 x 16
 // accumulator tile are the pieces of one x row, and the epilogue adds them
 // into that row's output.  XF = 2: the same from bf16 x (widened exactly).
+// XF = 3 (bf16 x, runtime-layout scales): two product rows per x row, on
+// the f16 MFMA.  v = fl(x * s) is scaled exactly by 2^(15 - er - eb) (er, eb:
+// the x row's and the N-block's bounds over their finite values, |x| < 2^er,
+// |s| < 2^eb, so a finite |v'| <= 2^15) and split into f16 pieces hi =
+// f16(v'), lo = f16(v' - hi) (v' - hi is exact in fp32; 0 for a non-finite
+// v', which stays in hi): row r = piece r % 2 of x row r / 2, and 16 q is
+// exact in f16.  The pieces hold v' to 2^-22 of itself, or to 2^-25 absolute
+// below the f16 normal range; the epilogue adds the two rows and scales
+// back by 2^-(15 - er - eb).  Half the MFMAs and staged rows of XF = 2.
 //
 // NC > 0: INT4 in the runtime layout (groups along N: one scale per
 // (N-block of rpn rows, k)).  The scale varies along K inside an MFMA, so it
@@ -139,7 +160,8 @@ template <int PREC, int BM, int BN, bool ZP, int WV, int BK, int XF, int NC>
 __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(kFourWavesPerSimd<PREC, BM, BN, WV, BK, NC> ? 4 : 1)))
 void gemm_bf16(const PParams p) {
     static_assert(NC == 0 || (PREC == 4 && XF != 0 && !ZP), "runtime-layout INT4 stages split x, no zero points");
-    static_assert(XF != 2 || NC > 0, "bf16 x is split only for runtime-layout scales");
+    static_assert(XF < 2 || NC > 0, "bf16 x is split only for runtime-layout scales");
+    constexpr int XP = XF == 3 ? 2 : 4;                     // product rows per x row (split x)
     constexpr int NCC = NC > 0 ? NC : 1;                    // copies of x in LDS
     // Steps wholly inside K and the N tile run an unmasked loop form, except
     // in INT4 blocks with K steps of 128 (256 VGPRs), which run every step
@@ -200,15 +222,28 @@ void gemm_bf16(const PParams p) {
     // ---- global -> registers for one step, into register stage d of kDepth:
     // the loads of steps t+1 .. t+kDepth-1 are in flight while step t runs
     // split x: a segment is 8 elements of one x row (two 16-byte loads of
-    // fp32, one of bf16), staged as the four product rows of its pieces; with
+    // fp32, one of bf16), staged as the XP product rows of its pieces; with
     // runtime-layout scales an item is a (segment, copy) pair and also loads
     // the copy's 8 scales
-    constexpr int XSEGF = (BM / 4) * (BK / 8);
+    constexpr int XSEGF = (BM / XP) * (BK / 8);
     constexpr int XPTF = XF ? (XSEGF * NCC + NT - 1) / NT : 1;
     constexpr int XPTL = XF ? XPTF : XPT;
     u32x4 xr[kDepth][XPTL][XF == 1 ? 2 : 1];
     u32x4 xsc[kDepth][NC > 0 ? XPTL : 1][2];
     bool xin[kDepth][XPTL];   // segment within K, applied at the LDS store
+    // XF = 3: each item's scaling exponent 15 - er - eb (its x row and copy
+    // are the same in every step)
+    int xsh[XF == 3 ? XPTL : 1];
+    if constexpr (XF == 3) {
+#pragma unroll
+        for (int j = 0; j < XPTF; ++j) {
+            const int i = min(tid + NT * j, XSEGF * NCC - 1);
+            const int s = NCC == 1 ? i : i % XSEGF;
+            const int m = min(m0 / XP + s / (BK / 8), p.Mout - 1);
+            const int nb = min(n0 / p.rpn + i / XSEGF, p.nbk - 1);
+            xsh[j] = 15 - p.row_exp[m] - p.nb_exp[nb];
+        }
+    }
     u32x4 wr[kDepth][WPT];
     float sr[kDepth][WPT];
     int8_t zq[kDepth][WPT];
@@ -227,7 +262,7 @@ void gemm_bf16(const PParams p) {
                 const int i = min(tid + NT * j, XSEGF * NCC - 1);   // threads past the last item repeat it
                 const int s = NCC == 1 ? i : i % XSEGF;
                 const int qrow = s / (BK / 8), kq = s % (BK / 8);
-                const int m = min(m0 / 4 + qrow, p.Mout - 1), k = k0 + 8 * kq;
+                const int m = min(m0 / XP + qrow, p.Mout - 1), k = k0 + 8 * kq;
                 const int kk = k < p.K ? k : 0;
                 xin[d][j] = k < kend;
                 if constexpr (XF == 1) {
@@ -285,14 +320,38 @@ void gemm_bf16(const PParams p) {
     auto store_step = [&](int d, int bb, auto full) {
         constexpr bool FULL = decltype(full)::value && !XF && kTwoForm;
         if constexpr (XF) {
-            // segment (quad row qrow, kq) of copy i / XSEGF -> product rows
-            // 4 qrow + piece
+            // segment (x row qrow of the tile, kq) of copy i / XSEGF -> product
+            // rows XP qrow + piece
 #pragma unroll
             for (int j = 0; j < XPTF; ++j) {
                 const int i = tid + NT * j;
                 if (i < XSEGF * NCC) {
                     const int s = NCC == 1 ? i : i % XSEGF;
                     const int qrow = s / (BK / 8), kq = s % (BK / 8);
+                    if constexpr (XF == 3) {
+                        uint32_t hi[4], lo[4];
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const uint32_t wv = xr[d][j][0][q];   // bf16 elements 2q (low half), 2q + 1
+                            float a = as_f32(wv << 16) * as_f32(xsc[d][j][(2 * q) / 4][(2 * q) % 4]);
+                            float b = as_f32(wv & 0xFFFF0000u) * as_f32(xsc[d][j][(2 * q + 1) / 4][(2 * q + 1) % 4]);
+                            if (!xin[d][j]) a = b = 0.0f;
+                            a = __builtin_ldexpf(a, xsh[j]);
+                            b = __builtin_ldexpf(b, xsh[j]);
+                            const f16x2 h = __builtin_convertvector(f32x2{a, b}, f16x2);
+                            const f32x2 hb = __builtin_convertvector(h, f32x2);
+                            // remainders (exact in fp32); a non-finite value stays in hi
+                            float ra = a - hb[0], rb = b - hb[1];
+                            ra = __builtin_isnan(ra) ? 0.0f : ra;
+                            rb = __builtin_isnan(rb) ? 0.0f : rb;
+                            hi[q] = __builtin_bit_cast(uint32_t, h);
+                            lo[q] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{ra, rb}, f16x2));
+                        }
+                        uint16_t *dst = &xs[bb][NCC == 1 ? 0 : i / XSEGF][(2 * qrow) * kLdsRow + 8 * kq];
+                        *(u32x4 *)dst = u32x4{hi[0], hi[1], hi[2], hi[3]};
+                        *(u32x4 *)(dst + kLdsRow) = u32x4{lo[0], lo[1], lo[2], lo[3]};
+                        continue;
+                    }
                     float pc[8][3];
 #pragma unroll
                     for (int h = 0; h < 8; ++h) {
@@ -363,10 +422,17 @@ void gemm_bf16(const PParams p) {
                         const uint32_t hi = w & 0xF0F0F0F0u;          // bytes: k + {2, 6, 3, 7}
                         const uint32_t lo = (w << 4) & 0xF0F0F0F0u;   // bytes: k + {0, 4, 1, 5}
                         uint32_t o[4];
-                        o[0] = pack_hi16(sbyte<0>(lo) - zf, sbyte<2>(lo) - zf);
-                        o[1] = pack_hi16(sbyte<0>(hi) - zf, sbyte<2>(hi) - zf);
-                        o[2] = pack_hi16(sbyte<1>(lo) - zf, sbyte<3>(lo) - zf);
-                        o[3] = pack_hi16(sbyte<1>(hi) - zf, sbyte<3>(hi) - zf);
+                        if constexpr (XF == 3) {   // f16 (16 q is exact)
+                            o[0] = pack_f16(sbyte<0>(lo), sbyte<2>(lo));
+                            o[1] = pack_f16(sbyte<0>(hi), sbyte<2>(hi));
+                            o[2] = pack_f16(sbyte<1>(lo), sbyte<3>(lo));
+                            o[3] = pack_f16(sbyte<1>(hi), sbyte<3>(hi));
+                        } else {
+                            o[0] = pack_hi16(sbyte<0>(lo) - zf, sbyte<2>(lo) - zf);
+                            o[1] = pack_hi16(sbyte<0>(hi) - zf, sbyte<2>(hi) - zf);
+                            o[2] = pack_hi16(sbyte<1>(lo) - zf, sbyte<3>(lo) - zf);
+                            o[3] = pack_hi16(sbyte<1>(hi) - zf, sbyte<3>(hi) - zf);
+                        }
                         *(u32x4 *)(dst + 8 * q) = u32x4{o[0], o[1], o[2], o[3]};
                     }
                     if constexpr (NC == 0) ssc[bb][s] = sr[d][j];
@@ -406,7 +472,12 @@ void gemm_bf16(const PParams p) {
                     for (int a = 0; a < TM; ++a)
                         af[a] = *(const bf16x8 *)&xs[bb][cb][(wm * WM + a * 16 + (lane & 15)) * kLdsRow + kofs];
                 }
-                if (PREC == 8 || NC > 0) {
+                if constexpr (XF == 3) {
+#pragma unroll
+                    for (int a = 0; a < TM; ++a)
+                        acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, af[a]),
+                                                                         __builtin_bit_cast(f16x8, bfr), acc[a][b], 0, 0, 0);
+                } else if (PREC == 8 || NC > 0) {
 #pragma unroll
                     for (int a = 0; a < TM; ++a)
                         acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[a], bfr, acc[a][b], 0, 0, 0);
@@ -497,6 +568,27 @@ void gemm_bf16(const PParams p) {
     // ---- epilogue: lane holds C[4 (lane / 16) + e][lane % 16] of each tile
     float *out = p.y + (int64_t)blockIdx.z * p.split_stride;
     const int mrow = m0 + wm * WM + 4 * (lane >> 4), ncol = n0 + wn * WN + (lane & 15);
+    if constexpr (XF == 3) {
+        // the lane's four rows are the two pieces of x rows (mrow + 16 a) / 2
+        // and the next
+#pragma unroll
+        for (int b = 0; b < TN; ++b) {
+            const int n = ncol + b * 16;
+            if (n >= p.N) continue;
+            const int eb = p.nb_exp[n / p.rpn] - 15;
+#pragma unroll
+            for (int a = 0; a < TM; ++a) {
+                const int m = (mrow + a * 16) >> 1;
+                if (m < p.Mout)
+                    out[(int64_t)m * p.ldy + n] =
+                        __builtin_ldexpf((acc[a][b][0] + acc[a][b][1]) * scn[b], eb + p.row_exp[m]);
+                if (m + 1 < p.Mout)
+                    out[(int64_t)(m + 1) * p.ldy + n] =
+                        __builtin_ldexpf((acc[a][b][2] + acc[a][b][3]) * scn[b], eb + p.row_exp[m + 1]);
+            }
+        }
+        return;
+    }
     if constexpr (XF) {
         // the lane's four rows are the pieces of x row (mrow + 16 a) / 4
 #pragma unroll
@@ -547,6 +639,32 @@ void gemm_bf16(const PParams p) {
                     if (m < p.M) out[(int64_t)m * p.ldy + n] = acc[a][b][e] * scn[b];
                 }
         }
+    }
+}
+
+// e[r] = the least e with |x[r][k]| < 2^e for every finite element of each
+// bf16 row of x (0 for a row with none but zeros; -126 when the largest is
+// subnormal): one wave per row.  Non-finite elements stay non-finite
+// through the scaling.  K % 8 == 0, rows 16-byte aligned.
+__global__ __launch_bounds__(256) void row_exponents(const uint16_t *__restrict__ x, int64_t ldx, int32_t K,
+                                                     int32_t rows, int32_t *__restrict__ e) {
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    const uint16_t *xr = x + (int64_t)r * ldx;
+    uint32_t mx = 0;   // largest finite |x| as bf16 bits (magnitudes order as their bits)
+    for (int k = lane * 8; k < K; k += 512) {
+        const u32x4 v = *(const u32x4 *)(xr + k);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const uint32_t lo = v[c] & 0x7FFFu, hi = (v[c] >> 16) & 0x7FFFu;
+            mx = max(mx, max(lo < 0x7F80u ? lo : 0u, hi < 0x7F80u ? hi : 0u));
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, o));
+    if (lane == 0) {
+        const int E = (int)(mx >> 7);   // exponent field
+        e[r] = mx == 0 ? 0 : (E == 0 ? -126 : E - 126);
     }
 }
 
@@ -693,7 +811,7 @@ hipError_t launch_tail(Kern kern, int threads, dim3 grid, PParams p, const TailR
             }
             if (parts >= 2) {
                 const size_t bytes = (size_t)parts * (size_t)R * BM * BN * sizeof(float);
-                const bool room = !tq->scr->is_fixed() || bytes <= tq->scr->fixed_bytes;
+                const bool room = !tq->scr->is_fixed() || tq->scr->offset + bytes <= tq->scr->fixed_bytes;
                 float *tp = room ? (float *)tq->scr->get(s, bytes) : nullptr;
                 if (tp != nullptr) {
                     p.tail_first = (int32_t)(T - R);
@@ -720,6 +838,17 @@ hipError_t launch_tail(Kern kern, int threads, dim3 grid, PParams p, const TailR
     return hipLaunchKernel((const void *)kern, grid, dim3(threads), args, 0, s);
 }
 
+// Product rows per bf16 x row for runtime-layout INT4 weights: 2 (f16
+// pieces of the scaled fl(x * s)) unless TBH_PREFILL_NG_PIECES=4 asks for the
+// three bf16 pieces and a zero row.
+int ng_x_pieces() {
+    static const int v = [] {
+        const char *e = std::getenv("TBH_PREFILL_NG_PIECES");
+        return e && std::atoi(e) == 4 ? 4 : 2;
+    }();
+    return v;
+}
+
 template <int PREC, int BM, int BN, int BK, int NC>
 hipError_t launch_tile(const PParams &p, int splits, hipStream_t s, const TailReq *tq = nullptr) {
     static const int waves = [] {   // 4 or 8 forces the waves per block
@@ -730,6 +859,7 @@ hipError_t launch_tile(const PParams &p, int splits, hipStream_t s, const TailRe
     if constexpr (NC > 0) {   // runtime-layout INT4: split x (fp32, or bf16 widened)
         constexpr int WVN = BM == 128 ? 8 : 4;
         if (p.xf) hipLaunchKernelGGL((gemm_bf16<4, BM, BN, false, WVN, BK, 1, NC>), grid, dim3(64 * WVN), 0, s, p);
+        else if (p.row_exp) hipLaunchKernelGGL((gemm_bf16<4, BM, BN, false, WVN, BK, 3, NC>), grid, dim3(64 * WVN), 0, s, p);
         else hipLaunchKernelGGL((gemm_bf16<4, BM, BN, false, WVN, BK, 2, NC>), grid, dim3(64 * WVN), 0, s, p);
     } else {
         const bool w8 = waves == 8 || (waves != 4 && BN == 128 && (p.M >= 256 || PREC == 4));
@@ -878,14 +1008,15 @@ int ng_copies(const tbh_weight &w) {
 }
 
 // Runtime-layout INT4 (one scale per (N-block, k)) with x given as p.x (bf16)
-// or p.xf (fp32), p.M = 4 * x rows: 64 x 64 tiles (16 x rows by 64 outputs,
-// four waves) or 128 x 64 tiles (32 x rows, eight waves), split along K when
-// the tiles are fewer than the CUs.
+// or p.xf (fp32), p.M = 4 or 2 (bf16 x with p.row_exp) product rows per x row:
+// 64 x 64 tiles (four waves) or 128 x 64 tiles (eight waves), split along K
+// when the tiles are fewer than the CUs.
 hipError_t launch_ngroup(const tbh_weight &w, PParams p, hipStream_t s, const Scratch &scr) {
     p.rpn = w.rows_per_nblock;
     p.nbk = (int32_t)((w.Np + w.rows_per_nblock - 1) / w.rows_per_nblock);
     const int64_t tiles = ((p.Np + 63) / 64) * ((p.M + 63) / 64);
-    // past 16 x rows (64 product rows): 128 x 64 tiles as 8-wave blocks,
+    // past 64 product rows (16 x rows in four pieces, 32 in two): 128 x 64
+    // tiles as 8-wave blocks,
     // which re-read the weights half as often (2048x5632, N-blocks of 32, us
     // per call 64 / 128 product rows: M = 64 28.1 / 24.6, M = 128 49.2 /
     // 41.0, M = 512 160.1 / 133.9, M = 2048 598 / 508); with four copies of
@@ -965,17 +1096,40 @@ hipError_t launch_prefill(const tbh_weight &w, const uint16_t *x, int64_t ldx, i
                           int64_t ldy, hipStream_t s, const Scratch &scr) {
     if (!prefill_supported(w) || M < 1 || w.K % 8 != 0 || ldx % 8 != 0 || ((uintptr_t)x & 15) != 0)
         return hipErrorInvalidValue;
-    // runtime-layout INT4: every x row becomes the three bf16 pieces of
-    // fl(x * s) and a zero row, as in the fp32 form
-    const int64_t pieces = w.path == Path::Int4NGroup ? 4 : 1;
+    // runtime-layout INT4: past 64 rows every x row becomes the two f16
+    // pieces of the scaled fl(x * s), after a pass that finds each row's
+    // exponent bound (an int32 per row ahead of the split-K scratch); up to
+    // 64 rows, or when that scratch is not to be had, the three bf16 pieces
+    // and a zero row.  2048x5632, us per call, four / two pieces: M = 64 24.1
+    // / 25.2 (the extra pass), 128 40.2 / 35.9, 512 131.6 / 98.5, 2048 516 /
+    // 372.
+    const bool ng = w.path == Path::Int4NGroup;
+    const bool f16x = ng && ng_x_pieces() == 2 && w.ng_sexp != nullptr;
     for (int64_t m0 = 0; m0 < M; m0 += kGemmRowsPerLaunch) {
         const int64_t mc = std::min(kGemmRowsPerLaunch, M - m0);
         PParams p = prefill_params(w, ldx, y + m0 * ldy, ldy);
         p.x = x + m0 * ldx;
+        Scratch sub = scr;
+        int64_t pieces = ng ? 4 : 1;
+        if (f16x && mc > 64) {
+            const size_t off = ((size_t)mc * sizeof(int32_t) + 255) / 256 * 256;
+            int32_t *re = (int32_t *)scr.get(s, off);
+            if (re != nullptr) {
+                hipLaunchKernelGGL(row_exponents, dim3((unsigned)((mc + 3) / 4)), dim3(256), 0, s, p.x, ldx,
+                                   (int32_t)w.K, (int32_t)mc, re);
+                p.row_exp = re;
+                p.nb_exp = w.ng_sexp;
+                sub.offset = scr.offset + off;
+                pieces = 2;
+            }
+        }
         p.M = (int32_t)(pieces * mc);
         p.Mout = (int32_t)mc;
-        const hipError_t e = launch_rows(w, p, s, scr);
-        if (e != hipSuccess) return e;
+        const hipError_t e = launch_rows(w, p, s, sub);
+        if (e != hipSuccess) {
+            scr.shortfall = sub.shortfall;
+            return e;
+        }
     }
     return hipSuccess;
 }
