@@ -130,8 +130,8 @@ def test_random_large_prefill(backend, seed):
 
 
 # Runtime-layout INT4 (groups along N) at 65..600 rows of x, where the bf16
-# entry's GEMM takes x as two f16 pieces scaled per x row and per N-block:
-# group sizes that give one, two or four N-blocks per 64-output tile or a
+# entry's GEMM scales x per row and the dequantized weights per N-block and
+# splits the weights into two f16 pieces: group sizes that give one, two or four N-blocks per 64-output tile or a
 # group spanning rows of k, ragged K, M and N.
 NG_KINDS = ["int4_kn_g16", "int4_kn_g32", "int4_kn_g64", "int4_kn_g128", "int4_kn_g48"]
 

@@ -1028,8 +1028,9 @@ def test_prefill_bf16_split_k_determinism_and_graphs(backend):
     (1000, 40, 80, 65),      # a group spans two k rows: all outputs share each k-block's scale
 ])
 def test_prefill_bf16_runtime_layout(backend, K, N, gs, M):
-    # INT4 with groups along N (one scale per (N-block, k)): the GEMM stages
-    # x times each N-block's scales, split into three bf16 pieces
+    # INT4 with groups along N (one scale per (N-block, k)): up to 64 rows the
+    # GEMM stages x times each N-block's scales as three bf16 pieces, past
+    # that the dequantized weights fl(q s) as two f16 pieces
     qk = _int4_kn(149 + K + N + gs, K, N, gs)
     pq = _product(qk, (K, N))
     assert backend.weight(pq).path == "int4_ngroup"
@@ -1038,10 +1039,10 @@ def test_prefill_bf16_runtime_layout(backend, K, N, gs, M):
 
 @pytest.mark.parametrize("M", [64, 65, 96])
 def test_prefill_bf16_runtime_layout_block_ranges(backend, M):
-    # past 64 rows the runtime-layout GEMM scales fl(x * s) by a power of two
-    # per x row and per N-block before splitting it into two f16 pieces:
+    # past 64 rows the runtime-layout GEMM scales x by a power of two per row
+    # and fl(q s) by one per N-block, the latter split into two f16 pieces:
     # N-blocks whose scales differ by 2^40, rows that differ by 2^30, each
-    # N-block checked on its own (M = 64 takes the three bf16 pieces)
+    # N-block checked on its own (M = 64 takes the three bf16 pieces of x)
     import torch
 
     K, N, gs = 1024, 256, 32
@@ -1069,7 +1070,8 @@ def test_prefill_bf16_runtime_layout_block_ranges(backend, M):
 def test_prefill_bf16_runtime_layout_nonfinite(backend, M):
     # infinities and NaNs in x reach the outputs as the float64 product of
     # the same dequantized weights gives them (inf * 0 = NaN, inf - inf =
-    # NaN), and leave the other rows' scaling alone
+    # NaN; an infinity meets both f16 pieces of a weight, which share its
+    # sign), and leave the other rows' scaling alone
     import torch
 
     K, N, gs = 512, 256, 32

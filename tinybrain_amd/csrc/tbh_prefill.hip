@@ -80,8 +80,8 @@ struct PParams {
     // dispatches them.
     int32_t tail_first, tail_parts, tail_steps, tail_n, tiles_n;
     float *tail_part;
-    // XF = 3: per x row e with max_k |x| < 2^e, and the weight's per N-block
-    // e with max_k |s| < 2^e
+    // gemm_ngw: per x row e with |x| < 2^e over its finite values, and the
+    // weight's per N-block e with |s| < 2^e over its finite scales
     const int32_t *row_exp;
     const int32_t *nb_exp;
 };
@@ -131,15 +131,6 @@ __device__ __forceinline__ float sbyte(uint32_t w) {
 // piece 3 is zero), so the four rows a lane holds in each 16 x 16
 // accumulator tile are the pieces of one x row, and the epilogue adds them
 // into that row's output.  XF = 2: the same from bf16 x (widened exactly).
-// XF = 3 (bf16 x, runtime-layout scales): two product rows per x row, on
-// the f16 MFMA.  v = fl(x * s) is scaled exactly by 2^(15 - er - eb) (er, eb:
-// the x row's and the N-block's bounds over their finite values, |x| < 2^er,
-// |s| < 2^eb, so a finite |v'| <= 2^15) and split into f16 pieces hi =
-// f16(v'), lo = f16(v' - hi) (v' - hi is exact in fp32; 0 for a non-finite
-// v', which stays in hi): row r = piece r % 2 of x row r / 2, and 16 q is
-// exact in f16.  The pieces hold v' to 2^-22 of itself, or to 2^-25 absolute
-// below the f16 normal range; the epilogue adds the two rows and scales
-// back by 2^-(15 - er - eb).  Half the MFMAs and staged rows of XF = 2.
 //
 // NC > 0: INT4 in the runtime layout (groups along N: one scale per
 // (N-block of rpn rows, k)).  The scale varies along K inside an MFMA, so it
@@ -160,8 +151,7 @@ template <int PREC, int BM, int BN, bool ZP, int WV, int BK, int XF, int NC>
 __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(kFourWavesPerSimd<PREC, BM, BN, WV, BK, NC> ? 4 : 1)))
 void gemm_bf16(const PParams p) {
     static_assert(NC == 0 || (PREC == 4 && XF != 0 && !ZP), "runtime-layout INT4 stages split x, no zero points");
-    static_assert(XF < 2 || NC > 0, "bf16 x is split only for runtime-layout scales");
-    constexpr int XP = XF == 3 ? 2 : 4;                     // product rows per x row (split x)
+    static_assert(XF != 2 || NC > 0, "bf16 x is split only for runtime-layout scales");
     constexpr int NCC = NC > 0 ? NC : 1;                    // copies of x in LDS
     // Steps wholly inside K and the N tile run an unmasked loop form, except
     // in INT4 blocks with K steps of 128 (256 VGPRs), which run every step
@@ -222,28 +212,15 @@ void gemm_bf16(const PParams p) {
     // ---- global -> registers for one step, into register stage d of kDepth:
     // the loads of steps t+1 .. t+kDepth-1 are in flight while step t runs
     // split x: a segment is 8 elements of one x row (two 16-byte loads of
-    // fp32, one of bf16), staged as the XP product rows of its pieces; with
+    // fp32, one of bf16), staged as the four product rows of its pieces; with
     // runtime-layout scales an item is a (segment, copy) pair and also loads
     // the copy's 8 scales
-    constexpr int XSEGF = (BM / XP) * (BK / 8);
+    constexpr int XSEGF = (BM / 4) * (BK / 8);
     constexpr int XPTF = XF ? (XSEGF * NCC + NT - 1) / NT : 1;
     constexpr int XPTL = XF ? XPTF : XPT;
     u32x4 xr[kDepth][XPTL][XF == 1 ? 2 : 1];
     u32x4 xsc[kDepth][NC > 0 ? XPTL : 1][2];
     bool xin[kDepth][XPTL];   // segment within K, applied at the LDS store
-    // XF = 3: each item's scaling exponent 15 - er - eb (its x row and copy
-    // are the same in every step)
-    int xsh[XF == 3 ? XPTL : 1];
-    if constexpr (XF == 3) {
-#pragma unroll
-        for (int j = 0; j < XPTF; ++j) {
-            const int i = min(tid + NT * j, XSEGF * NCC - 1);
-            const int s = NCC == 1 ? i : i % XSEGF;
-            const int m = min(m0 / XP + s / (BK / 8), p.Mout - 1);
-            const int nb = min(n0 / p.rpn + i / XSEGF, p.nbk - 1);
-            xsh[j] = 15 - p.row_exp[m] - p.nb_exp[nb];
-        }
-    }
     u32x4 wr[kDepth][WPT];
     float sr[kDepth][WPT];
     int8_t zq[kDepth][WPT];
@@ -262,7 +239,7 @@ void gemm_bf16(const PParams p) {
                 const int i = min(tid + NT * j, XSEGF * NCC - 1);   // threads past the last item repeat it
                 const int s = NCC == 1 ? i : i % XSEGF;
                 const int qrow = s / (BK / 8), kq = s % (BK / 8);
-                const int m = min(m0 / XP + qrow, p.Mout - 1), k = k0 + 8 * kq;
+                const int m = min(m0 / 4 + qrow, p.Mout - 1), k = k0 + 8 * kq;
                 const int kk = k < p.K ? k : 0;
                 xin[d][j] = k < kend;
                 if constexpr (XF == 1) {
@@ -320,38 +297,14 @@ void gemm_bf16(const PParams p) {
     auto store_step = [&](int d, int bb, auto full) {
         constexpr bool FULL = decltype(full)::value && !XF && kTwoForm;
         if constexpr (XF) {
-            // segment (x row qrow of the tile, kq) of copy i / XSEGF -> product
-            // rows XP qrow + piece
+            // segment (quad row qrow, kq) of copy i / XSEGF -> product rows
+            // 4 qrow + piece
 #pragma unroll
             for (int j = 0; j < XPTF; ++j) {
                 const int i = tid + NT * j;
                 if (i < XSEGF * NCC) {
                     const int s = NCC == 1 ? i : i % XSEGF;
                     const int qrow = s / (BK / 8), kq = s % (BK / 8);
-                    if constexpr (XF == 3) {
-                        uint32_t hi[4], lo[4];
-#pragma unroll
-                        for (int q = 0; q < 4; ++q) {
-                            const uint32_t wv = xr[d][j][0][q];   // bf16 elements 2q (low half), 2q + 1
-                            float a = as_f32(wv << 16) * as_f32(xsc[d][j][(2 * q) / 4][(2 * q) % 4]);
-                            float b = as_f32(wv & 0xFFFF0000u) * as_f32(xsc[d][j][(2 * q + 1) / 4][(2 * q + 1) % 4]);
-                            if (!xin[d][j]) a = b = 0.0f;
-                            a = __builtin_ldexpf(a, xsh[j]);
-                            b = __builtin_ldexpf(b, xsh[j]);
-                            const f16x2 h = __builtin_convertvector(f32x2{a, b}, f16x2);
-                            const f32x2 hb = __builtin_convertvector(h, f32x2);
-                            // remainders (exact in fp32); a non-finite value stays in hi
-                            float ra = a - hb[0], rb = b - hb[1];
-                            ra = __builtin_isnan(ra) ? 0.0f : ra;
-                            rb = __builtin_isnan(rb) ? 0.0f : rb;
-                            hi[q] = __builtin_bit_cast(uint32_t, h);
-                            lo[q] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{ra, rb}, f16x2));
-                        }
-                        uint16_t *dst = &xs[bb][NCC == 1 ? 0 : i / XSEGF][(2 * qrow) * kLdsRow + 8 * kq];
-                        *(u32x4 *)dst = u32x4{hi[0], hi[1], hi[2], hi[3]};
-                        *(u32x4 *)(dst + kLdsRow) = u32x4{lo[0], lo[1], lo[2], lo[3]};
-                        continue;
-                    }
                     float pc[8][3];
 #pragma unroll
                     for (int h = 0; h < 8; ++h) {
@@ -422,17 +375,10 @@ void gemm_bf16(const PParams p) {
                         const uint32_t hi = w & 0xF0F0F0F0u;          // bytes: k + {2, 6, 3, 7}
                         const uint32_t lo = (w << 4) & 0xF0F0F0F0u;   // bytes: k + {0, 4, 1, 5}
                         uint32_t o[4];
-                        if constexpr (XF == 3) {   // f16 (16 q is exact)
-                            o[0] = pack_f16(sbyte<0>(lo), sbyte<2>(lo));
-                            o[1] = pack_f16(sbyte<0>(hi), sbyte<2>(hi));
-                            o[2] = pack_f16(sbyte<1>(lo), sbyte<3>(lo));
-                            o[3] = pack_f16(sbyte<1>(hi), sbyte<3>(hi));
-                        } else {
-                            o[0] = pack_hi16(sbyte<0>(lo) - zf, sbyte<2>(lo) - zf);
-                            o[1] = pack_hi16(sbyte<0>(hi) - zf, sbyte<2>(hi) - zf);
-                            o[2] = pack_hi16(sbyte<1>(lo) - zf, sbyte<3>(lo) - zf);
-                            o[3] = pack_hi16(sbyte<1>(hi) - zf, sbyte<3>(hi) - zf);
-                        }
+                        o[0] = pack_hi16(sbyte<0>(lo) - zf, sbyte<2>(lo) - zf);
+                        o[1] = pack_hi16(sbyte<0>(hi) - zf, sbyte<2>(hi) - zf);
+                        o[2] = pack_hi16(sbyte<1>(lo) - zf, sbyte<3>(lo) - zf);
+                        o[3] = pack_hi16(sbyte<1>(hi) - zf, sbyte<3>(hi) - zf);
                         *(u32x4 *)(dst + 8 * q) = u32x4{o[0], o[1], o[2], o[3]};
                     }
                     if constexpr (NC == 0) ssc[bb][s] = sr[d][j];
@@ -472,12 +418,7 @@ void gemm_bf16(const PParams p) {
                     for (int a = 0; a < TM; ++a)
                         af[a] = *(const bf16x8 *)&xs[bb][cb][(wm * WM + a * 16 + (lane & 15)) * kLdsRow + kofs];
                 }
-                if constexpr (XF == 3) {
-#pragma unroll
-                    for (int a = 0; a < TM; ++a)
-                        acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, af[a]),
-                                                                         __builtin_bit_cast(f16x8, bfr), acc[a][b], 0, 0, 0);
-                } else if (PREC == 8 || NC > 0) {
+                if (PREC == 8 || NC > 0) {
 #pragma unroll
                     for (int a = 0; a < TM; ++a)
                         acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[a], bfr, acc[a][b], 0, 0, 0);
@@ -568,27 +509,6 @@ void gemm_bf16(const PParams p) {
     // ---- epilogue: lane holds C[4 (lane / 16) + e][lane % 16] of each tile
     float *out = p.y + (int64_t)blockIdx.z * p.split_stride;
     const int mrow = m0 + wm * WM + 4 * (lane >> 4), ncol = n0 + wn * WN + (lane & 15);
-    if constexpr (XF == 3) {
-        // the lane's four rows are the two pieces of x rows (mrow + 16 a) / 2
-        // and the next
-#pragma unroll
-        for (int b = 0; b < TN; ++b) {
-            const int n = ncol + b * 16;
-            if (n >= p.N) continue;
-            const int eb = p.nb_exp[n / p.rpn] - 15;
-#pragma unroll
-            for (int a = 0; a < TM; ++a) {
-                const int m = (mrow + a * 16) >> 1;
-                if (m < p.Mout)
-                    out[(int64_t)m * p.ldy + n] =
-                        __builtin_ldexpf((acc[a][b][0] + acc[a][b][1]) * scn[b], eb + p.row_exp[m]);
-                if (m + 1 < p.Mout)
-                    out[(int64_t)(m + 1) * p.ldy + n] =
-                        __builtin_ldexpf((acc[a][b][2] + acc[a][b][3]) * scn[b], eb + p.row_exp[m + 1]);
-            }
-        }
-        return;
-    }
     if constexpr (XF) {
         // the lane's four rows are the pieces of x row (mrow + 16 a) / 4
 #pragma unroll
@@ -639,6 +559,194 @@ void gemm_bf16(const PParams p) {
                     if (m < p.M) out[(int64_t)m * p.ldy + n] = acc[a][b][e] * scn[b];
                 }
         }
+    }
+}
+
+// The low f16 piece of a weight w' whose high piece was rounded toward zero
+// (r = w' - hi, exact; NaN for a non-finite w', which hi holds): r, but at
+// least 2^-24 in magnitude and with w's sign unless w' = 0, so that an
+// infinite x meets two pieces of one sign (inf * w' as one product: +-inf,
+// or NaN for w' = 0) and never inf * 0 = NaN from an empty low piece.
+__device__ __forceinline__ float lo_piece(float w, float r) {
+    return w == 0.0f ? 0.0f : __builtin_copysignf(__builtin_fmaxf(__builtin_fabsf(r), 0x1p-24f), w);
+}
+
+// Runtime-layout INT4 (one scale per (N-block, k)) with bf16 x, scaled on
+// the weight side: each weight's fl(q * s), the reference's dequantized
+// value, is scaled exactly by 2^(12 - eb) (|s| < 2^eb over the N-block's
+// finite scales, so |w'| < 2^15) and staged as two f16 pieces, hi = w'
+// rounded toward zero and lo = lo_piece(w', w' - hi), in two LDS row blocks;
+// x is staged once as f16 scaled by 2^(15 - er) (bf16 values are exact in
+// f16 there), every A fragment meets both pieces, and y = 2^(er + eb - 27) *
+// sum(x' hi + x' lo).  The pieces hold w' to 2^-21 of itself, and to 2^-24
+// absolute below the f16 normal range.  Each weight element and each x
+// element is staged once per tile.  (Scaling and splitting x instead, once
+// per N-block of a tile, as gemm_bf16 does for fp32 x, stages N / rpn times
+// the x elements: at 2048x5632, N-blocks of 32, two f16 pieces of x took 99
+// / 373 us at M = 512 / 2048 against 56 / 155 us here.)
+//
+// Tiles BM x rows by BN outputs, WV waves as 2 x (WV / 2), K steps of 64 in
+// two LDS buffers with a two-step register ring (the gemm_bf16 loop); K
+// split z of p.split_steps steps writes p.y + z * p.split_stride.
+template <int BM, int BN, int WV>
+__global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(WV == 8 ? 4 : 1)))
+void gemm_ngw(const PParams p) {
+    constexpr int BK = 64, kLdsRow = BK + kRowPad;
+    constexpr int NT = 64 * WV, WC = WV / 2;
+    constexpr int WM = BM / 2, WN = BN / WC, TM = WM / 16, TN = WN / 16;
+    constexpr int XSEG = BM * (BK / 8), XPT = XSEG / NT;   // x: 8-element segments per step
+    constexpr int WIT = BN * (BK / 8), WPT = WIT / NT;     // weights: 8-k words per step
+    static_assert(XSEG % NT == 0 && WIT % NT == 0 && TM >= 1 && TN >= 1, "tile too small for the waves");
+
+    __shared__ __attribute__((aligned(16))) uint16_t xs[2][BM * kLdsRow];
+    __shared__ __attribute__((aligned(16))) uint16_t ws[2][2 * BN * kLdsRow];   // hi rows, then lo rows
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wm = wave / WC, wn = wave % WC;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN, kpart = blockIdx.z;
+    const int kp = p.chunks * 32;   // padded row length (the scale table's too)
+    const int nsteps = (kp + BK - 1) / BK;
+    const int t_begin = kpart * p.split_steps;
+    const int t_end = min(nsteps, t_begin + p.split_steps);
+    const int kend = min(p.K, t_end * BK);
+
+    // each item's row is the same in every step, so its scaling exponent is too
+    int xsh[XPT], wsh[WPT];
+#pragma unroll
+    for (int j = 0; j < XPT; ++j) xsh[j] = 15 - p.row_exp[min(m0 + (tid + NT * j) / (BK / 8), p.Mout - 1)];
+#pragma unroll
+    for (int j = 0; j < WPT; ++j) wsh[j] = 8 - p.nb_exp[min(n0 + (tid + NT * j) / (BK / 8), p.Np - 1) / p.rpn];
+
+    u32x4 xr[kDepth][XPT];
+    bool xin[kDepth][XPT];
+    uint32_t wr[kDepth][WPT];
+    u32x4 sr[kDepth][WPT][2];
+    auto load_step = [&](int t, int d) {
+        const int k0 = t * BK;
+#pragma unroll
+        for (int j = 0; j < XPT; ++j) {
+            const int s = tid + NT * j, row = s / (BK / 8), k = k0 + 8 * (s % (BK / 8));
+            const int m = min(m0 + row, p.Mout - 1);   // rows past M read row M - 1 (never stored)
+            xin[d][j] = k < kend;
+            xr[d][j] = *(const u32x4 *)(p.x + (int64_t)m * p.ldx + (k < p.K ? k : 0));
+        }
+#pragma unroll
+        for (int j = 0; j < WPT; ++j) {
+            const int s = tid + NT * j, row = s / (BK / 8), k = k0 + 8 * (s % (BK / 8));
+            const int n = min(n0 + row, p.Np - 1);
+            const int kk = k < kp ? k : 0;   // past the padded row: any valid word (x is 0 there)
+            // word kk / 8 of the row: nibbles of k + {0, 2, 4, 6} at bits 0, 4, 8, 12, of
+            // k + {1, 3, 5, 7} at bits 16, 20, 24, 28
+            wr[d][j] = __builtin_nontemporal_load((const uint32_t *)(p.data + (int64_t)n * p.row_bytes + kk / 2));
+            const float *sp = p.scales + (int64_t)(n / p.rpn) * kp + kk;
+            sr[d][j][0] = *(const u32x4 *)sp;
+            sr[d][j][1] = *(const u32x4 *)(sp + 4);
+        }
+    };
+    auto store_step = [&](int d, int bb) {
+#pragma unroll
+        for (int j = 0; j < XPT; ++j) {
+            const int s = tid + NT * j, row = s / (BK / 8), kq = s % (BK / 8);
+            uint32_t o[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t wv = xr[d][j][q];   // bf16 elements 2q (low half), 2q + 1
+                const float a = xin[d][j] ? as_f32(wv << 16) : 0.0f;
+                const float b = xin[d][j] ? as_f32(wv & 0xFFFF0000u) : 0.0f;
+                o[q] = pack_f16(__builtin_ldexpf(a, xsh[j]), __builtin_ldexpf(b, xsh[j]));
+            }
+            *(u32x4 *)&xs[bb][row * kLdsRow + 8 * kq] = u32x4{o[0], o[1], o[2], o[3]};
+        }
+#pragma unroll
+        for (int j = 0; j < WPT; ++j) {
+            const int s = tid + NT * j, row = s / (BK / 8), kw = s % (BK / 8);
+            // u = q + 8 per nibble: flipping each nibble's top bit leaves q as
+            // a 4-bit two's complement value, read as the signed byte 16 q once
+            // moved into the upper half of its byte
+            const uint32_t w = wr[d][j] ^ 0x88888888u;
+            const uint32_t hi = w & 0xF0F0F0F0u;          // bytes: k + {2, 6, 3, 7}
+            const uint32_t lo = (w << 4) & 0xF0F0F0F0u;   // bytes: k + {0, 4, 1, 5}
+            const float q16[8] = {sbyte<0>(lo), sbyte<2>(lo), sbyte<0>(hi), sbyte<2>(hi),
+                                  sbyte<1>(lo), sbyte<3>(lo), sbyte<1>(hi), sbyte<3>(hi)};
+            uint32_t ph[4], pl[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                // 16 q * (s 2^(8 - eb)) = fl(q s) 2^(12 - eb), exactly
+                const float a = q16[2 * q] * __builtin_ldexpf(as_f32(sr[d][j][q / 2][(2 * q) % 4]), wsh[j]);
+                const float b = q16[2 * q + 1] * __builtin_ldexpf(as_f32(sr[d][j][q / 2][(2 * q + 1) % 4]), wsh[j]);
+                const f16x2 h = __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(a, b));   // toward zero
+                const f32x2 hb = __builtin_convertvector(h, f32x2);
+                ph[q] = __builtin_bit_cast(uint32_t, h);
+                pl[q] = pack_f16(lo_piece(a, a - hb[0]), lo_piece(b, b - hb[1]));
+            }
+            uint16_t *dst = &ws[bb][row * kLdsRow + 8 * kw];
+            *(u32x4 *)dst = u32x4{ph[0], ph[1], ph[2], ph[3]};
+            *(u32x4 *)(dst + BN * kLdsRow) = u32x4{pl[0], pl[1], pl[2], pl[3]};
+        }
+    };
+
+    f32x4 acc[TM][TN];
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto compute = [&](int bb) {
+#pragma unroll
+        for (int ks = 0; ks < BK / 32; ++ks) {
+            const int kofs = ks * 32 + 8 * (lane >> 4);
+            f16x8 af[TM];
+#pragma unroll
+            for (int a = 0; a < TM; ++a)
+                af[a] = *(const f16x8 *)&xs[bb][(wm * WM + a * 16 + (lane & 15)) * kLdsRow + kofs];
+#pragma unroll
+            for (int b = 0; b < TN; ++b) {
+                const int wrow = wn * WN + b * 16 + (lane & 15);
+                const f16x8 bh = *(const f16x8 *)&ws[bb][wrow * kLdsRow + kofs];
+                const f16x8 bl = *(const f16x8 *)&ws[bb][(BN + wrow) * kLdsRow + kofs];
+#pragma unroll
+                for (int a = 0; a < TM; ++a) {
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[a], bh, acc[a][b], 0, 0, 0);
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[a], bl, acc[a][b], 0, 0, 0);
+                }
+            }
+        }
+    };
+
+    // the register ring and LDS buffers of gemm_bf16: each iteration stages
+    // step t + 1, refills its slot with step t + 3, computes step t, and ends
+    // with the step's one barrier; steps past this split's K meet x = 0
+    const int t_stop = t_begin + ((t_end - t_begin + kDepth - 1) / kDepth) * kDepth;
+    load_step(t_begin, 0);
+    load_step(t_begin + 1, 1);
+    store_step(0, 0);
+    lds_barrier();
+    load_step(t_begin + 2, 0);
+    for (int t0 = t_begin; t0 < t_stop; t0 += 2) {
+        store_step(1, 1);
+        load_step(t0 + 3, 1);
+        compute(0);
+        lds_barrier();
+        store_step(0, 0);
+        load_step(t0 + 4, 0);
+        compute(1);
+        lds_barrier();
+    }
+
+    // lane holds C[4 (lane / 16) + e][lane % 16] of each 16 x 16 tile
+    float *out = p.y + (int64_t)kpart * p.split_stride;
+    const int mrow = m0 + wm * WM + 4 * (lane >> 4), ncol = n0 + wn * WN + (lane & 15);
+#pragma unroll
+    for (int b = 0; b < TN; ++b) {
+        const int n = ncol + b * 16;
+        if (n >= p.N) continue;
+        const int eb = p.nb_exp[n / p.rpn] - 27;
+#pragma unroll
+        for (int a = 0; a < TM; ++a)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int m = mrow + a * 16 + e;
+                if (m < p.Mout) out[(int64_t)m * p.ldy + n] = __builtin_ldexpf(acc[a][b][e], eb + p.row_exp[m]);
+            }
     }
 }
 
@@ -838,13 +946,13 @@ hipError_t launch_tail(Kern kern, int threads, dim3 grid, PParams p, const TailR
     return hipLaunchKernel((const void *)kern, grid, dim3(threads), args, 0, s);
 }
 
-// Product rows per bf16 x row for runtime-layout INT4 weights: 2 (f16
-// pieces of the scaled fl(x * s)) unless TBH_PREFILL_NG_PIECES=4 asks for the
-// three bf16 pieces and a zero row.
-int ng_x_pieces() {
-    static const int v = [] {
-        const char *e = std::getenv("TBH_PREFILL_NG_PIECES");
-        return e && std::atoi(e) == 4 ? 4 : 2;
+// Fewest x rows of bf16 x that runtime-layout INT4 weights take on the
+// weight-side kernel (gemm_ngw; TBH_PREFILL_NG_F16_MIN); fewer rows go to
+// gemm_bf16 with x split into three bf16 pieces and a zero row per N-block.
+int64_t ng_f16_min_rows() {
+    static const int64_t v = [] {
+        const char *e = std::getenv("TBH_PREFILL_NG_F16_MIN");
+        return e && *e ? std::max<int64_t>(1, std::atoll(e)) : (int64_t)65;
     }();
     return v;
 }
@@ -859,7 +967,6 @@ hipError_t launch_tile(const PParams &p, int splits, hipStream_t s, const TailRe
     if constexpr (NC > 0) {   // runtime-layout INT4: split x (fp32, or bf16 widened)
         constexpr int WVN = BM == 128 ? 8 : 4;
         if (p.xf) hipLaunchKernelGGL((gemm_bf16<4, BM, BN, false, WVN, BK, 1, NC>), grid, dim3(64 * WVN), 0, s, p);
-        else if (p.row_exp) hipLaunchKernelGGL((gemm_bf16<4, BM, BN, false, WVN, BK, 3, NC>), grid, dim3(64 * WVN), 0, s, p);
         else hipLaunchKernelGGL((gemm_bf16<4, BM, BN, false, WVN, BK, 2, NC>), grid, dim3(64 * WVN), 0, s, p);
     } else {
         const bool w8 = waves == 8 || (waves != 4 && BN == 128 && (p.M >= 256 || PREC == 4));
@@ -893,6 +1000,64 @@ int blocks_per_cu(int dflt) {
 }
 
 constexpr int kMinSplitK = 256;  // K a split keeps at least
+
+// y[0, n) = the sum of `splits` partial arrays part + z n, in split order.
+hipError_t launch_split_sum(const float *part, int splits, float *y, int64_t n, int64_t cus, hipStream_t s) {
+    const int64_t grid_cap = 4 * cus;
+    if (n % 4 == 0 && ((uintptr_t)y & 15) == 0) {
+        const int64_t n4 = n / 4;
+        hipLaunchKernelGGL(split_sum4, dim3((unsigned)std::min(grid_cap, (n4 + 255) / 256)), dim3(256), 0, s,
+                           (const float4 *)part, n4, splits, (float4 *)y, n4);
+    } else {
+        hipLaunchKernelGGL(split_sum, dim3((unsigned)std::min(grid_cap, (n + 255) / 256)), dim3(256), 0, s,
+                           part, n, splits, y, n);
+    }
+    return hipGetLastError();
+}
+
+// Runtime-layout INT4 with bf16 x on the weight-side kernel (p.row_exp set,
+// p.M = x rows): 128 x 64 tiles as 8-wave blocks past 64 rows, else 64 x 64
+// as 4-wave blocks, split along K to a block per CU.
+hipError_t launch_ngw(const tbh_weight &w, PParams p, hipStream_t s, const Scratch &scr) {
+    p.rpn = w.rows_per_nblock;
+    p.nbk = (int32_t)((w.Np + w.rows_per_nblock - 1) / w.rows_per_nblock);
+    constexpr int BK = 64;
+    const int nsteps = (int)((p.chunks * kInt4ChunkElems + BK - 1) / BK);
+    const int64_t cus = std::max(1, w.dev->cu_count);
+    const bool big = p.M > 64;
+    const int64_t bm = big ? 128 : 64;
+    const int64_t tiles = ((p.Np + 63) / 64) * ((p.M + bm - 1) / bm);
+    const int bpc = blocks_per_cu(1);
+    int splits = 1, sps = nsteps;
+    if (tiles < bpc * cus && p.ldy == p.N) {
+        const int64_t want = (bpc * cus + tiles - 1) / tiles;
+        sps = (int)std::max<int64_t>(kMinSplitK / BK, (nsteps + want - 1) / want);
+        sps = (sps + kDepth - 1) / kDepth * kDepth;
+        splits = (nsteps + sps - 1) / sps;
+    }
+    float *const y = p.y;
+    const int64_t n = (int64_t)p.Mout * p.N;
+    float *part = nullptr;
+    if (splits > 1) {
+        part = (float *)scr.get(s, (size_t)(splits * n) * sizeof(float));
+        if (!part && scr.is_fixed()) return hipErrorOutOfMemory;
+        if (!part) {          // no workspace (graph capture before any eager call): one pass
+            splits = 1;
+            sps = nsteps;
+        }
+    }
+    p.split_steps = sps;
+    if (splits > 1) {
+        p.y = part;
+        p.split_stride = n;
+    }
+    const dim3 grid((unsigned)((p.Np + 63) / 64), (unsigned)((p.M + bm - 1) / bm), (unsigned)splits);
+    if (big) hipLaunchKernelGGL((gemm_ngw<128, 64, 8>), grid, dim3(512), 0, s, p);
+    else hipLaunchKernelGGL((gemm_ngw<64, 64, 4>), grid, dim3(256), 0, s, p);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess || splits == 1) return e;
+    return launch_split_sum(part, splits, y, n, cus, s);
+}
 
 // K is split over blocks when there are fewer than bpc blocks per CU.  BK:
 // K per staged step (64 or 128).
@@ -928,16 +1093,7 @@ hipError_t launch_split(const tbh_weight &w, PParams p, int64_t tiles, int bpc, 
     const TailReq tq{nsteps, cus, &scr};
     hipError_t e = launch_tile<PREC, BM, BN, BK, NC>(p, splits, s, splits == 1 ? &tq : nullptr);
     if (e != hipSuccess || splits == 1) return e;
-    const int64_t grid_cap = 4 * cus;
-    if (n % 4 == 0 && ((uintptr_t)y & 15) == 0) {
-        const int64_t n4 = n / 4;
-        hipLaunchKernelGGL(split_sum4, dim3((unsigned)std::min(grid_cap, (n4 + 255) / 256)), dim3(256), 0, s,
-                           (const float4 *)part, n4, splits, (float4 *)y, n4);
-    } else {
-        hipLaunchKernelGGL(split_sum, dim3((unsigned)std::min(grid_cap, (n + 255) / 256)), dim3(256), 0, s,
-                           (const float *)part, n, splits, y, n);
-    }
-    return hipGetLastError();
+    return launch_split_sum(part, splits, y, n, cus, s);
 }
 
 template <int PREC>
@@ -1008,15 +1164,14 @@ int ng_copies(const tbh_weight &w) {
 }
 
 // Runtime-layout INT4 (one scale per (N-block, k)) with x given as p.x (bf16)
-// or p.xf (fp32), p.M = 4 or 2 (bf16 x with p.row_exp) product rows per x row:
-// 64 x 64 tiles (four waves) or 128 x 64 tiles (eight waves), split along K
-// when the tiles are fewer than the CUs.
+// or p.xf (fp32), p.M = 4 * x rows: 64 x 64 tiles (16 x rows by 64 outputs,
+// four waves) or 128 x 64 tiles (32 x rows, eight waves), split along K when
+// the tiles are fewer than the CUs.
 hipError_t launch_ngroup(const tbh_weight &w, PParams p, hipStream_t s, const Scratch &scr) {
     p.rpn = w.rows_per_nblock;
     p.nbk = (int32_t)((w.Np + w.rows_per_nblock - 1) / w.rows_per_nblock);
     const int64_t tiles = ((p.Np + 63) / 64) * ((p.M + 63) / 64);
-    // past 64 product rows (16 x rows in four pieces, 32 in two): 128 x 64
-    // tiles as 8-wave blocks,
+    // past 16 x rows (64 product rows): 128 x 64 tiles as 8-wave blocks,
     // which re-read the weights half as often (2048x5632, N-blocks of 32, us
     // per call 64 / 128 product rows: M = 64 28.1 / 24.6, M = 128 49.2 /
     // 41.0, M = 512 160.1 / 133.9, M = 2048 598 / 508); with four copies of
@@ -1096,22 +1251,20 @@ hipError_t launch_prefill(const tbh_weight &w, const uint16_t *x, int64_t ldx, i
                           int64_t ldy, hipStream_t s, const Scratch &scr) {
     if (!prefill_supported(w) || M < 1 || w.K % 8 != 0 || ldx % 8 != 0 || ((uintptr_t)x & 15) != 0)
         return hipErrorInvalidValue;
-    // runtime-layout INT4: past 64 rows every x row becomes the two f16
-    // pieces of the scaled fl(x * s), after a pass that finds each row's
-    // exponent bound (an int32 per row ahead of the split-K scratch); up to
-    // 64 rows, or when that scratch is not to be had, the three bf16 pieces
-    // and a zero row.  2048x5632, us per call, four / two pieces: M = 64 24.1
-    // / 25.2 (the extra pass), 128 40.2 / 35.9, 512 131.6 / 98.5, 2048 516 /
-    // 372.
+    // runtime-layout INT4: past 64 rows the weight-side kernel, after a pass
+    // that finds each x row's exponent bound (an int32 per row, ahead of the
+    // split-K scratch); up to 64 rows, or when that scratch is not to be had,
+    // gemm_bf16 with every x row as three bf16 pieces of fl(x * s) and a zero
+    // row.  2048x5632, us per call, pieces / weight side: M = 64 24.1 / 26.6
+    // (the extra pass), 128 40.2 / 27.4, 512 131.6 / 56.3, 2048 516 / 155.
     const bool ng = w.path == Path::Int4NGroup;
-    const bool f16x = ng && ng_x_pieces() == 2 && w.ng_sexp != nullptr;
+    const bool wside = ng && w.ng_sexp != nullptr;
     for (int64_t m0 = 0; m0 < M; m0 += kGemmRowsPerLaunch) {
         const int64_t mc = std::min(kGemmRowsPerLaunch, M - m0);
         PParams p = prefill_params(w, ldx, y + m0 * ldy, ldy);
         p.x = x + m0 * ldx;
         Scratch sub = scr;
-        int64_t pieces = ng ? 4 : 1;
-        if (f16x && mc > 64) {
+        if (wside && mc >= ng_f16_min_rows()) {
             const size_t off = ((size_t)mc * sizeof(int32_t) + 255) / 256 * 256;
             int32_t *re = (int32_t *)scr.get(s, off);
             if (re != nullptr) {
@@ -1119,11 +1272,18 @@ hipError_t launch_prefill(const tbh_weight &w, const uint16_t *x, int64_t ldx, i
                                    (int32_t)w.K, (int32_t)mc, re);
                 p.row_exp = re;
                 p.nb_exp = w.ng_sexp;
+                p.M = (int32_t)mc;
+                p.Mout = (int32_t)mc;
                 sub.offset = scr.offset + off;
-                pieces = 2;
+                const hipError_t e = launch_ngw(w, p, s, sub);
+                if (e != hipSuccess) {
+                    scr.shortfall = sub.shortfall;
+                    return e;
+                }
+                continue;
             }
         }
-        p.M = (int32_t)(pieces * mc);
+        p.M = (int32_t)((ng ? 4 : 1) * mc);
         p.Mout = (int32_t)mc;
         const hipError_t e = launch_rows(w, p, s, sub);
         if (e != hipSuccess) {
