@@ -752,15 +752,16 @@ void gemm_ngw(const PParams p) {
 
 // e[r] = the least e with |x[r][k]| < 2^e for every finite element of each
 // bf16 row of x (0 for a row with none but zeros; -126 when the largest is
-// subnormal): one wave per row.  Non-finite elements stay non-finite
-// through the scaling.  K % 8 == 0, rows 16-byte aligned.
+// subnormal): one block of 256 threads per row.  Non-finite elements stay
+// non-finite through the scaling.  K % 8 == 0, rows 16-byte aligned.
 __global__ __launch_bounds__(256) void row_exponents(const uint16_t *__restrict__ x, int64_t ldx, int32_t K,
                                                      int32_t rows, int32_t *__restrict__ e) {
-    const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    if (r >= rows) return;
+    __shared__ uint32_t wmax[4];
+    const int r = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint16_t *xr = x + (int64_t)r * ldx;
     uint32_t mx = 0;   // largest finite |x| as bf16 bits (magnitudes order as their bits)
-    for (int k = lane * 8; k < K; k += 512) {
+#pragma unroll 4
+    for (int k = threadIdx.x * 8; k < K; k += 2048) {
         const u32x4 v = *(const u32x4 *)(xr + k);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
@@ -770,7 +771,10 @@ __global__ __launch_bounds__(256) void row_exponents(const uint16_t *__restrict_
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, o));
-    if (lane == 0) {
+    if (lane == 0) wmax[wave] = mx;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        mx = max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3]));
         const int E = (int)(mx >> 7);   // exponent field
         e[r] = mx == 0 ? 0 : (E == 0 ? -126 : E - 126);
     }
@@ -1024,7 +1028,11 @@ hipError_t launch_ngw(const tbh_weight &w, PParams p, hipStream_t s, const Scrat
     constexpr int BK = 64;
     const int nsteps = (int)((p.chunks * kInt4ChunkElems + BK - 1) / BK);
     const int64_t cus = std::max(1, w.dev->cu_count);
-    const bool big = p.M > 64;
+    static const int force = [] {   // 64 or 128: the tile's x rows (lab override)
+        const char *v = std::getenv("TBH_PREFILL_NGW_ROWS");
+        return v && *v ? std::atoi(v) : 0;
+    }();
+    const bool big = force ? force == 128 : p.M > 64;
     const int64_t bm = big ? 128 : 64;
     const int64_t tiles = ((p.Np + 63) / 64) * ((p.M + bm - 1) / bm);
     const int bpc = blocks_per_cu(1);
@@ -1268,8 +1276,8 @@ hipError_t launch_prefill(const tbh_weight &w, const uint16_t *x, int64_t ldx, i
             const size_t off = ((size_t)mc * sizeof(int32_t) + 255) / 256 * 256;
             int32_t *re = (int32_t *)scr.get(s, off);
             if (re != nullptr) {
-                hipLaunchKernelGGL(row_exponents, dim3((unsigned)((mc + 3) / 4)), dim3(256), 0, s, p.x, ldx,
-                                   (int32_t)w.K, (int32_t)mc, re);
+                hipLaunchKernelGGL(row_exponents, dim3((unsigned)mc), dim3(256), 0, s, p.x, ldx, (int32_t)w.K,
+                                   (int32_t)mc, re);
                 p.row_exp = re;
                 p.nb_exp = w.ng_sexp;
                 p.M = (int32_t)mc;
