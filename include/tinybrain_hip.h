@@ -269,9 +269,13 @@ tbh_status tbh_linear_device(const tbh_weight *w, const float *x, int64_t M,
  * product computed here for x = the bf16 values widened to fp32: weight
  * operands are exact integers (INT8: q - zp, the row scale applied after
  * accumulation; INT4 K-groups: 16 (q - zp), each 32-deep MFMA's partial
- * product times its group scale; INT4 runtime layout: 16 q against x times
- * the N-block's per-k scale, rounded once in fp32 and split exactly into
- * three bf16 pieces), accumulation is fp32.  x is [M, K] row-major bf16 bits
+ * product times its group scale; INT4 runtime layout up to 64 rows: 16 q
+ * against x times the N-block's per-k scale, rounded once in fp32 and split
+ * exactly into three bf16 pieces), accumulation is fp32.  INT4 runtime
+ * layout past 64 rows runs on f16 MFMA: the dequantized weight fl(q * s),
+ * scaled by a power of two per N-block, as two f16 pieces holding it to
+ * 2^-21 of itself, against x scaled by a power of two per row (exact), with
+ * a pass over x for the row exponents in the stream's workspace.  x is [M, K] row-major bf16 bits
  * (16-byte aligned, K % 8 == 0), y is [M, N] fp32, both device pointers;
  * enqueued on `stream`.  TBH_E_UNSUPPORTED for weights outside the INT8
  * row / INT4 K-group / INT4 runtime-layout paths (tbh_weight_info.path), for
