@@ -432,9 +432,9 @@ def measure_prefill(args, backend, T, torch, workload, cpu_budget):
         roof = {"bound": "hbm", "achieved": round(byts / kern_us / 1e3, 1),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s"}
     roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
-    # runtime-layout INT4 past 64 rows (TBH_PREFILL_NG_F16_MIN) runs the
+    # runtime-layout INT4 past 64 rows (TBH_PREFILL_F16_MIN) runs the
     # weight-side kernel on the f16 MFMA
-    ngw = prec == "int4kn" and M >= int(os.environ.get("TBH_PREFILL_NG_F16_MIN") or 65)
+    ngw = prec == "int4kn" and M >= int(os.environ.get("TBH_PREFILL_F16_MIN") or 65)
     roof.update({"traffic": profiled_traffic(prec, N, K, M, "prefill"),
                  "kernel": f"{'gemm_ngw' if ngw else 'gemm_bf16'} {N}x{K} M={M} ({pool[0].path})",
                  "kernel_us": round(kern_us, 3), "alg_bytes_per_launch": byts,

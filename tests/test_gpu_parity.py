@@ -901,9 +901,9 @@ def test_prefill_split_tail_graph(backend):
     del g
 
 
-def _prefill_tile(prec, N, M, cus=256):
-    """The launch rule of tbh_prefill.hip (launch_prec), restated to show
-    which tile family and wave count each case below reaches."""
+def _prefill_tile(prec, N, M, K=0, cus=256):
+    """The launch rule of tbh_prefill.hip (launch_prec) for bf16 x, restated
+    to show which tile family and wave count each case below reaches."""
     Np = -(-N // 8) * 8
     t128 = -(-Np // 128) * -(-M // 128)
     t64x128 = -(-Np // 128) * -(-M // 64)
@@ -911,7 +911,7 @@ def _prefill_tile(prec, N, M, cus=256):
     if M >= 256:
         if t128 >= cus:
             return "128x128", 8
-        if t64 >= 2 * cus:
+        if t64 >= 2 * cus and (prec == "int8" or -(-K // 64) <= 48):
             return "64x64", 4
         return "128x128 split", 8
     if prec == "int4":
@@ -939,9 +939,18 @@ def test_prefill_bf16_int8_tiles(backend, K, N, M, tile):
 
 def test_prefill_bf16_int4_64x64(backend):
     # INT4 on 64 x 64 tiles without a K split (M >= 256, too few 128 x 128
-    # tiles for the CUs, enough 64 x 64 tiles for two per CU)
+    # tiles for the CUs, enough 64 x 64 tiles for two per CU, short rows)
     K, N, M = 2048, 5632, 512
-    assert backend.cu_count != 256 or _prefill_tile("int4", N, M) == ("64x64", 4)
+    assert backend.cu_count != 256 or _prefill_tile("int4", N, M, K) == ("64x64", 4)
+    oq = _int4_nk(137, K, N, 32)
+    _prefill_check(backend, _product(oq, (K, N), T.Layout.NK_FLAT), oq, M, seed=31)
+
+
+def test_prefill_bf16_int4_128x128_split(backend):
+    # INT4 with rows of more than 48 K steps where the same tile counts
+    # would give INT8 64 x 64 tiles: 128 x 128 tiles split along K
+    K, N, M = 5632, 2048, 1024
+    assert backend.cu_count != 256 or _prefill_tile("int4", N, M, K) == ("128x128 split", 8)
     oq = _int4_nk(137, K, N, 32)
     _prefill_check(backend, _product(oq, (K, N), T.Layout.NK_FLAT), oq, M, seed=31)
 

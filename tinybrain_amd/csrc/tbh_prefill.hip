@@ -104,6 +104,16 @@ __device__ __forceinline__ uint32_t pack_f16(float lo_elem, float hi_elem) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo_elem, hi_elem}, f16x2));
 }
 
+// One 16x16x32 MFMA of eight 16-bit operands per lane: f16 or bf16.
+template <bool F16>
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+    if constexpr (F16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                     0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
 // A 32-bit word as fp32.  By value: __builtin_bit_cast applied directly to
 // an element of an ext_vector_type value (v[1]) reads element 0.
 __device__ __forceinline__ float as_f32(uint32_t u) { return __builtin_bit_cast(float, u); }
@@ -131,6 +141,15 @@ __device__ __forceinline__ float sbyte(uint32_t w) {
 // piece 3 is zero), so the four rows a lane holds in each 16 x 16
 // accumulator tile are the pieces of one x row, and the epilogue adds them
 // into that row's output.  XF = 2: the same from bf16 x (widened exactly).
+// XF = 3 (fp32 x, INT8 rows or INT4 K-groups): two product rows per x row,
+// on the f16 MFMA: x is scaled exactly by 2^(15 - e) (e: the row's bound,
+// |x| < 2^e over its finite values, from row_exponents) and split into
+// hi = f16(x') and lo = f16(x' - hi) (the difference exact in fp32; 0 for a
+// non-finite x', which hi holds), row r = piece r % 2 of x row r / 2; the
+// weights' integers (q - zp, 16 (q - zp)) are exact in f16, and the
+// epilogue adds the two rows and scales back by 2^(e - 15).  The pieces hold
+// x' to 2^-22 of itself (2^-25 absolute below the f16 normal range); half
+// the MFMAs and staged rows of XF = 1.
 //
 // NC > 0: INT4 in the runtime layout (groups along N: one scale per
 // (N-block of rpn rows, k)).  The scale varies along K inside an MFMA, so it
@@ -152,6 +171,9 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(kFourWa
 void gemm_bf16(const PParams p) {
     static_assert(NC == 0 || (PREC == 4 && XF != 0 && !ZP), "runtime-layout INT4 stages split x, no zero points");
     static_assert(XF != 2 || NC > 0, "bf16 x is split only for runtime-layout scales");
+    static_assert(XF != 3 || NC == 0, "two f16 pieces of fp32 x take weights with exact integers");
+    constexpr int XP = XF == 3 ? 2 : 4;                     // product rows per x row (split x)
+    constexpr bool F16 = XF == 3;                           // f16 operands and MFMA
     constexpr int NCC = NC > 0 ? NC : 1;                    // copies of x in LDS
     // Steps wholly inside K and the N tile run an unmasked loop form, except
     // in INT4 blocks with K steps of 128 (256 VGPRs), which run every step
@@ -215,12 +237,19 @@ void gemm_bf16(const PParams p) {
     // fp32, one of bf16), staged as the four product rows of its pieces; with
     // runtime-layout scales an item is a (segment, copy) pair and also loads
     // the copy's 8 scales
-    constexpr int XSEGF = (BM / 4) * (BK / 8);
+    constexpr int XSEGF = (BM / XP) * (BK / 8);
     constexpr int XPTF = XF ? (XSEGF * NCC + NT - 1) / NT : 1;
     constexpr int XPTL = XF ? XPTF : XPT;
-    u32x4 xr[kDepth][XPTL][XF == 1 ? 2 : 1];
+    u32x4 xr[kDepth][XPTL][XF == 1 || XF == 3 ? 2 : 1];
     u32x4 xsc[kDepth][NC > 0 ? XPTL : 1][2];
     bool xin[kDepth][XPTL];   // segment within K, applied at the LDS store
+    // XF = 3: each item's x row, so its scaling exponent, is the same in every step
+    int xsh[XF == 3 ? XPTL : 1];
+    if constexpr (XF == 3) {
+#pragma unroll
+        for (int j = 0; j < XPTF; ++j)
+            xsh[j] = 15 - p.row_exp[min(m0 / XP + min(tid + NT * j, XSEGF - 1) / (BK / 8), p.Mout - 1)];
+    }
     u32x4 wr[kDepth][WPT];
     float sr[kDepth][WPT];
     int8_t zq[kDepth][WPT];
@@ -239,10 +268,10 @@ void gemm_bf16(const PParams p) {
                 const int i = min(tid + NT * j, XSEGF * NCC - 1);   // threads past the last item repeat it
                 const int s = NCC == 1 ? i : i % XSEGF;
                 const int qrow = s / (BK / 8), kq = s % (BK / 8);
-                const int m = min(m0 / 4 + qrow, p.Mout - 1), k = k0 + 8 * kq;
+                const int m = min(m0 / XP + qrow, p.Mout - 1), k = k0 + 8 * kq;
                 const int kk = k < p.K ? k : 0;
                 xin[d][j] = k < kend;
-                if constexpr (XF == 1) {
+                if constexpr (XF == 1 || XF == 3) {
                     const float *src = p.xf + (int64_t)m * p.ldx + kk;
                     xr[d][j][0] = *(const u32x4 *)src;
                     xr[d][j][1] = *(const u32x4 *)(src + 4);
@@ -305,6 +334,26 @@ void gemm_bf16(const PParams p) {
                 if (i < XSEGF * NCC) {
                     const int s = NCC == 1 ? i : i % XSEGF;
                     const int qrow = s / (BK / 8), kq = s % (BK / 8);
+                    if constexpr (XF == 3) {
+                        uint32_t hi[4], lo[4];
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            float a = as_f32(xr[d][j][(2 * q) / 4][(2 * q) % 4]);
+                            float b = as_f32(xr[d][j][(2 * q + 1) / 4][(2 * q + 1) % 4]);
+                            if (!xin[d][j]) a = b = 0.0f;
+                            a = __builtin_ldexpf(a, xsh[j]);
+                            b = __builtin_ldexpf(b, xsh[j]);
+                            const f16x2 h = __builtin_convertvector(f32x2{a, b}, f16x2);
+                            const f32x2 hb = __builtin_convertvector(h, f32x2);
+                            const float ra = a - hb[0], rb = b - hb[1];
+                            hi[q] = __builtin_bit_cast(uint32_t, h);
+                            lo[q] = pack_f16(__builtin_isnan(ra) ? 0.0f : ra, __builtin_isnan(rb) ? 0.0f : rb);
+                        }
+                        uint16_t *dst = &xs[bb][0][(2 * qrow) * kLdsRow + 8 * kq];
+                        *(u32x4 *)dst = u32x4{hi[0], hi[1], hi[2], hi[3]};
+                        *(u32x4 *)(dst + kLdsRow) = u32x4{lo[0], lo[1], lo[2], lo[3]};
+                        continue;
+                    }
                     float pc[8][3];
 #pragma unroll
                     for (int h = 0; h < 8; ++h) {
@@ -357,8 +406,8 @@ void gemm_bf16(const PParams p) {
                         const float f1 = sbyte<2>(w) - zf;
                         const float f2 = sbyte<1>(w) - zf;
                         const float f3 = sbyte<3>(w) - zf;
-                        o[2 * q] = pack_hi16(f0, f1);
-                        o[2 * q + 1] = pack_hi16(f2, f3);
+                        o[2 * q] = F16 ? pack_f16(f0, f1) : pack_hi16(f0, f1);
+                        o[2 * q + 1] = F16 ? pack_f16(f2, f3) : pack_hi16(f2, f3);
                     }
                     *(u32x4 *)dst = u32x4{o[0], o[1], o[2], o[3]};
                     *(u32x4 *)(dst + 8) = u32x4{o[4], o[5], o[6], o[7]};
@@ -375,10 +424,17 @@ void gemm_bf16(const PParams p) {
                         const uint32_t hi = w & 0xF0F0F0F0u;          // bytes: k + {2, 6, 3, 7}
                         const uint32_t lo = (w << 4) & 0xF0F0F0F0u;   // bytes: k + {0, 4, 1, 5}
                         uint32_t o[4];
-                        o[0] = pack_hi16(sbyte<0>(lo) - zf, sbyte<2>(lo) - zf);
-                        o[1] = pack_hi16(sbyte<0>(hi) - zf, sbyte<2>(hi) - zf);
-                        o[2] = pack_hi16(sbyte<1>(lo) - zf, sbyte<3>(lo) - zf);
-                        o[3] = pack_hi16(sbyte<1>(hi) - zf, sbyte<3>(hi) - zf);
+                        if constexpr (F16) {
+                            o[0] = pack_f16(sbyte<0>(lo) - zf, sbyte<2>(lo) - zf);
+                            o[1] = pack_f16(sbyte<0>(hi) - zf, sbyte<2>(hi) - zf);
+                            o[2] = pack_f16(sbyte<1>(lo) - zf, sbyte<3>(lo) - zf);
+                            o[3] = pack_f16(sbyte<1>(hi) - zf, sbyte<3>(hi) - zf);
+                        } else {
+                            o[0] = pack_hi16(sbyte<0>(lo) - zf, sbyte<2>(lo) - zf);
+                            o[1] = pack_hi16(sbyte<0>(hi) - zf, sbyte<2>(hi) - zf);
+                            o[2] = pack_hi16(sbyte<1>(lo) - zf, sbyte<3>(lo) - zf);
+                            o[3] = pack_hi16(sbyte<1>(hi) - zf, sbyte<3>(hi) - zf);
+                        }
                         *(u32x4 *)(dst + 8 * q) = u32x4{o[0], o[1], o[2], o[3]};
                     }
                     if constexpr (NC == 0) ssc[bb][s] = sr[d][j];
@@ -421,13 +477,12 @@ void gemm_bf16(const PParams p) {
                 if (PREC == 8 || NC > 0) {
 #pragma unroll
                     for (int a = 0; a < TM; ++a)
-                        acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[a], bfr, acc[a][b], 0, 0, 0);
+                        acc[a][b] = mfma16<F16>(af[a], bfr, acc[a][b]);
                 } else {
                     const float sc = ssc[bb][wrow * CPR + ks];
 #pragma unroll
                     for (int a = 0; a < TM; ++a) {
-                        const f32x4 part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            af[a], bfr, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                        const f32x4 part = mfma16<F16>(af[a], bfr, f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
                         for (int e = 0; e < 4; ++e) acc[a][b][e] = __builtin_fmaf(part[e], sc, acc[a][b][e]);
                     }
@@ -509,6 +564,26 @@ void gemm_bf16(const PParams p) {
     // ---- epilogue: lane holds C[4 (lane / 16) + e][lane % 16] of each tile
     float *out = p.y + (int64_t)blockIdx.z * p.split_stride;
     const int mrow = m0 + wm * WM + 4 * (lane >> 4), ncol = n0 + wn * WN + (lane & 15);
+    if constexpr (XF == 3) {
+        // the lane's four rows are the two pieces of x rows (mrow + 16 a) / 2
+        // and the next
+#pragma unroll
+        for (int b = 0; b < TN; ++b) {
+            const int n = ncol + b * 16;
+            if (n >= p.N) continue;
+#pragma unroll
+            for (int a = 0; a < TM; ++a) {
+                const int m = (mrow + a * 16) >> 1;
+                if (m < p.Mout)
+                    out[(int64_t)m * p.ldy + n] =
+                        __builtin_ldexpf(acc[a][b][0] + acc[a][b][1], p.row_exp[m] - 15) * scn[b];
+                if (m + 1 < p.Mout)
+                    out[(int64_t)(m + 1) * p.ldy + n] =
+                        __builtin_ldexpf(acc[a][b][2] + acc[a][b][3], p.row_exp[m + 1] - 15) * scn[b];
+            }
+        }
+        return;
+    }
     if constexpr (XF) {
         // the lane's four rows are the pieces of x row (mrow + 16 a) / 4
 #pragma unroll
@@ -751,22 +826,30 @@ void gemm_ngw(const PParams p) {
 }
 
 // e[r] = the least e with |x[r][k]| < 2^e for every finite element of each
-// bf16 row of x (0 for a row with none but zeros; -126 when the largest is
-// subnormal): one block of 256 threads per row.  Non-finite elements stay
-// non-finite through the scaling.  K % 8 == 0, rows 16-byte aligned.
-__global__ __launch_bounds__(256) void row_exponents(const uint16_t *__restrict__ x, int64_t ldx, int32_t K,
+// row of x, bf16 bits (F32 = false) or fp32 (0 for a row with none but
+// zeros; -126 when the largest is subnormal): one block of 256 threads per
+// row.  Non-finite elements stay non-finite through the scaling.  Rows
+// 16-byte aligned, K a multiple of the 16-byte segment.
+template <bool F32>
+__global__ __launch_bounds__(256) void row_exponents(const void *__restrict__ xv, int64_t ldx, int32_t K,
                                                      int32_t rows, int32_t *__restrict__ e) {
+    constexpr int EPS = F32 ? 4 : 8;   // elements per 16-byte segment
     __shared__ uint32_t wmax[4];
     const int r = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint16_t *xr = x + (int64_t)r * ldx;
-    uint32_t mx = 0;   // largest finite |x| as bf16 bits (magnitudes order as their bits)
+    const char *xr = (const char *)xv + (int64_t)r * ldx * (F32 ? 4 : 2);
+    uint32_t mx = 0;   // largest finite |x| as bits (magnitudes order as their bits)
 #pragma unroll 4
-    for (int k = threadIdx.x * 8; k < K; k += 2048) {
-        const u32x4 v = *(const u32x4 *)(xr + k);
+    for (int k = threadIdx.x * EPS; k < K; k += 256 * EPS) {
+        const u32x4 v = *(const u32x4 *)(xr + (int64_t)k * (F32 ? 4 : 2));
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            const uint32_t lo = v[c] & 0x7FFFu, hi = (v[c] >> 16) & 0x7FFFu;
-            mx = max(mx, max(lo < 0x7F80u ? lo : 0u, hi < 0x7F80u ? hi : 0u));
+            if constexpr (F32) {
+                const uint32_t a = v[c] & 0x7FFFFFFFu;
+                mx = max(mx, a < 0x7F800000u ? a : 0u);
+            } else {
+                const uint32_t lo = v[c] & 0x7FFFu, hi = (v[c] >> 16) & 0x7FFFu;
+                mx = max(mx, max(lo < 0x7F80u ? lo : 0u, hi < 0x7F80u ? hi : 0u));
+            }
         }
     }
 #pragma unroll
@@ -775,7 +858,7 @@ __global__ __launch_bounds__(256) void row_exponents(const uint16_t *__restrict_
     __syncthreads();
     if (threadIdx.x == 0) {
         mx = max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3]));
-        const int E = (int)(mx >> 7);   // exponent field
+        const int E = (int)(mx >> (F32 ? 23 : 7));   // exponent field
         e[r] = mx == 0 ? 0 : (E == 0 ? -126 : E - 126);
     }
 }
@@ -950,12 +1033,26 @@ hipError_t launch_tail(Kern kern, int threads, dim3 grid, PParams p, const TailR
     return hipLaunchKernel((const void *)kern, grid, dim3(threads), args, 0, s);
 }
 
-// Fewest x rows of bf16 x that runtime-layout INT4 weights take on the
-// weight-side kernel (gemm_ngw; TBH_PREFILL_NG_F16_MIN); fewer rows go to
-// gemm_bf16 with x split into three bf16 pieces and a zero row per N-block.
-int64_t ng_f16_min_rows() {
+// Product rows per fp32 x row for INT8-row and INT4 K-group weights: 2 (f16
+// pieces, XF = 3) unless TBH_PREFILL_F32_PIECES=4 asks for three bf16 pieces
+// and a zero row (XF = 1).
+int f32_x_pieces() {
+    static const int v = [] {
+        const char *e = std::getenv("TBH_PREFILL_F32_PIECES");
+        return e && std::atoi(e) == 4 ? 4 : 2;
+    }();
+    return v;
+}
+
+// Fewest x rows that take the f16 forms, which need a pass over x for the
+// row exponents (TBH_PREFILL_F16_MIN): bf16 x on runtime-layout INT4
+// (gemm_ngw) and fp32 x on INT8 rows or INT4 K-groups (gemm_bf16, XF = 3).
+// Fewer rows go to the three-bf16-piece forms, whose time the extra launch
+// would exceed (2048x5632 at M = 64, us: runtime layout 24.1 / 26.6, fp32 x
+// INT4 K-groups 20.2 / 21.8, INT8 20.3 / 20.7).
+int64_t f16_min_rows() {
     static const int64_t v = [] {
-        const char *e = std::getenv("TBH_PREFILL_NG_F16_MIN");
+        const char *e = std::getenv("TBH_PREFILL_F16_MIN");
         return e && *e ? std::max<int64_t>(1, std::atoll(e)) : (int64_t)65;
     }();
     return v;
@@ -974,7 +1071,15 @@ hipError_t launch_tile(const PParams &p, int splits, hipStream_t s, const TailRe
         else hipLaunchKernelGGL((gemm_bf16<4, BM, BN, false, WVN, BK, 2, NC>), grid, dim3(64 * WVN), 0, s, p);
     } else {
         const bool w8 = waves == 8 || (waves != 4 && BN == 128 && (p.M >= 256 || PREC == 4));
-        if (p.xf) {   // fp32 x
+        if (p.xf && p.row_exp) {   // fp32 x as two f16 pieces
+            if (p.zp) {
+                if (w8) hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, true, 8, BK, 3, 0>), grid, dim3(512), 0, s, p);
+                else hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, true, 4, BK, 3, 0>), grid, dim3(256), 0, s, p);
+            } else {
+                if (w8) hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, false, 8, BK, 3, 0>), grid, dim3(512), 0, s, p);
+                else hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, false, 4, BK, 3, 0>), grid, dim3(256), 0, s, p);
+            }
+        } else if (p.xf) {   // fp32 x as three bf16 pieces and a zero row
             if (p.zp) {
                 if (w8) hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, true, 8, BK, 1, 0>), grid, dim3(512), 0, s, p);
                 else hipLaunchKernelGGL((gemm_bf16<PREC, BM, BN, true, 4, BK, 1, 0>), grid, dim3(256), 0, s, p);
@@ -1137,10 +1242,17 @@ hipError_t launch_prec(const tbh_weight &w, const PParams &p, hipStream_t s, con
         // 84.1 us.  INT8 launches measured slower with 128 (M = 512 on 64 x 64
         // tiles 31.7 -> 33.6 us, M = 2048 79.0 -> 79.9 us), and the split INT4
         // launch at M = 512 no faster (32.4 -> 32.8 us).
+        // INT4 takes 64 x 64 tiles only with bf16 x and short rows, else the
+        // split 128 x 128 tiles (us, 64 x 64 / 128 x 128 split: bf16 x,
+        // 5632x2048 (32 K steps) M = 512 36.0 / 41.8, 2048x5632 (88 steps) at
+        // 1024 rows 74.1 / 47.6; fp32 x in two f16 pieces, 5632x2048 M = 512
+        // 90.9 / 74.6, 2048x5632 M = 512 101.8 / 58.2).
         if (t128 >= cus)
             return PREC == 4 ? launch_split<PREC, 128, 128, 128>(w, p, t128, 1, s, scr)
                              : launch_split<PREC, 128, 128>(w, p, t128, 1, s, scr);
-        if (t64 >= 2 * cus) return launch_split<PREC, 64, 64>(w, p, t64, 2, s, scr);
+        const int64_t steps64 = (p.chunks * (int64_t)(PREC == 8 ? kInt8ChunkElems : kInt4ChunkElems) + 63) / 64;
+        if (t64 >= 2 * cus && (PREC == 8 || (!p.xf && steps64 <= 48)))
+            return launch_split<PREC, 64, 64>(w, p, t64, 2, s, scr);
         return launch_split<PREC, 128, 128>(w, p, t128, 1, s, scr);
     }
     // Fewer rows (HBM-bound).  INT4, whose K steps carry a group scale per
@@ -1243,14 +1355,40 @@ hipError_t launch_prefill_f32(const tbh_weight &w, const float *x, int64_t ldx, 
                               int64_t ldy, hipStream_t s, const Scratch &scr) {
     if (!prefill_supported(w) || M < 1 || w.K % 8 != 0 || ldx % 4 != 0 || ((uintptr_t)x & 15) != 0)
         return hipErrorInvalidValue;
+    // INT8 rows and INT4 K-groups past 64 rows: every x row becomes two f16
+    // pieces scaled by a power of two per row, after a pass that finds each
+    // row's exponent bound (an int32 per row, ahead of the split-K scratch);
+    // fewer rows, runtime-layout INT4, or a workspace that cannot grow (graph
+    // capture before any eager call) take three bf16 pieces and a zero row.
+    // us per call, four / two pieces: INT8 5632x2048 M = 512 70.8 / 52.5,
+    // 2048 253 / 166; INT4 2048x5632 M = 128 29.3 / 25.8, 512 79.9 / 58.7,
+    // 2048 315 / 189.
+    const bool two = w.path != Path::Int4NGroup && f32_x_pieces() == 2;
     for (int64_t m0 = 0; m0 < M; m0 += kGemmRowsPerLaunch) {
         const int64_t mc = std::min(kGemmRowsPerLaunch, M - m0);
         PParams p = prefill_params(w, ldx, y + m0 * ldy, ldy);
         p.xf = x + m0 * ldx;
-        p.M = (int32_t)(4 * mc);    // three bf16 pieces and a zero row per x row
+        Scratch sub = scr;
+        int64_t pieces = 4;
+        if (two && mc >= f16_min_rows()) {
+            const size_t off = ((size_t)mc * sizeof(int32_t) + 255) / 256 * 256;
+            int32_t *re = (int32_t *)scr.get(s, off);
+            if (re == nullptr && scr.is_fixed()) return hipErrorOutOfMemory;
+            if (re != nullptr) {
+                hipLaunchKernelGGL(row_exponents<true>, dim3((unsigned)mc), dim3(256), 0, s, (const void *)p.xf, ldx,
+                                   (int32_t)w.K, (int32_t)mc, re);
+                p.row_exp = re;
+                sub.offset = scr.offset + off;
+                pieces = 2;
+            }
+        }
+        p.M = (int32_t)(pieces * mc);
         p.Mout = (int32_t)mc;
-        const hipError_t e = launch_rows(w, p, s, scr);
-        if (e != hipSuccess) return e;
+        const hipError_t e = launch_rows(w, p, s, sub);
+        if (e != hipSuccess) {
+            scr.shortfall = sub.shortfall;
+            return e;
+        }
     }
     return hipSuccess;
 }
@@ -1272,12 +1410,12 @@ hipError_t launch_prefill(const tbh_weight &w, const uint16_t *x, int64_t ldx, i
         PParams p = prefill_params(w, ldx, y + m0 * ldy, ldy);
         p.x = x + m0 * ldx;
         Scratch sub = scr;
-        if (wside && mc >= ng_f16_min_rows()) {
+        if (wside && mc >= f16_min_rows()) {
             const size_t off = ((size_t)mc * sizeof(int32_t) + 255) / 256 * 256;
             int32_t *re = (int32_t *)scr.get(s, off);
             if (re != nullptr) {
-                hipLaunchKernelGGL(row_exponents, dim3((unsigned)mc), dim3(256), 0, s, p.x, ldx, (int32_t)w.K,
-                                   (int32_t)mc, re);
+                hipLaunchKernelGGL(row_exponents<false>, dim3((unsigned)mc), dim3(256), 0, s, (const void *)p.x, ldx,
+                                   (int32_t)w.K, (int32_t)mc, re);
                 p.row_exp = re;
                 p.nb_exp = w.ng_sexp;
                 p.M = (int32_t)mc;
