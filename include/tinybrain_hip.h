@@ -211,7 +211,9 @@ tbh_status tbh_weight_get_info(const tbh_weight *w, tbh_weight_info *info);
  * outputs (16, 32 or a multiple of 64 rows, or one block) run on the bf16
  * MFMA GEMM with every fp32 x row split exactly into three bf16 pieces (for
  * the runtime layout, x times the N-block's per-k scale, one fp32 rounding,
- * then split).  The GEMV kernels stage a row of
+ * then split); past 64 rows INT8 rows and INT4 K-groups take x as two f16
+ * pieces, scaled by a power of two per row, holding it to 2^-22 of the row's
+ * largest element, on the f16 MFMA.  The GEMV kernels stage a row of
  * x in LDS, so a K past about 13 K (INT8) or 14.5 K (INT4) elements runs on
  * the MFMA GEMM at every M (runtime-layout INT4 of such a K keeps the
  * reference's flat array and runs on the generic kernel); a long K that is

@@ -715,12 +715,62 @@ def test_fp32_mfma_exact_split(backend, mfma_from):
     assert float(rel.max()) < 3e-5
 
 
-def test_fp32_mfma_device_and_graph(backend):
-    # tbh_matmul_device through the rule (M = 64): bit-identical across calls
+@pytest.mark.parametrize("kind", ["int8", "int4", "int8_zp"])
+def test_fp32_mfma_f16_pieces(backend, kind):
+    # past 64 rows fp32 x goes to the GEMM as two f16 pieces scaled by a
+    # power of two per row: rows across the exponent range with all 24
+    # significant bits in use, a row mixing magnitudes 2^-30..2^30, zero rows
+    # and rows holding infinities or NaN (whose NaN and signed-infinity
+    # pattern must equal the float64 product's)
+    K, N, M = 512, 256, 80
+    if kind == "int4":
+        qt = _int4_nk(183, K, N, 32)
+        pq = _product(qt, (K, N), T.Layout.NK_FLAT)
+    else:
+        qt = _int8_pc(183, K, N)
+        if kind == "int8_zp":
+            qt.zero_points = ((np.arange(N) % 9) - 4).astype(np.int8)
+        pq = _product(qt, (K, N))
+    W = _oracle_weight(qt, pq.layout)
+    rng = np.random.default_rng(184)
+    mant = rng.integers(1 << 23, 1 << 24, size=(M, K)).astype(np.float64) / (1 << 23)
+    sign = np.where(rng.random((M, K)) < 0.5, -1.0, 1.0)
+    expo = rng.integers(-60, 60, size=(M, 1)).astype(np.float64) * np.ones((1, K))
+    expo[6], expo[7] = 100, -100
+    expo[8] = rng.integers(-30, 31, size=K)
+    x = (sign * mant * np.exp2(expo)).astype(np.float32)
+    x[3] = 0.0
+    x[5, ::2] = 0.0
+    x[10, 17] = np.inf
+    x[11, 3], x[11, 40] = -np.inf, 2.5e38
+    x[12, 9] = np.nan
+    y = backend.matmulQuantized(x, pq)
+    with np.errstate(invalid="ignore", over="ignore"):
+        y64 = O.gemm_f64(x, W)
+    for m in (10, 11, 12):
+        np.testing.assert_array_equal(np.isnan(y[m]), np.isnan(y64[m]), err_msg=str(m))
+        np.testing.assert_array_equal(np.isposinf(y[m]), np.isposinf(y64[m]), err_msg=str(m))
+        np.testing.assert_array_equal(np.isneginf(y[m]), np.isneginf(y64[m]), err_msg=str(m))
+    fin = [m for m in range(M) if m not in (10, 11, 12)]
+    for m in fin:
+        assert O.parity_errors(y[m:m + 1], y64[m:m + 1])["gated"] <= GATE, m
+    assert np.all(y[3] == 0.0)
+    # error against sum_k |x_k w_kn|: the pieces hold x to 2^-22 of the
+    # row's largest element, below fp32 accumulation's sqrt(K) 2^-24
+    mag = np.abs(x[fin].astype(np.float64)) @ np.abs(W.astype(np.float64))
+    with np.errstate(invalid="ignore"):
+        rel = np.where(mag > 0, np.abs(y[fin] - y64[fin]) / mag, 0.0)
+    assert float(rel.max()) < 3e-5
+
+
+@pytest.mark.parametrize("M", [64, 96])
+def test_fp32_mfma_device_and_graph(backend, M):
+    # tbh_matmul_device through the rule (M = 64: three bf16 pieces; 96: two
+    # f16 pieces after the row-exponent pass): bit-identical across calls
     # and graph replays, equal to the host entry point
     import torch
 
-    K, N, M = 2048, 2048, 64
+    K, N = 2048, 2048
     oq = _int4_nk(191, K, N, 32)
     pq = _product(oq, (K, N), T.Layout.NK_FLAT)
     w = backend.weight(pq)

@@ -215,8 +215,9 @@ hipError_t launch_prefill(const tbh_weight &w, const uint16_t *x, int64_t ldx, i
 // The same GEMM for fp32 x [M][ldx] (16-byte aligned rows, K % 8 == 0):
 // each x row is split exactly into three bf16 pieces and a zero
 // row, the four rows go through the bf16 MFMAs, and the epilogue adds each
-// row's four results (tbh_prefill.hip).  hipErrorInvalidValue for weights or
-// shapes it does not take.
+// row's four results; past 64 rows of INT8-row or INT4 K-group weights, two
+// f16 pieces of x scaled per row on the f16 MFMA (tbh_prefill.hip).
+// hipErrorInvalidValue for weights or shapes it does not take.
 hipError_t launch_prefill_f32(const tbh_weight &w, const float *x, int64_t ldx, int64_t M, float *y,
                               int64_t ldy, hipStream_t s, const Scratch &scr);
 
