@@ -660,16 +660,22 @@ __device__ __forceinline__ float lo_piece(float w, float r) {
 // the x elements: at 2048x5632, N-blocks of 32, two f16 pieces of x took 99
 // / 373 us at M = 512 / 2048 against 56 / 155 us here.)
 //
-// Tiles BM x rows by BN outputs, WV waves as 2 x (WV / 2), K steps of 64 in
-// two LDS buffers with a two-step register ring (the gemm_bf16 loop); K
-// split z of p.split_steps steps writes p.y + z * p.split_stride.
-template <int BM, int BN, int WV>
+// fp32 x (F32, p.xf): two product rows per x row, the f16 pieces hi =
+// f16(x') and lo = f16(x' - hi) of x' = x 2^(15 - er) (to 2^-22 of the
+// row's largest element; 0 in lo for a non-finite x', which hi holds), so
+// four MFMAs per x fragment and weight; the epilogue adds the two rows.
+//
+// Tiles BM product rows by BN outputs, WV waves as 2 x (WV / 2), K steps of
+// 64 in two LDS buffers with a two-step register ring (the gemm_bf16 loop);
+// K split z of p.split_steps steps writes p.y + z * p.split_stride.
+template <int BM, int BN, int WV, bool F32>
 __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(WV == 8 ? 4 : 1)))
 void gemm_ngw(const PParams p) {
     constexpr int BK = 64, kLdsRow = BK + kRowPad;
     constexpr int NT = 64 * WV, WC = WV / 2;
     constexpr int WM = BM / 2, WN = BN / WC, TM = WM / 16, TN = WN / 16;
-    constexpr int XSEG = BM * (BK / 8), XPT = XSEG / NT;   // x: 8-element segments per step
+    constexpr int XP = F32 ? 2 : 1;                          // product rows per x row
+    constexpr int XSEG = (BM / XP) * (BK / 8), XPT = XSEG / NT;   // x: 8-element segments per step
     constexpr int WIT = BN * (BK / 8), WPT = WIT / NT;     // weights: 8-k words per step
     static_assert(XSEG % NT == 0 && WIT % NT == 0 && TM >= 1 && TN >= 1, "tile too small for the waves");
 
@@ -688,11 +694,11 @@ void gemm_ngw(const PParams p) {
     // each item's row is the same in every step, so its scaling exponent is too
     int xsh[XPT], wsh[WPT];
 #pragma unroll
-    for (int j = 0; j < XPT; ++j) xsh[j] = 15 - p.row_exp[min(m0 + (tid + NT * j) / (BK / 8), p.Mout - 1)];
+    for (int j = 0; j < XPT; ++j) xsh[j] = 15 - p.row_exp[min(m0 / XP + (tid + NT * j) / (BK / 8), p.Mout - 1)];
 #pragma unroll
     for (int j = 0; j < WPT; ++j) wsh[j] = 8 - p.nb_exp[min(n0 + (tid + NT * j) / (BK / 8), p.Np - 1) / p.rpn];
 
-    u32x4 xr[kDepth][XPT];
+    u32x4 xr[kDepth][XPT][XP];
     bool xin[kDepth][XPT];
     uint32_t wr[kDepth][WPT];
     u32x4 sr[kDepth][WPT][2];
@@ -701,9 +707,16 @@ void gemm_ngw(const PParams p) {
 #pragma unroll
         for (int j = 0; j < XPT; ++j) {
             const int s = tid + NT * j, row = s / (BK / 8), k = k0 + 8 * (s % (BK / 8));
-            const int m = min(m0 + row, p.Mout - 1);   // rows past M read row M - 1 (never stored)
+            const int m = min(m0 / XP + row, p.Mout - 1);   // rows past M read row M - 1 (never stored)
+            const int kk = k < p.K ? k : 0;
             xin[d][j] = k < kend;
-            xr[d][j] = *(const u32x4 *)(p.x + (int64_t)m * p.ldx + (k < p.K ? k : 0));
+            if constexpr (F32) {
+                const float *src = p.xf + (int64_t)m * p.ldx + kk;
+                xr[d][j][0] = *(const u32x4 *)src;
+                xr[d][j][1] = *(const u32x4 *)(src + 4);
+            } else {
+                xr[d][j][0] = *(const u32x4 *)(p.x + (int64_t)m * p.ldx + kk);
+            }
         }
 #pragma unroll
         for (int j = 0; j < WPT; ++j) {
@@ -722,15 +735,34 @@ void gemm_ngw(const PParams p) {
 #pragma unroll
         for (int j = 0; j < XPT; ++j) {
             const int s = tid + NT * j, row = s / (BK / 8), kq = s % (BK / 8);
-            uint32_t o[4];
+            if constexpr (F32) {
+                uint32_t hi[4], lo[4];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint32_t wv = xr[d][j][q];   // bf16 elements 2q (low half), 2q + 1
-                const float a = xin[d][j] ? as_f32(wv << 16) : 0.0f;
-                const float b = xin[d][j] ? as_f32(wv & 0xFFFF0000u) : 0.0f;
-                o[q] = pack_f16(__builtin_ldexpf(a, xsh[j]), __builtin_ldexpf(b, xsh[j]));
+                for (int q = 0; q < 4; ++q) {
+                    float a = as_f32(xr[d][j][q / 2][(2 * q) % 4]), b = as_f32(xr[d][j][q / 2][(2 * q + 1) % 4]);
+                    if (!xin[d][j]) a = b = 0.0f;
+                    a = __builtin_ldexpf(a, xsh[j]);
+                    b = __builtin_ldexpf(b, xsh[j]);
+                    const f16x2 h = __builtin_convertvector(f32x2{a, b}, f16x2);
+                    const f32x2 hb = __builtin_convertvector(h, f32x2);
+                    const float ra = a - hb[0], rb = b - hb[1];
+                    hi[q] = __builtin_bit_cast(uint32_t, h);
+                    lo[q] = pack_f16(__builtin_isnan(ra) ? 0.0f : ra, __builtin_isnan(rb) ? 0.0f : rb);
+                }
+                uint16_t *dst = &xs[bb][(2 * row) * kLdsRow + 8 * kq];
+                *(u32x4 *)dst = u32x4{hi[0], hi[1], hi[2], hi[3]};
+                *(u32x4 *)(dst + kLdsRow) = u32x4{lo[0], lo[1], lo[2], lo[3]};
+            } else {
+                uint32_t o[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const uint32_t wv = xr[d][j][0][q];   // bf16 elements 2q (low half), 2q + 1
+                    const float a = xin[d][j] ? as_f32(wv << 16) : 0.0f;
+                    const float b = xin[d][j] ? as_f32(wv & 0xFFFF0000u) : 0.0f;
+                    o[q] = pack_f16(__builtin_ldexpf(a, xsh[j]), __builtin_ldexpf(b, xsh[j]));
+                }
+                *(u32x4 *)&xs[bb][row * kLdsRow + 8 * kq] = u32x4{o[0], o[1], o[2], o[3]};
             }
-            *(u32x4 *)&xs[bb][row * kLdsRow + 8 * kq] = u32x4{o[0], o[1], o[2], o[3]};
         }
 #pragma unroll
         for (int j = 0; j < WPT; ++j) {
@@ -816,12 +848,22 @@ void gemm_ngw(const PParams p) {
         if (n >= p.N) continue;
         const int eb = p.nb_exp[n / p.rpn] - 27;
 #pragma unroll
-        for (int a = 0; a < TM; ++a)
+        for (int a = 0; a < TM; ++a) {
+            if constexpr (F32) {   // rows e = 0, 1: the pieces of x row (mrow + 16 a) / 2; e = 2, 3: the next
+                const int m = (mrow + a * 16) >> 1;
+                if (m < p.Mout)
+                    out[(int64_t)m * p.ldy + n] = __builtin_ldexpf(acc[a][b][0] + acc[a][b][1], eb + p.row_exp[m]);
+                if (m + 1 < p.Mout)
+                    out[(int64_t)(m + 1) * p.ldy + n] =
+                        __builtin_ldexpf(acc[a][b][2] + acc[a][b][3], eb + p.row_exp[m + 1]);
+            } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int m = mrow + a * 16 + e;
-                if (m < p.Mout) out[(int64_t)m * p.ldy + n] = __builtin_ldexpf(acc[a][b][e], eb + p.row_exp[m]);
+                for (int e = 0; e < 4; ++e) {
+                    const int m = mrow + a * 16 + e;
+                    if (m < p.Mout) out[(int64_t)m * p.ldy + n] = __builtin_ldexpf(acc[a][b][e], eb + p.row_exp[m]);
+                }
             }
+        }
     }
 }
 
@@ -1124,16 +1166,17 @@ hipError_t launch_split_sum(const float *part, int splits, float *y, int64_t n, 
     return hipGetLastError();
 }
 
-// Runtime-layout INT4 with bf16 x on the weight-side kernel (p.row_exp set,
-// p.M = x rows): 128 x 64 tiles as 8-wave blocks past 64 rows, else 64 x 64
-// as 4-wave blocks, split along K to a block per CU.
+// Runtime-layout INT4 on the weight-side kernel (p.row_exp set; bf16 x with
+// p.M = x rows, or fp32 x with p.M = 2 x rows): 128 x 64 tiles as 8-wave
+// blocks past 64 product rows, else 64 x 64 as 4-wave blocks, split along K
+// to a block per CU.
 hipError_t launch_ngw(const tbh_weight &w, PParams p, hipStream_t s, const Scratch &scr) {
     p.rpn = w.rows_per_nblock;
     p.nbk = (int32_t)((w.Np + w.rows_per_nblock - 1) / w.rows_per_nblock);
     constexpr int BK = 64;
     const int nsteps = (int)((p.chunks * kInt4ChunkElems + BK - 1) / BK);
     const int64_t cus = std::max(1, w.dev->cu_count);
-    static const int force = [] {   // 64 or 128: the tile's x rows (lab override)
+    static const int force = [] {   // 64 or 128: the tile's product rows (lab override)
         const char *v = std::getenv("TBH_PREFILL_NGW_ROWS");
         return v && *v ? std::atoi(v) : 0;
     }();
@@ -1165,8 +1208,13 @@ hipError_t launch_ngw(const tbh_weight &w, PParams p, hipStream_t s, const Scrat
         p.split_stride = n;
     }
     const dim3 grid((unsigned)((p.Np + 63) / 64), (unsigned)((p.M + bm - 1) / bm), (unsigned)splits);
-    if (big) hipLaunchKernelGGL((gemm_ngw<128, 64, 8>), grid, dim3(512), 0, s, p);
-    else hipLaunchKernelGGL((gemm_ngw<64, 64, 4>), grid, dim3(256), 0, s, p);
+    if (p.xf) {
+        if (big) hipLaunchKernelGGL((gemm_ngw<128, 64, 8, true>), grid, dim3(512), 0, s, p);
+        else hipLaunchKernelGGL((gemm_ngw<64, 64, 4, true>), grid, dim3(256), 0, s, p);
+    } else {
+        if (big) hipLaunchKernelGGL((gemm_ngw<128, 64, 8, false>), grid, dim3(512), 0, s, p);
+        else hipLaunchKernelGGL((gemm_ngw<64, 64, 4, false>), grid, dim3(256), 0, s, p);
+    }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess || splits == 1) return e;
     return launch_split_sum(part, splits, y, n, cus, s);
@@ -1355,15 +1403,17 @@ hipError_t launch_prefill_f32(const tbh_weight &w, const float *x, int64_t ldx, 
                               int64_t ldy, hipStream_t s, const Scratch &scr) {
     if (!prefill_supported(w) || M < 1 || w.K % 8 != 0 || ldx % 4 != 0 || ((uintptr_t)x & 15) != 0)
         return hipErrorInvalidValue;
-    // INT8 rows and INT4 K-groups past 64 rows: every x row becomes two f16
-    // pieces scaled by a power of two per row, after a pass that finds each
-    // row's exponent bound (an int32 per row, ahead of the split-K scratch);
-    // fewer rows, runtime-layout INT4, or a workspace that cannot grow (graph
-    // capture before any eager call) take three bf16 pieces and a zero row.
+    // Past 64 rows every x row becomes two f16 pieces scaled by a power of two
+    // per row, after a pass that finds each row's exponent bound (an int32 per
+    // row, ahead of the split-K scratch), for gemm_bf16 (INT8 rows, INT4
+    // K-groups) or the weight-side gemm_ngw (runtime-layout INT4); fewer rows,
+    // or a workspace that cannot grow (graph capture before any eager call),
+    // take three bf16 pieces and a zero row.
     // us per call, four / two pieces: INT8 5632x2048 M = 512 70.8 / 52.5,
     // 2048 253 / 166; INT4 2048x5632 M = 128 29.3 / 25.8, 512 79.9 / 58.7,
     // 2048 315 / 189.
-    const bool two = w.path != Path::Int4NGroup && f32_x_pieces() == 2;
+    const bool ng = w.path == Path::Int4NGroup;
+    const bool two = f32_x_pieces() == 2 && (!ng || w.ng_sexp != nullptr);
     for (int64_t m0 = 0; m0 < M; m0 += kGemmRowsPerLaunch) {
         const int64_t mc = std::min(kGemmRowsPerLaunch, M - m0);
         PParams p = prefill_params(w, ldx, y + m0 * ldy, ldy);
@@ -1384,7 +1434,13 @@ hipError_t launch_prefill_f32(const tbh_weight &w, const float *x, int64_t ldx, 
         }
         p.M = (int32_t)(pieces * mc);
         p.Mout = (int32_t)mc;
-        const hipError_t e = launch_rows(w, p, s, sub);
+        hipError_t e;
+        if (ng && pieces == 2) {   // runtime layout: the weight-side kernel, x in two f16 pieces
+            p.nb_exp = w.ng_sexp;
+            e = launch_ngw(w, p, s, sub);
+        } else {
+            e = launch_rows(w, p, s, sub);
+        }
         if (e != hipSuccess) {
             scr.shortfall = sub.shortfall;
             return e;
