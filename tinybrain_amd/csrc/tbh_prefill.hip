@@ -656,9 +656,9 @@ __device__ __forceinline__ float lo_piece(float w, float r) {
 // sum(x' hi + x' lo).  The pieces hold w' to 2^-21 of itself, and to 2^-24
 // absolute below the f16 normal range.  Each weight element and each x
 // element is staged once per tile.  (Scaling and splitting x instead, once
-// per N-block of a tile, as gemm_bf16 does for fp32 x, stages N / rpn times
-// the x elements: at 2048x5632, N-blocks of 32, two f16 pieces of x took 99
-// / 373 us at M = 512 / 2048 against 56 / 155 us here.)
+// per N-block of a tile, as gemm_bf16 does up to 64 rows, stages N / rpn
+// times the x elements: at 2048x5632, N-blocks of 32, two f16 pieces of x
+// took 99 / 373 us at M = 512 / 2048 against 56 / 155 us here.)
 //
 // fp32 x (F32, p.xf): two product rows per x row, the f16 pieces hi =
 // f16(x') and lo = f16(x' - hi) of x' = x 2^(15 - er) (to 2^-22 of the
@@ -1458,7 +1458,7 @@ hipError_t launch_prefill(const tbh_weight &w, const uint16_t *x, int64_t ldx, i
     // split-K scratch); up to 64 rows, or when that scratch is not to be had,
     // gemm_bf16 with every x row as three bf16 pieces of fl(x * s) and a zero
     // row.  2048x5632, us per call, pieces / weight side: M = 64 24.1 / 26.6
-    // (the extra pass), 128 40.2 / 27.4, 512 131.6 / 56.3, 2048 516 / 155.
+    // (the extra pass), 128 40.2 / 26.0, 512 131.6 / 53.2, 2048 516 / 157.
     const bool ng = w.path == Path::Int4NGroup;
     const bool wside = ng && w.ng_sexp != nullptr;
     for (int64_t m0 = 0; m0 < M; m0 += kGemmRowsPerLaunch) {
