@@ -65,6 +65,9 @@ for _m in (64, 128, 512, 2048):
     PREFILL[f"prefill_int4_m{_m}"] = ("int4", 32, (2048, 5632), _m)
     # the INT4 shape in the runtime layout Tensor.quantize(.int4) writes
     PREFILL[f"prefill_int4kn_m{_m}"] = ("int4kn", 32, (2048, 5632), _m)
+# The same products through the fp32 entry (tbh_matmul_device), the
+# reference's own activation type: x [M x K] fp32 N(0,1).
+PREFILL_F32 = {"prefill_f32_" + k[len("prefill_"):]: v for k, v in PREFILL.items()}
 # Decode (BASELINE configs[2] and [4]): one token of a LLaMA-shaped model on
 # the GPU decode step.  name: (precision, group, config kwargs, context)
 CFG_7B = dict(num_layers=32, hidden=4096, num_heads=32, num_kv_heads=32, intermediate=11008, vocab=32000)
@@ -325,21 +328,23 @@ def cpu_best_effort(qts, oq, shapes, xs, M: int, threads: int, budget_s: float):
     }
 
 
-def prefill_bytes(prec: str, gs: int, N: int, K: int, M: int) -> int:
-    """W + S + 2*M*K (bf16 x) + 4*M*N (fp32 y)."""
-    return alg_bytes(prec, gs, N, K, 0) + 2 * M * K + 4 * M * N
+def prefill_bytes(prec: str, gs: int, N: int, K: int, M: int, x_bytes: int = 2) -> int:
+    """W + S + x_bytes*M*K (bf16 x, or 4 for fp32 x) + 4*M*N (fp32 y)."""
+    return alg_bytes(prec, gs, N, K, 0) + x_bytes * M * K + 4 * M * N
 
 
-def cpu_baseline_prefill(qt, N, K, M, budget_s: float = 15.0):
+def cpu_baseline_prefill(qt, N, K, M, budget_s: float = 15.0, bf16_x: bool = True):
     """Reference CPU path on the same product: dequantize() single-threaded,
-    then sgemm of the (bf16-valued) fp32 activations on all host cores."""
+    then sgemm of the fp32 activations (bf16-valued for a bf16 workload) on
+    all host cores."""
     import oracle as O
 
     threads = cpu_threads()
     oq = O.QTensor(qt.shape, qt.data, qt.scales, qt.zeroPoints, int(qt.mode), int(qt.precision),
                    qt.groupSize)
     x = np.random.default_rng(1).normal(size=(M, K)).astype(np.float32)
-    x = (x.view(np.uint32) & 0xFFFF0000).view(np.float32)   # bf16-valued
+    if bf16_x:
+        x = (x.view(np.uint32) & 0xFFFF0000).view(np.float32)
     steps, t_deq, t_gemm = 0, 0.0, 0.0
     t0 = time.perf_counter()
     while True:
@@ -363,10 +368,13 @@ def cpu_baseline_prefill(qt, N, K, M, budget_s: float = 15.0):
 
 
 def measure_prefill(args, backend, T, torch, workload, cpu_budget):
-    """Prefill TFLOP/s of one PREFILL workload: graphs of back-to-back
-    tbh_matmul_bf16_device calls over a >= 2 GiB weight pool.  Returns the
-    result object (the bench line's fields)."""
-    prec, gs, (N, K), M = PREFILL[workload]
+    """Prefill TFLOP/s of one PREFILL workload (graphs of back-to-back
+    tbh_matmul_bf16_device calls over a >= 2 GiB weight pool) or PREFILL_F32
+    workload (tbh_matmul_device with fp32 x).  Returns the result object (the
+    bench line's fields)."""
+    f32 = workload in PREFILL_F32
+    prec, gs, (N, K), M = (PREFILL_F32 if f32 else PREFILL)[workload]
+    matmul = backend.matmul_device if f32 else backend.matmul_bf16_device
     dev = torch.device("cuda", 0)
     t_setup = time.perf_counter()
     base = make_weight(prec, gs, N, K, seed=0x7B1A0030)
@@ -374,7 +382,9 @@ def measure_prefill(args, backend, T, torch, workload, cpu_budget):
     pool = [T.DeviceWeight(backend, base) for _ in range(n_sets)]
     setup_s = time.perf_counter() - t_setup
     gen = torch.Generator(device=dev).manual_seed(3)
-    x = torch.randn((M, K), generator=gen, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    x = torch.randn((M, K), generator=gen, device=dev, dtype=torch.float32)
+    if not f32:
+        x = x.to(torch.bfloat16)
     y = torch.empty((M, N), device=dev, dtype=torch.float32)
     cap = torch.cuda.Stream(dev)
     cap.wait_stream(torch.cuda.current_stream(dev))
@@ -384,17 +394,17 @@ def measure_prefill(args, backend, T, torch, workload, cpu_budget):
         for _ in range(5):
             dst.copy_(src)
         for i in range(20):
-            backend.matmul_bf16_device(x, pool[i % n_sets], out=y, stream=cap)
+            matmul(x, pool[i % n_sets], out=y, stream=cap)
         torch.cuda.synchronize()
         return {"pmc_pass": True, "copy_bytes": src.numel() * 4, "workload": workload,
-                "alg_bytes_per_launch": prefill_bytes(prec, gs, N, K, M)}
+                "alg_bytes_per_launch": prefill_bytes(prec, gs, N, K, M, 4 if f32 else 2)}
     for i in range(n_sets):
-        backend.matmul_bf16_device(x, pool[i], out=y, stream=cap)
+        matmul(x, pool[i], out=y, stream=cap)
     torch.cuda.synchronize()
     eager = y.clone()
 
     def step(i):
-        backend.matmul_bf16_device(x, pool[i % n_sets], out=y, stream=cap)
+        matmul(x, pool[i % n_sets], out=y, stream=cap)
 
     check = step_graphs(torch, cap, step, n_sets, n_sets)[0]
     for _ in range(2):
@@ -422,7 +432,7 @@ def measure_prefill(args, backend, T, torch, workload, cpu_budget):
     steps_done = args.steps
     kern_us = e0.elapsed_time(e1) * 1e3 / steps_done
     flops = 2.0 * M * N * K
-    byts = prefill_bytes(prec, gs, N, K, M)
+    byts = prefill_bytes(prec, gs, N, K, M, 4 if f32 else 2)
     value = flops * steps_done / wall / 1e12
     mfma_bound = flops / byts >= RIDGE_FLOP_PER_BYTE
     if mfma_bound:
@@ -432,15 +442,18 @@ def measure_prefill(args, backend, T, torch, workload, cpu_budget):
         roof = {"bound": "hbm", "achieved": round(byts / kern_us / 1e3, 1),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s"}
     roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
-    # runtime-layout INT4 past 64 rows (TBH_PREFILL_F16_MIN) runs the
-    # weight-side kernel on the f16 MFMA
-    ngw = prec == "int4kn" and M >= int(os.environ.get("TBH_PREFILL_F16_MIN") or 65)
-    roof.update({"traffic": profiled_traffic(prec, N, K, M, "prefill"),
-                 "kernel": f"{'gemm_ngw' if ngw else 'gemm_bf16'} {N}x{K} M={M} ({pool[0].path})",
+    # past 64 rows (TBH_PREFILL_F16_MIN) the f16 forms: runtime-layout INT4
+    # on the weight-side kernel, fp32 x as two f16 pieces
+    f16 = M >= int(os.environ.get("TBH_PREFILL_F16_MIN") or 65) and (
+        prec == "int4kn" or (f32 and os.environ.get("TBH_PREFILL_F32_PIECES") != "4"))
+    kern = "gemm_ngw" if prec == "int4kn" and f16 else "gemm_bf16"
+    x_form = ("fp32 x, two f16 pieces" if f16 else "fp32 x, three bf16 pieces") if f32 else "bf16 x"
+    roof.update({"traffic": profiled_traffic(prec, N, K, M, "prefill_f32" if f32 else "prefill"),
+                 "kernel": f"{kern} {N}x{K} M={M} ({pool[0].path}, {x_form})",
                  "kernel_us": round(kern_us, 3), "alg_bytes_per_launch": byts,
                  "flops_per_launch": int(flops), "frac_basis": FRAC_BASIS_CALL})
     out = {
-        "metric": f"prefill dequant-GEMM TFLOP/s on {'f16' if ngw else 'bf16'} MFMA ({ {'int4kn': 'INT4 runtime layout'}.get(prec, prec.upper()) }, M={M})",
+        "metric": f"prefill dequant-GEMM TFLOP/s on {'f16' if f16 else 'bf16'} MFMA ({ {'int4kn': 'INT4 runtime layout'}.get(prec, prec.upper()) }, M={M}{', fp32 x' if f32 else ''})",
         "value": round(value, 2),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -450,7 +463,7 @@ def measure_prefill(args, backend, T, torch, workload, cpu_budget):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16" if ngw else "bf16",
+        "dtype": "f16" if f16 else "bf16",
         "data": "synthetic",
         "config": {
             "workload": workload,
@@ -458,14 +471,14 @@ def measure_prefill(args, backend, T, torch, workload, cpu_budget):
                         "int4kn": "INT4 symmetric, group 32 along N (runtime layout, Tensor.quantize(.int4))",
                         "int8": "INT8 symmetric per output channel"}[prec],
             "shape_NxK": f"{N}x{K}", "M": M,
-            "x": "bf16 (rounded from fp32 N(0,1)), W fp32 N(0,0.02) quantized",
+            "x": ("fp32 N(0,1)" if f32 else "bf16 (rounded from fp32 N(0,1))") + ", W fp32 N(0,0.02) quantized",
             "pool_sets": n_sets,
         },
         "roofline": roof,
         "setup_s": round(setup_s, 1),
     }
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline_prefill(base, N, K, M, cpu_budget)
+        out["cpu_baseline"] = cpu_baseline_prefill(base, N, K, M, cpu_budget, bf16_x=not f32)
     return out
 
 
@@ -955,7 +968,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="int4_g32_gemv_m1",
-                    choices=sorted(WORKLOADS) + sorted(PREFILL) + sorted(DECODE) + sorted(PROJ) + sorted(PROJ_SEP) +
+                    choices=sorted(WORKLOADS) + sorted(PREFILL) + sorted(PREFILL_F32) + sorted(DECODE) + sorted(PROJ) +
+                    sorted(PROJ_SEP) +
                     sorted(OPS))
     ap.add_argument("--pool-gib", type=float, default=2.2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -994,7 +1008,7 @@ def main():
 
     torch.cuda.set_device(0)
     backend = T.HIPBackend(0)
-    if args.workload in PREFILL:
+    if args.workload in PREFILL or args.workload in PREFILL_F32:
         return run_prefill(args, backend, T, torch)
     if args.workload in DECODE:
         return run_decode(args, backend, T, torch)

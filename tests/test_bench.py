@@ -28,6 +28,16 @@ def test_table_rows_are_workloads():
     assert len(set(bench.TABLE)) == len(bench.TABLE)
 
 
+def test_fp32_prefill_workloads_mirror_the_bf16_ones():
+    # every bf16 prefill workload has an fp32-entry twin of the same product,
+    # whose algorithmic bytes count 4-byte x
+    assert {k.replace("prefill_f32_", "prefill_") for k in bench.PREFILL_F32} == set(bench.PREFILL)
+    for name, (prec, gs, (N, K), M) in bench.PREFILL_F32.items():
+        assert bench.PREFILL[name.replace("prefill_f32_", "prefill_")] == (prec, gs, (N, K), M)
+        assert bench.prefill_bytes(prec, gs, N, K, M, 4) - bench.prefill_bytes(prec, gs, N, K, M) == 2 * M * K
+    assert bench.profiled_traffic("int8", 5632, 2048, 512, "prefill_f32") is None   # no counter record
+
+
 @pytest.mark.parametrize("prec,N,K,M,kind", [
     ("int4", 32000, 2048, 1, ""),            # the headline's dominant launch
     ("int8", 5632, 2048, 1, ""),             # configs[0]
