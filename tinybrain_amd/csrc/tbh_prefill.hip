@@ -756,9 +756,8 @@ void gemm_ngw(const PParams p) {
                 uint32_t o[4];
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    const uint32_t wv = xr[d][j][0][q];   // bf16 elements 2q (low half), 2q + 1
-                    const float a = xin[d][j] ? as_f32(wv << 16) : 0.0f;
-                    const float b = xin[d][j] ? as_f32(wv & 0xFFFF0000u) : 0.0f;
+                    const uint32_t wv = xin[d][j] ? xr[d][j][0][q] : 0u;   // bf16 elements 2q (low half), 2q + 1
+                    const float a = as_f32(wv << 16), b = as_f32(wv & 0xFFFF0000u);
                     o[q] = pack_f16(__builtin_ldexpf(a, xsh[j]), __builtin_ldexpf(b, xsh[j]));
                 }
                 *(u32x4 *)&xs[bb][row * kLdsRow + 8 * kq] = u32x4{o[0], o[1], o[2], o[3]};
