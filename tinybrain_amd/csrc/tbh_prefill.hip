@@ -641,7 +641,9 @@ void gemm_bf16(const PParams p) {
 // (r = w' - hi, exact; NaN for a non-finite w', which hi holds): r, but at
 // least 2^-24 in magnitude and with w's sign unless w' = 0, so that an
 // infinite x meets two pieces of one sign (inf * w' as one product: +-inf,
-// or NaN for w' = 0) and never inf * 0 = NaN from an empty low piece.
+// or NaN for w' = 0) and never inf * 0 = NaN from an empty low piece.  (A
+// |w'| below 2^-24, a scale 2^39 or more under its N-block's largest, has
+// hi = 0, so an infinite x gives NaN there; finite x loses at most 2^-24.)
 __device__ __forceinline__ float lo_piece(float w, float r) {
     return w == 0.0f ? 0.0f : __builtin_copysignf(__builtin_fmaxf(__builtin_fabsf(r), 0x1p-24f), w);
 }
