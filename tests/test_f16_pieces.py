@@ -10,8 +10,9 @@ values on the CPU.
   remainder at least 2^-24 in magnitude with w's sign unless w = 0:
   |w - (hi + lo)| <= max(2^-21 |w|, 2^-24), lo has w's sign, and lo = 0
   only for w = 0.  So an infinite x times the two pieces gives inf * w
-  (+-inf, or NaN for w = 0) for every |w| >= 2^-24; below that (a scale
-  2^39 or more under its N-block's largest) hi is 0 and the product is NaN.
+  (+-inf, or NaN for w = 0) for every |w| >= 2^-24.  Below that hi would be
+  0, which is why the kernel floors a scaled scale at 2^-28 for weights
+  whose scales span that far (|16 q| >= 16 makes |w| >= 2^-24 for q != 0).
 """
 import numpy as np
 import pytest
@@ -93,12 +94,20 @@ def test_infinite_x_meets_weight_pieces_like_the_product():
             np.testing.assert_array_equal(got[ok], want[ok])
 
 
-def test_weights_below_the_f16_range_have_an_empty_high_piece():
-    # the documented limit: |w| < 2^-24 rounds toward zero to hi = 0, so an
-    # infinite x meets it as inf * 0 (finite x loses at most 2^-24 there)
+def test_floored_scales_keep_the_high_piece():
+    # |w| < 2^-24 rounds toward zero to hi = 0 (inf * 0 = NaN for an infinite
+    # x); with the scale floored at 2^-28, every q != 0 gives |16 q s| >=
+    # 2^-24, a nonzero high piece of w's sign, and q = 0 still gives 0
     w = np.array([2.0 ** -25, -(2.0 ** -30), 2.0 ** -40], np.float32)
     hi, lo = _w_pieces(w)
     assert np.all(hi.astype(np.float32) == 0)
-    assert np.all(np.sign(lo.astype(np.float32)) == np.sign(w))
     with np.errstate(invalid="ignore"):
         assert np.all(np.isnan(np.inf * hi.astype(np.float64) + np.inf * lo.astype(np.float64)))
+    s = np.array([2.0 ** -50, -(2.0 ** -40), 2.0 ** -29, 0.0], np.float32)
+    s_floor = np.where(s == 0, s, np.copysign(np.maximum(np.abs(s), np.float32(2.0 ** -28)), s)).astype(np.float32)
+    for q16 in range(-128, 128, 16):
+        w = (np.float32(q16) * s_floor).astype(np.float32)
+        hi, lo = _w_pieces(w)
+        nz = w != 0
+        assert np.all(nz == ((q16 != 0) & (s != 0)))
+        assert np.all(hi[nz] != 0) and np.all(np.sign(hi[nz].astype(np.float32)) == np.sign(w[nz]))

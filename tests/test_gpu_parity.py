@@ -1158,6 +1158,42 @@ def test_prefill_bf16_runtime_layout_nonfinite(backend, M):
     assert err["gated"] <= GATE, (M, err)
 
 
+@pytest.mark.parametrize("entry", ["bf16", "fp32"])
+def test_prefill_runtime_layout_wide_scales_nonfinite(backend, entry):
+    # an N-block whose scales span 2^60 (one k row of tiny weights): the
+    # weight-side kernel's variant that floors tiny scales keeps every
+    # nonzero weight's high f16 piece nonzero, so infinite x meets it as
+    # inf * w (+-inf), as the float64 product does; finite rows stay within
+    # the gate
+    import torch
+
+    K, N, gs, M = 512, 256, 32, 80
+    src = O.fill_normal(0xA1, K * N, std=0.02).reshape(K, N)
+    src[7, :] *= np.float32(1e-18)
+    qk = O.quantize_int4(src, gs)
+    pq = _product(qk, (K, N))
+    W = _oracle_weight(qk, pq.layout)
+    x = O.fill_normal(0xA2, M * K).reshape(M, K)
+    x[0, 7] = np.inf                      # meets the tiny weights of k = 7
+    x[1, 7], x[1, 8] = -np.inf, 1e30
+    xin = torch.from_numpy(x)
+    if entry == "bf16":
+        xin = xin.to(torch.bfloat16)
+        y = backend.matmul_bf16_device(xin.cuda(), backend.weight(pq))
+        torch.cuda.synchronize()
+        y = y.cpu().numpy()
+    else:
+        y = backend.matmulQuantized(x, pq)
+    with np.errstate(invalid="ignore", over="ignore"):
+        y64 = O.gemm_f64(xin.float().numpy(), W)
+    for m in (0, 1):
+        np.testing.assert_array_equal(np.isnan(y[m]), np.isnan(y64[m]), err_msg=str(m))
+        np.testing.assert_array_equal(np.isposinf(y[m]), np.isposinf(y64[m]), err_msg=str(m))
+        np.testing.assert_array_equal(np.isneginf(y[m]), np.isneginf(y64[m]), err_msg=str(m))
+    err = O.parity_errors(y[2:], y64[2:])
+    assert err["gated"] <= GATE, (entry, err)
+
+
 @pytest.mark.parametrize("kind,K,N,M", [
     ("int8", 2048, 1024, 64),      # split along K
     ("int8", 2048, 5632, 512),     # one block per tile, no split

@@ -593,6 +593,11 @@ tbh_status tbh_weight_create(tbh_device *dev, const tbh_qtensor_desc *desc, tbh_
                     int e2 = 0;
                     if (mx > 0.0f) (void)std::frexp(mx, &e2);
                     ex[(size_t)nb] = e2;
+                    const float lo_ok = std::ldexp(1.0f, e2 - 36);
+                    for (int64_t k = 0; k < K && !w->ng_wide; ++k) {
+                        const float a = std::fabs(t[nb * w->Kp + k]);
+                        w->ng_wide = a > 0.0f && a < lo_ok;
+                    }
                 }
                 if (e == hipSuccess) e = upload(&w->ng_sexp, ex.data(), ex.size(), w->device_bytes, w->n_ng_sexp);
                 w->stream_bytes = (count + 1) / 2 + 4 * d.n_scales;

@@ -112,6 +112,10 @@ struct tbh_weight {
     // scales (0 when all are zero), for the prefill GEMM's f16 scaling
     int32_t *ng_sexp = nullptr;
     int64_t n_ng_sexp = 0;
+    // some N-block holds a nonzero finite scale below 2^(e - 36), so that a
+    // weight 16 q s 2^(8 - e) can fall under the f16 range: the prefill GEMM
+    // takes a variant that floors such scales (gemm_ngw with FLOOR)
+    bool ng_wide = false;
     bool mfma_tiles = false;     // data in 1 KiB MFMA tiles (else K-contiguous rows)
 
     // generic path: the reference arrays as given

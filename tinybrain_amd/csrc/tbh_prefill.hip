@@ -641,9 +641,11 @@ void gemm_bf16(const PParams p) {
 // (r = w' - hi, exact; NaN for a non-finite w', which hi holds): r, but at
 // least 2^-24 in magnitude and with w's sign unless w' = 0, so that an
 // infinite x meets two pieces of one sign (inf * w' as one product: +-inf,
-// or NaN for w' = 0) and never inf * 0 = NaN from an empty low piece.  (A
-// |w'| below 2^-24, a scale 2^39 or more under its N-block's largest, has
-// hi = 0, so an infinite x gives NaN there; finite x loses at most 2^-24.)
+// or NaN for w' = 0) and never inf * 0 = NaN from an empty low piece.  A
+// nonzero |w'| below 2^-24 would also empty the high piece; the FLOOR
+// variant of gemm_ngw keeps every nonzero scale at 2^-28 or more after
+// scaling, so that |w'| >= 16 * 2^-28 for q != 0 (at most 2^-21 added on
+// a 2^15 scale), for weights whose scales span that far (tbh_weight.ng_wide).
 __device__ __forceinline__ float lo_piece(float w, float r) {
     return w == 0.0f ? 0.0f : __builtin_copysignf(__builtin_fmaxf(__builtin_fabsf(r), 0x1p-24f), w);
 }
@@ -670,7 +672,7 @@ __device__ __forceinline__ float lo_piece(float w, float r) {
 // Tiles BM product rows by BN outputs, WV waves as 2 x (WV / 2), K steps of
 // 64 in two LDS buffers with a two-step register ring (the gemm_bf16 loop);
 // K split z of p.split_steps steps writes p.y + z * p.split_stride.
-template <int BM, int BN, int WV, bool F32>
+template <int BM, int BN, int WV, bool F32, bool FLOOR>
 __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(WV == 8 ? 4 : 1)))
 void gemm_ngw(const PParams p) {
     constexpr int BK = 64, kLdsRow = BK + kRowPad;
@@ -780,8 +782,14 @@ void gemm_ngw(const PParams p) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 // 16 q * (s 2^(8 - eb)) = fl(q s) 2^(12 - eb), exactly
-                const float a = q16[2 * q] * __builtin_ldexpf(as_f32(sr[d][j][q / 2][(2 * q) % 4]), wsh[j]);
-                const float b = q16[2 * q + 1] * __builtin_ldexpf(as_f32(sr[d][j][q / 2][(2 * q + 1) % 4]), wsh[j]);
+                float sa = __builtin_ldexpf(as_f32(sr[d][j][q / 2][(2 * q) % 4]), wsh[j]);
+                float sb = __builtin_ldexpf(as_f32(sr[d][j][q / 2][(2 * q + 1) % 4]), wsh[j]);
+                if constexpr (FLOOR) {
+                    sa = sa == 0.0f ? sa : __builtin_copysignf(__builtin_fmaxf(__builtin_fabsf(sa), 0x1p-28f), sa);
+                    sb = sb == 0.0f ? sb : __builtin_copysignf(__builtin_fmaxf(__builtin_fabsf(sb), 0x1p-28f), sb);
+                }
+                const float a = q16[2 * q] * sa;
+                const float b = q16[2 * q + 1] * sb;
                 const f16x2 h = __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(a, b));   // toward zero
                 const f32x2 hb = __builtin_convertvector(h, f32x2);
                 ph[q] = __builtin_bit_cast(uint32_t, h);
@@ -1209,12 +1217,20 @@ hipError_t launch_ngw(const tbh_weight &w, PParams p, hipStream_t s, const Scrat
         p.split_stride = n;
     }
     const dim3 grid((unsigned)((p.Np + 63) / 64), (unsigned)((p.M + bm - 1) / bm), (unsigned)splits);
-    if (p.xf) {
-        if (big) hipLaunchKernelGGL((gemm_ngw<128, 64, 8, true>), grid, dim3(512), 0, s, p);
-        else hipLaunchKernelGGL((gemm_ngw<64, 64, 4, true>), grid, dim3(256), 0, s, p);
+    if (w.ng_wide) {
+        if (p.xf) {
+            if (big) hipLaunchKernelGGL((gemm_ngw<128, 64, 8, true, true>), grid, dim3(512), 0, s, p);
+            else hipLaunchKernelGGL((gemm_ngw<64, 64, 4, true, true>), grid, dim3(256), 0, s, p);
+        } else {
+            if (big) hipLaunchKernelGGL((gemm_ngw<128, 64, 8, false, true>), grid, dim3(512), 0, s, p);
+            else hipLaunchKernelGGL((gemm_ngw<64, 64, 4, false, true>), grid, dim3(256), 0, s, p);
+        }
+    } else if (p.xf) {
+        if (big) hipLaunchKernelGGL((gemm_ngw<128, 64, 8, true, false>), grid, dim3(512), 0, s, p);
+        else hipLaunchKernelGGL((gemm_ngw<64, 64, 4, true, false>), grid, dim3(256), 0, s, p);
     } else {
-        if (big) hipLaunchKernelGGL((gemm_ngw<128, 64, 8, false>), grid, dim3(512), 0, s, p);
-        else hipLaunchKernelGGL((gemm_ngw<64, 64, 4, false>), grid, dim3(256), 0, s, p);
+        if (big) hipLaunchKernelGGL((gemm_ngw<128, 64, 8, false, false>), grid, dim3(512), 0, s, p);
+        else hipLaunchKernelGGL((gemm_ngw<64, 64, 4, false, false>), grid, dim3(256), 0, s, p);
     }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess || splits == 1) return e;
