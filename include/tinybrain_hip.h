@@ -224,8 +224,9 @@ tbh_status tbh_matmul(tbh_device *dev, const float *x, int64_t M, int64_t K,
 
 /* Same product on device pointers, enqueued on `stream` (a hipStream_t of the
  * weight's device; NULL = the null stream).  Returns after the launch.
- * Launches that split K (matrix-core GEMV, MFMA GEMM) keep their partial sums
- * in a workspace the library allocates per (device, stream) on first use and
+ * Launches that split K (matrix-core GEMV, MFMA GEMM) keep their partial sums,
+ * and the MFMA GEMM past 64 rows its per-row exponents of x (an int32 per
+ * row), in a workspace the library allocates per (device, stream) on first use and
  * keeps, with every buffer it outgrew, until tbh_device_close (a graph
  * captured on the stream may still hold them): a caller that creates many
  * short-lived streams should reuse a few, or call
@@ -241,6 +242,7 @@ tbh_status tbh_matmul_device(const tbh_weight *w, const float *x, int64_t M,
  * allocate device memory: code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc.  Same product, same kernels, same
  * arguments; the split-K partial sums (matrix-core small-M GEMV, MFMA GEMM)
+ * and the GEMM's per-row exponents of x
  * go to a fixed 16 MiB scratch array per GPU (held until the process ends)
  * instead of a per-stream workspace, and the call makes no allocation.  A
  * call one of whose launches would need more than the scratch holds (16 MiB,
