@@ -1159,6 +1159,63 @@ def test_prefill_bf16_runtime_layout_nonfinite(backend, M):
 
 
 @pytest.mark.parametrize("entry", ["bf16", "fp32"])
+def test_prefill_runtime_layout_graphs(backend, entry):
+    # runtime-layout INT4 past 64 rows (exponent pass, weight-side kernel,
+    # K split): calls bit-identical to each other; a graph captured on a
+    # stream without a workspace takes the three-piece form, one captured
+    # after an eager call the f16 form, and its replays, with eager calls on
+    # another stream between them, equal the eager call bit for bit
+    import torch
+
+    K, N, gs, M = 2048, 1024, 32, 96
+    qk = _int4_kn(0xB1, K, N, gs)
+    pq = _product(qk, (K, N))
+    w = backend.weight(pq)
+    xh = O.fill_normal(0xB2, M * K).reshape(M, K)
+    if entry == "bf16":
+        xt = torch.from_numpy(xh).to(torch.bfloat16)
+        run = backend.matmul_bf16_device
+    else:
+        xt = torch.from_numpy(xh)
+        run = backend.matmul_device
+    ref = O.gemm_f64(xt.float().numpy(), _oracle_weight(qk, pq.layout))
+    x = xt.cuda()
+    a = run(x, w)
+    b = run(x, w)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(a.cpu().numpy(), b.cpu().numpy())
+    assert O.parity_errors(a.cpu().numpy(), ref)["gated"] <= GATE
+    s = torch.cuda.Stream()
+    y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    for phase in range(2):
+        if phase == 1:
+            with torch.cuda.stream(s):
+                run(x, w, out=y)
+            torch.cuda.synchronize()
+            eager = y.cpu().numpy().copy()
+            np.testing.assert_array_equal(eager, a.cpu().numpy())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            run(x, w, out=y)
+        first = None
+        for _ in range(3):
+            y.zero_()
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            got = y.cpu().numpy()
+            assert O.parity_errors(got, ref)["gated"] <= GATE, phase
+            if first is None:
+                first = got.copy()
+            np.testing.assert_array_equal(got, first)
+            run(x, w)                          # eager work between the replays
+            torch.cuda.synchronize()
+        if phase == 1:
+            np.testing.assert_array_equal(first, eager)
+        del g
+
+
+@pytest.mark.parametrize("entry", ["bf16", "fp32"])
 def test_prefill_runtime_layout_wide_scales_nonfinite(backend, entry):
     # an N-block whose scales span 2^60 (one k row of tiny weights): the
     # weight-side kernel's variant that floors tiny scales keeps every
