@@ -2,8 +2,9 @@
 
 The no-allocation entry point runs the same kernels as tbh_matmul_device;
 only the split-K partial sums (of the matrix-core small-M GEMV and of the
-fp32 MFMA GEMM route for more rows) go to a fixed per-GPU scratch array
-instead of a per-stream workspace.  So every result is
+fp32 MFMA GEMM route for more rows) and, past 64 rows, the GEMM's per-row
+exponents of x go to a fixed per-GPU scratch array instead of a per-stream
+workspace.  So every result is
 bit-identical to tbh_matmul_device's on the same input, and within the matmul
 gate (floored max relative error <= 1e-3) of the float64 product of the
 bit-exact dequantized weights.
@@ -44,6 +45,14 @@ def _int8_pc(seed, K, N):
     return pq, O.dequantize(qt)
 
 
+def _int4_kn(seed, K, N, gs=32):
+    # the runtime layout Tensor.quantize(.int4) writes: groups along N
+    qt = O.quantize_int4(O.fill_normal(seed, K * N, std=0.02).reshape(K, N), gs)
+    pq = T.QuantizedTensor((K, N), qt.data, qt.scales, qt.mode, qt.precision, gs, qt.zero_points,
+                           T.Layout.KN_FLAT)
+    return pq, O.dequantize(qt)
+
+
 def _noalloc(w, x, y, stream):
     """tbh_matmul_device_noalloc through ctypes; returns the status."""
     L = _abi.lib()
@@ -60,9 +69,12 @@ def test_noalloc_matches_device_entry_point(backend):
     # with the matrix-core path forced from 2 rows (4 K splits, 48 KB of
     # scratch over what the first call left there); third: INT8 on the VALU
     # GEMV (no scratch); fourth: 16 rows on [5632 -> 2048], the fp32 MFMA
-    # GEMM route with K split over the CUs (2 MB of scratch)
+    # GEMM route with K split over the CUs (2 MB of scratch); fifth: 96 rows
+    # there, x as two f16 pieces (the row exponents ahead of the partials);
+    # sixth: 80 rows of a runtime-layout weight on the weight-side kernel
     cases = [(_int4_nk(901, 4096, 11008), 8, 0), (_int4_nk(902, 2048, 1024), 3, 2),
-             (_int8_pc(903, 2048, 512), 1, 0), (_int4_nk(905, 5632, 2048), 16, 0)]
+             (_int8_pc(903, 2048, 512), 1, 0), (_int4_nk(905, 5632, 2048), 16, 0),
+             (_int4_nk(906, 5632, 2048), 96, 0), (_int4_kn(907, 2048, 1024), 80, 0)]
     try:
         for (pq, W), M, min_rows in cases:
             backend.set_option(_abi.OPT_SGEMV_MIN_ROWS, min_rows)
