@@ -1406,8 +1406,8 @@ static PParams prefill_params(const tbh_weight &w, int64_t ldx, float *y, int64_
 }
 
 // Rows of x per GEMM launch.  The grid's second dimension counts row tiles,
-// and the fp32 and runtime-layout forms run four product rows per x row in
-// 32-bit row indices; longer x is taken in chunks of this many rows, one
+// and the fp32 and runtime-layout forms run up to four product rows per x
+// row in 32-bit row indices; longer x is taken in chunks of this many rows, one
 // launch (and split sum) after the other on the caller's stream.
 constexpr int64_t kGemmRowsPerLaunch = (int64_t)1 << 18;
 
